@@ -1,0 +1,230 @@
+"""MoE-layer benchmark on one MI355X (BASELINE.json metric: MoE-layer tokens/s at
+decode b=1 and prefill 512; % of HBM / MFMA roofline).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--copies C] [--no-cpu]
+
+A step is one forward of the MoE layer over one batch of synthetic input that
+is already resident in HBM:
+
+* value (the headline line): configs[1], the Qwen3-30B-A3B-shaped Q4_K layer
+  at prefill 512 tokens with Zipf-biased routing. K steps are captured in one
+  HIP graph that cycles over C resident copies of the layer's weights (so the
+  256 MB Infinity Cache cannot serve repeated weight reads) and timed between
+  HIP events; value = 512 * K / elapsed.
+* decode: configs[0] (same layer shape, decode batch 1) the same way over 32
+  copies, reported in the "decode" object.
+* roofline: the dominant kernel of the prefill step (the stage with the
+  largest time), timed live by graph-captured replays with HIP events on the
+  stream it runs on; achieved = its algorithmic FLOPs (or bytes) / duration.
+* cpu_baseline: the C++ CPU restatement of the layer (oracle/liboracle.so,
+  fp32 accumulation, one thread per available core) timed on a bounded sample
+  of the same workload. The reference (Rust + Metal) cannot run on Linux.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def prefill_stage_work(spec, ids, T):
+    """Algorithmic FLOPs / bytes of each prefill stage (intermediates excluded from bytes)."""
+    H, F, K, E = spec.hidden, spec.ffn, spec.top_k, spec.experts
+    P = T * K
+    touched = np.unique(ids).size
+    bpe = spec.weight_bytes_per_expert()
+    gu_bytes = touched * (spec.gate.rows * spec.gate.stride + spec.up.rows * spec.up.stride)
+    dn_bytes = touched * spec.down.rows * spec.down.stride
+    return {
+        "router": {"flops": 2.0 * T * E * H, "bytes": 4.0 * (E * H + T * H + T * E)},
+        "gate_up": {"flops": 2.0 * P * 2 * F * H, "bytes": float(gu_bytes)},
+        "down": {"flops": 2.0 * P * F * H, "bytes": float(dn_bytes)},
+        "layer": {"flops": 2.0 * P * 3 * F * H + 2.0 * T * E * H,
+                  "bytes": float(touched * bpe + 4 * E * H + 2 * 4 * T * H), "touched": int(touched)},
+    }
+
+
+def time_graph(gpu, layers, dx, T, dout, steps, warmup):
+    from ingot_amd.moe import Graph  # noqa: F401
+    for l in layers:
+        l.reserve(T)
+        l.forward(dx, T, dout)
+    gpu.synchronize()
+    gpu.check_device_flags()
+    gpu.graph_begin()
+    for i in range(warmup):
+        layers[i % len(layers)].forward(dx, T, dout)
+    gw = gpu.graph_end()
+    gpu.graph_begin()
+    for i in range(steps):
+        layers[i % len(layers)].forward(dx, T, dout)
+    g = gpu.graph_end()
+    if warmup:
+        gw.launch()
+    gpu.synchronize()
+    ms = g.time(1)
+    gw.destroy()
+    g.destroy()
+    return ms
+
+
+def cpu_baseline(spec, x, budget_s, label):
+    from oracle import pyoracle as O
+    cores = len(os.sched_getaffinity(0))
+    st, _, _, _ = O.moe_forward(spec, x, O.F32, threads=cores)  # warm-up
+    assert st == 0
+    n, t0 = 0, time.perf_counter()
+    while True:
+        st, _, _, _ = O.moe_forward(spec, x, O.F32, threads=cores)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    T = x.shape[0]
+    return {"value": T * n / el, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{label}: {n} forward(s) of {T} token(s), fp32 accumulation, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=8, help="resident weight copies for the prefill step")
+    ap.add_argument("--decode-copies", type=int, default=32)
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from ingot_amd import configs as CF
+    from ingot_amd.moe import (STAGE_DISPATCH, STAGE_DOWN, STAGE_GATEUP, STAGE_ROUTE, STAGE_ROUTER, STAGE_COMBINE,
+                               Gpu, MoeLayer, time_stage)
+
+    gpu = Gpu(0)
+    log(f"device: {gpu.name()}")
+
+    # ---------------- prefill 512 ----------------
+    t0 = time.time()
+    spec1 = CF.c1_layer()
+    x1 = CF.inputs(1, 512, 2048)
+    log(f"C1 layer synthesized in {time.time() - t0:.1f} s")
+    base = MoeLayer(gpu, spec1)
+    layers = [base] + [base.clone() for _ in range(args.copies - 1)]
+    T = 512
+    dx = gpu.to_device(x1)
+    dout = gpu.buffer(4 * T * 2048)
+    dids = gpu.buffer(4 * T * 8)
+    base.forward(dx, T, dout, dids)
+    gpu.synchronize()
+    ids = dids.download(np.uint32, T * 8)
+    ms = time_graph(gpu, layers, dx, T, dout, args.steps, args.warmup)
+    ms_step = ms / args.steps
+    log(f"prefill: {ms_step * 1e3:.1f} us/step over {args.steps} steps, {args.copies} copies")
+    work = prefill_stage_work(spec1, ids, T)
+    stages = {}
+    for name, st in (("router", STAGE_ROUTER), ("route", STAGE_ROUTE), ("dispatch", STAGE_DISPATCH),
+                     ("gate_up", STAGE_GATEUP), ("down", STAGE_DOWN), ("combine", STAGE_COMBINE)):
+        for l in layers:
+            l.forward(dx, T, dout)
+        stages[name] = {"us": 1e3 * time_stage(layers, st, 40), "kernel": base.stage_kernel(st)}
+    gpu.synchronize()
+    log("prefill stages (us): " + ", ".join(f"{k} {v['us']:.1f}" for k, v in stages.items()))
+    dom = max(("gate_up", "down"), key=lambda k: stages[k]["us"])
+    dflops = work[dom]["flops"]
+    achieved = dflops / (stages[dom]["us"] * 1e-6) / 1e12
+    layer_tflops = work["layer"]["flops"] / (ms_step * 1e-3) / 1e12
+
+    # ---------------- decode b=1 ----------------
+    spec0 = CF.c0_layer()
+    x0 = CF.inputs(0, 1, 2048)
+    d0 = MoeLayer(gpu, spec0)
+    dl = [d0] + [d0.clone() for _ in range(args.decode_copies - 1)]
+    dx0 = gpu.to_device(x0)
+    dout0 = gpu.buffer(4 * 2048)
+    dms = time_graph(gpu, dl, dx0, 1, dout0, args.decode_steps, args.warmup)
+    dms_step = dms / args.decode_steps
+    d_bytes = 4 * 128 * 2048 + 8 * spec0.weight_bytes_per_expert() + 2 * 4 * 2048
+    gu_bytes = 8 * (spec0.gate.rows * spec0.gate.stride + spec0.up.rows * spec0.up.stride) + 4 * 2048
+    dn_bytes = 8 * spec0.down.rows * spec0.down.stride + 8 * 4 * 768 + 4 * 2048
+    dstages = {}
+    for name, st in (("router", STAGE_ROUTER), ("route", STAGE_ROUTE), ("gate_up", STAGE_GATEUP),
+                     ("down", STAGE_DOWN)):
+        for l in dl:
+            l.forward(dx0, 1, dout0)
+        dstages[name] = {"us": 1e3 * time_stage(dl, st, 256), "kernel": d0.stage_kernel(st)}
+    gpu.synchronize()
+    log(f"decode: {dms_step * 1e3:.2f} us/step; stages (us): " +
+        ", ".join(f"{k} {v['us']:.2f}" for k, v in dstages.items()))
+    decode = {
+        "config": "configs[0]: Qwen3-30B-A3B-shaped Q4_K MoE layer, decode batch 1",
+        "tokens_per_s": 1.0 / (dms_step * 1e-3),
+        "us_per_step": dms_step * 1e3,
+        "steps": args.decode_steps,
+        "weight_copies": args.decode_copies,
+        "layer_hbm": {"bytes": d_bytes, "achieved_GBs": d_bytes / (dms_step * 1e-3) / 1e9,
+                      "frac": d_bytes / (dms_step * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "kernels": {
+            "gate_up": {"kernel": dstages["gate_up"]["kernel"], "us": dstages["gate_up"]["us"], "bytes": gu_bytes,
+                        "achieved_GBs": gu_bytes / (dstages["gate_up"]["us"] * 1e-6) / 1e9},
+            "down": {"kernel": dstages["down"]["kernel"], "us": dstages["down"]["us"], "bytes": dn_bytes,
+                     "achieved_GBs": dn_bytes / (dstages["down"]["us"] * 1e-6) / 1e9},
+            "router": {"kernel": dstages["router"]["kernel"], "us": dstages["router"]["us"]},
+            "route": {"kernel": dstages["route"]["kernel"], "us": dstages["route"]["us"]},
+        },
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(spec1, x1, args.cpu_seconds, "configs[1] prefill 512")
+        cpu_d = cpu_baseline(spec0, x0, max(2.0, args.cpu_seconds / 4), "configs[0] decode b=1")
+        decode["cpu_baseline"] = cpu_d
+        log(f"cpu baseline: prefill {cpu['value']:.0f} tok/s, decode {cpu_d['value']:.1f} tok/s on {cpu['cores']} cores")
+
+    line = {
+        "metric": "MoE-layer tokens/s at prefill 512 (configs[1]); decode b=1 in 'decode'",
+        "value": T / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: weights N(0,0.02) quantized to Q4_K, x ~ N(0,1), seeded SplitMix64",
+        "config": {"workload": "configs[1]: Qwen3-30B-A3B-shaped Q4_K MoE layer, prefill 512 tokens, Zipf router bias",
+                   "hidden": 2048, "experts": 128, "top_k": 8, "ffn": 768, "tokens": T, "format": "Q4_K",
+                   "weight_copies": args.copies, "experts_touched": work["layer"]["touched"]},
+        "roofline": {"bound": "mfma", "kernel": stages[dom]["kernel"], "achieved": achieved,
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS,
+                     "traffic": None, "kernel_us": stages[dom]["us"], "algorithmic_flops": dflops},
+        "layer_mfma_frac": layer_tflops / MFMA_F32_PEAK_TFLOPS,
+        "stages_us": {k: round(v["us"], 2) for k, v in stages.items()},
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

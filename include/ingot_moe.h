@@ -1,0 +1,205 @@
+/* ingot_moe.h: C ABI of the MI355X (gfx950) backend for Ingot's MoE-layer hot path.
+ *
+ * The library (ingot_amd/libingot_moe.so, HIP, one GPU) replaces the Metal
+ * backend for this path: routing, token-to-expert dispatch, grouped
+ * gate/up/SwiGLU/down expert products on GGUF-quantized weights, and the
+ * weighted combine. Plain C types only; no torch or HIP types appear here
+ * (streams are passed as void*).
+ *
+ * Reference interfaces each entry point replaces (paths in majiayu000/ingot):
+ *   ingot_geometry           gguf::geometry              src/gguf.rs:470-491
+ *   ingot_validate_matrix    Gpu::validate_matrix        src/metal.rs:1602-1621
+ *   ingot_route              route()                     src/lib.rs:43-60
+ *   ingot_ctx_create/destroy Gpu::new / Drop             src/metal.rs:238-533
+ *   ingot_device_name        Gpu::name                   src/metal.rs:1247
+ *   ingot_project            Gpu::project                src/metal.rs:1622-1632
+ *   ingot_dequant            Gpu::dequant                src/metal.rs:1581-1601
+ *   ingot_moe                Gpu::moe                    src/metal.rs:1664-1713
+ *   ingot_route_batch        route_topk / route_gpu_batch / glm_route kernels
+ *                            (kernels/generic.metal:479-494, kernels/qwen.metal:177-180,
+ *                            kernels/glm.metal:81-98) as encoded by Generic::ffn
+ *                            (src/generic.rs:510-530) and Glm::moe (src/glm.rs:983-991)
+ *   ingot_layer_create       resident expert weights: Gpu::load_weight +
+ *                            ExpertWeights::Resident (src/metal.rs:546-582,
+ *                            src/weights.rs:55-58), built per layer by
+ *                            Loader::layers (src/generic_arch.rs:370-376)
+ *   ingot_layer_forward      the trunks' MoE FFN call: Generic::ffn MoE branch
+ *                            (src/generic.rs:510-574) and moe_packed (:578-662),
+ *                            Qwen::ffn (src/qwen.rs:1062-1260), resident_ffn_packed
+ *                            (src/qwen_prefill.rs:30-116), Glm::moe (src/glm.rs:974-1060),
+ *                            plus the pre-FFN RMSNorm and residual add of
+ *                            Generic::hidden (src/generic.rs:716-724) when a norm
+ *                            gain is given
+ *
+ * Errors follow the reference: an invalid argument, shape or format is
+ * INGOT_INVALID (io::ErrorKind::InvalidData via invalid(), src/lib.rs:39-41);
+ * non-finite input or output is INGOT_NONFINITE (src/metal.rs:1575-1577,
+ * :1680); a HIP failure is INGOT_DEVICE and is sticky: every later call on the
+ * context fails until it is destroyed and recreated (src/metal.rs:170-190,
+ * :1349-1353). ingot_last_error() returns the message of the last failure.
+ *
+ * Threading: a context, and the layers created on it, belong to one host
+ * thread at a time (Gpu is !Send in the reference). Synchronous entry points
+ * (host buffers) wait for completion; ingot_layer_forward and
+ * ingot_route_batch take device pointers and are asynchronous on the
+ * context's stream.
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum ingot_status {
+    INGOT_OK = 0,
+    INGOT_INVALID = 1,
+    INGOT_NONFINITE = 2,
+    INGOT_DEVICE = 3,
+    INGOT_UNSUPPORTED = 4
+};
+
+/* GGML type ids the kernels decode (src/gguf.rs:470-491 lists every id the
+ * reference loader accepts; ingot_geometry answers for all of them). */
+enum ingot_kind {
+    INGOT_F32 = 0,
+    INGOT_F16 = 1,
+    INGOT_Q4_0 = 2,
+    INGOT_Q8_0 = 8,
+    INGOT_Q4_K = 12,
+    INGOT_IQ2_XS = 17,
+    INGOT_IQ3_XXS = 18,
+    INGOT_IQ4_NL = 20
+};
+
+enum ingot_routing { INGOT_ROUTE_SOFTMAX = 0, INGOT_ROUTE_SIGMOID = 1 };
+
+/* gguf::Matrix (src/gguf.rs:462-469): `count` matrices of rows x cols stored
+ * back to back, row r of matrix e at byte (e * rows + r) * stride. data is a
+ * host pointer to nbytes of GGUF block bytes. */
+typedef struct ingot_matrix {
+    const uint8_t* data;
+    uint64_t nbytes;
+    uint64_t cols;
+    uint64_t rows;
+    uint64_t count;
+    uint32_t kind;
+    uint64_t stride;
+} ingot_matrix;
+
+typedef struct ingot_ctx ingot_ctx;
+typedef struct ingot_layer ingot_layer;
+typedef struct ingot_graph ingot_graph;
+
+/* ---- host-only helpers (no GPU needed) ---- */
+int ingot_geometry(uint32_t kind, uint32_t* block_values, uint32_t* block_bytes);
+int ingot_validate_matrix(const ingot_matrix* m);
+const char* ingot_status_string(int status);
+/* 1 if the kernels decode `kind`, else 0. */
+int ingot_kind_supported(uint32_t kind);
+
+/* ---- context ---- */
+int ingot_ctx_create(int device, ingot_ctx** out);
+void ingot_ctx_destroy(ingot_ctx* ctx);
+const char* ingot_last_error(const ingot_ctx* ctx);
+/* Launch on a caller-owned hipStream_t (NULL: the context's own stream). */
+int ingot_ctx_set_stream(ingot_ctx* ctx, void* hip_stream);
+void* ingot_ctx_stream(const ingot_ctx* ctx);
+int ingot_ctx_synchronize(ingot_ctx* ctx);
+const char* ingot_device_name(ingot_ctx* ctx);
+
+/* ---- drop-ins for the reference's public Gpu API (host buffers, synchronous) ---- */
+/* route(): ids[K] (uint32) and weights[K] for one token's E logits. */
+int ingot_route(ingot_ctx* ctx, const float* logits, uint32_t E, uint32_t K, uint32_t* ids, float* weights);
+/* Gpu::project: y[rows] = m . x, m.count must be 1. */
+int ingot_project(ingot_ctx* ctx, const ingot_matrix* m, const float* x, float* y);
+/* Gpu::dequant: out[count * rows * cols] floats. */
+int ingot_dequant(ingot_ctx* ctx, const ingot_matrix* m, float* out);
+/* Gpu::moe: routed[3] = gate, up, down holding the K selected experts
+ * (count = K, expert k uses weights[k]); shared[3] and shared_gate (a
+ * [cols = H, rows = 1] matrix) may be NULL for a layer without a shared
+ * expert; out[H] = sum_k w_k E_k(x) + sigmoid(shared_gate . x) S(x). */
+int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* shared,
+              const ingot_matrix* shared_gate, const float* x, const float* weights, uint32_t K,
+              float* out);
+
+/* ---- device routing (device pointers, asynchronous) ----
+ * logits [T][E]; softmax mode: selection and weights on logits + bias (bias
+ * may be NULL); sigmoid mode: selection on sigmoid(l) + bias, weights
+ * sigmoid(l) / sum * scale. ids [T][K] uint32, weights [T][K]. A non-finite
+ * logit sets the context's device error flag (reported by
+ * ingot_ctx_check_device_flags). */
+int ingot_route_batch(ingot_ctx* ctx, const float* d_logits, const float* d_bias, uint32_t T, uint32_t E,
+                      uint32_t K, uint32_t routing, float scale, uint32_t* d_ids, float* d_weights);
+/* Synchronizes, reads and clears the device flags; INGOT_NONFINITE if a
+ * kernel met a non-finite router logit since the last check. */
+int ingot_ctx_check_device_flags(ingot_ctx* ctx);
+
+/* ---- resident layer ---- */
+typedef struct ingot_layer_desc {
+    uint32_t hidden;         /* H: embedding_length */
+    uint32_t experts;        /* E: expert_count */
+    uint32_t top_k;          /* K: expert_used_count */
+    uint32_t routing;        /* ingot_routing */
+    float route_scale;       /* sigmoid mode: weight scale (GLM expert_weights_scale); softmax: 1 */
+    float swiglu_limit;      /* 0: plain SwiGLU; > 0: GLM clamp g <= L, |u| <= L */
+    const float* router;     /* host [E][H] fp32 (ffn_gate_inp) */
+    const float* router_bias;/* host [E] or NULL (softmax: added to logits; sigmoid: selection only) */
+    ingot_matrix gate;       /* routed experts [cols H, rows F, count E] */
+    ingot_matrix up;         /* [H, F, E] */
+    ingot_matrix down;       /* [F, H, E] */
+    ingot_matrix shared_gate;/* optional shared expert [H, SF, 1] (data NULL: none) */
+    ingot_matrix shared_up;  /* [H, SF, 1] */
+    ingot_matrix shared_down;/* [SF, H, 1] */
+    const float* shared_gate_vec; /* host [H] or NULL: shared expert scaled by sigmoid(v . x), else by 1 */
+    const float* norm_gain;  /* host [H] or NULL: out = x + MoE(RMSNorm(x)) */
+    float norm_eps;
+} ingot_layer_desc;
+
+/* Copies the layer to device memory (every expert resident). */
+int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* desc, ingot_layer** out);
+/* A second resident copy of the same weights at new device addresses. */
+int ingot_layer_clone(const ingot_layer* src, ingot_layer** out);
+void ingot_layer_destroy(ingot_layer* layer);
+/* Reserve workspace for up to T tokens (done implicitly by forward; call it
+ * before graph capture, which must not allocate). */
+int ingot_layer_reserve(ingot_layer* layer, uint32_t T);
+/* out[T][H] = layer(x[T][H]); device pointers, asynchronous on the context
+ * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL. */
+int ingot_layer_forward(ingot_layer* layer, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
+                        float* d_weights);
+/* Device bytes held by the layer's weights. */
+uint64_t ingot_layer_weight_bytes(const ingot_layer* layer);
+
+/* ---- graphs and timing on the context stream ---- */
+int ingot_graph_begin(ingot_ctx* ctx);
+int ingot_graph_end(ingot_ctx* ctx, ingot_graph** out);
+int ingot_graph_launch(ingot_ctx* ctx, ingot_graph* g);
+void ingot_graph_destroy(ingot_graph* g);
+/* Records HIP events around `launches` replays of g on the context stream and
+ * returns the elapsed milliseconds. */
+int ingot_graph_time(ingot_ctx* ctx, ingot_graph* g, uint32_t launches, float* ms);
+
+/* Kernel-level timing for roofline reporting: captures `reps` replays of one
+ * stage of the last forward of `layer` (same inputs) in a HIP graph, launches
+ * it once to warm up, then times one launch between HIP events on the context
+ * stream and returns the mean milliseconds per stage launch.
+ * stage: 0 router, 1 route, 2 gate/up, 3 down (+combine at decode), 4 combine,
+ * 5 dispatch. Returns INGOT_INVALID if the stage did not run in that forward. */
+int ingot_layer_time_stage(ingot_layer* layer, uint32_t stage, uint32_t reps, float* ms);
+/* The same over n layers (resident copies) replayed round-robin, so that
+ * consecutive launches read weights at different addresses. */
+int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t stage, uint32_t reps, float* ms);
+/* Name of the HIP kernel that implements `stage` in the last forward. */
+const char* ingot_layer_stage_kernel(const ingot_layer* layer, uint32_t stage);
+
+/* ---- device memory helpers (so callers without a tensor library can drive it) ---- */
+int ingot_malloc(ingot_ctx* ctx, uint64_t bytes, void** d_ptr);
+int ingot_free(ingot_ctx* ctx, void* d_ptr);
+int ingot_memcpy_h2d(ingot_ctx* ctx, void* d_dst, const void* h_src, uint64_t bytes);
+int ingot_memcpy_d2h(ingot_ctx* ctx, void* h_dst, const void* d_src, uint64_t bytes);
+
+#ifdef __cplusplus
+}
+#endif

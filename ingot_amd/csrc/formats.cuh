@@ -1,0 +1,424 @@
+// Device-side decoding of GGUF blocks for the MoE kernels (gfx950).
+//
+// Every supported format is handled in "chunks" of 32 weights of one row:
+//   chunk c of a row covers 32 columns chosen by the format so that one chunk
+//   is one natural unit of its block layout (a 32-value group of a 256-value
+//   superblock, or one 32-value block):
+//     Q4_K    superblock c/8, quarter q=(c%8)/2, half h=c%2: 16 bytes of
+//             nibbles holding columns 64q+16h+[0,16) (low nibbles, group 2q)
+//             and 64q+32+16h+[0,16) (high nibbles, group 2q+1)
+//     IQ2_XS  superblock c/8, group c%8: columns 32*(c%8)+[0,32)
+//     IQ3_XXS superblock c/8, group c%8: columns 32*(c%8)+[0,32)
+//     Q8_0, Q4_0, IQ4_NL, F32, F16: block / columns 32c+[0,32)
+//   Chunks 2s and 2s+1 together always cover the 64 columns [64s, 64s+64):
+//   the GEMM kernels stage weights in 64-column slabs built from two chunks.
+//
+// The formulas are the reference's (kernels/iq3_mix.metal:13-36 for Q4_K,
+// IQ2_XS and IQ3_XXS; kernels/moe.metal:14-17, :76-80 for F32, F16, Q4_0, Q8_0
+// and IQ4_NL), organised for 16-byte loads and factored scales: a chunk dot
+// product is sum_i w_i x_i with w_i = scale * small_int_i - min, evaluated as
+// scale * sum_i small_int_i x_i - min * sum_i x_i.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "codebooks.h"
+
+namespace ingot {
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+// 4 bytes from a 2-byte aligned address.
+__device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+    return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+}
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t i) { return (w >> (8 * i)) & 0xffu; }
+__device__ __forceinline__ float ubyte_f(uint32_t w, uint32_t i) { return (float)((w >> (8 * i)) & 0xffu); }
+__device__ __forceinline__ float sbyte_f(uint32_t w, uint32_t i) { return (float)(int8_t)((w >> (8 * i)) & 0xffu); }
+__device__ __forceinline__ float flip_sign(float v, uint32_t bit) {
+    return __int_as_float(__float_as_int(v) ^ (int)(bit << 31));
+}
+
+template <int KIND>
+struct Fmt;
+
+// ------------------------------------------------------------------ Q4_K (12)
+template <>
+struct Fmt<12> {
+    static constexpr uint32_t BLOCK = 256, BYTES = 144;
+    // Column of value i (0..31) of chunk c.
+    __device__ static uint32_t col(uint32_t c, uint32_t i) {
+        uint32_t q = c & 7u;
+        return (c >> 3) * 256u + 64u * (q >> 1) + 16u * (q & 1u) + (i < 16 ? i : 16u + i);
+    }
+    __device__ static void load_x(const float* x, uint32_t c, float* xv) {
+        uint32_t q = c & 7u;
+        const float* p = x + (c >> 3) * 256u + 64u * (q >> 1) + 16u * (q & 1u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 a = reinterpret_cast<const float4*>(p)[i];
+            float4 b = reinterpret_cast<const float4*>(p + 32)[i];
+            xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
+            xv[16 + 4 * i] = b.x; xv[17 + 4 * i] = b.y; xv[18 + 4 * i] = b.z; xv[19 + 4 * i] = b.w;
+        }
+    }
+    // Scale (sc) and min (m) of the chunk's two groups, from the 16-byte header
+    // {d, dmin, scales[12]} (ggml get_scale_min_k4, kernels/iq3_mix.metal:13-15).
+    __device__ static void scales(uint4 hdr, uint32_t c, float& d0, float& m0, float& d1, float& m1) {
+        uint32_t qq = (c & 7u) >> 1;  // 64-column quarter: groups 2qq, 2qq+1
+        uint32_t scw, mw;
+        if (qq < 2) {
+            scw = hdr.y & 0x3f3f3f3fu;
+            mw = hdr.z & 0x3f3f3f3fu;
+        } else {
+            scw = (hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u);
+            mw = ((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u);
+        }
+        uint32_t g0 = (2u * qq) & 3u;
+        float d = half_bits_to_float(hdr.x), dm = half_bits_to_float(hdr.x >> 16);
+        d0 = d * ubyte_f(scw, g0);
+        d1 = d * ubyte_f(scw, g0 + 1);
+        m0 = dm * ubyte_f(mw, g0);
+        m1 = dm * ubyte_f(mw, g0 + 1);
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float xs0, float xs1) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        uint32_t q = c & 7u;
+        uint4 hdr = *reinterpret_cast<const uint4*>(b);
+        uint4 qs = *reinterpret_cast<const uint4*>(b + 16 + 32 * (q >> 1) + 16 * (q & 1u));
+        float d0, m0, d1, m1;
+        scales(hdr, c, d0, m0, d1, m1);
+        uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+        float slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo = w[k] & 0x0f0f0f0fu, hi = (w[k] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                slo = __builtin_fmaf(ubyte_f(lo, j), xv[4 * k + j], slo);
+                shi = __builtin_fmaf(ubyte_f(hi, j), xv[16 + 4 * k + j], shi);
+            }
+        }
+        return (d0 * slo + d1 * shi) - (m0 * xs0 + m1 * xs1);
+    }
+    // Raw bytes of a chunk for the GEMM staging path: {header, nibbles}.
+    struct Raw {
+        uint4 a, b;
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        uint32_t q = c & 7u;
+        Raw r;
+        r.a = *reinterpret_cast<const uint4*>(b);
+        r.b = *reinterpret_cast<const uint4*>(b + 16 + 32 * (q >> 1) + 16 * (q & 1u));
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
+        float d0, m0, d1, m1;
+        scales(r.a, c, d0, m0, d1, m1);
+        uint32_t v[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo = v[k] & 0x0f0f0f0fu, hi = (v[k] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[4 * k + j] = d0 * ubyte_f(lo, j) - m0;
+                w[16 + 4 * k + j] = d1 * ubyte_f(hi, j) - m1;
+            }
+        }
+    }
+};
+
+// --------------------------------------------------------- contiguous chunks
+// Formats whose chunk c covers columns 32c..32c+31 in order.
+struct Contig {
+    __device__ static uint32_t col(uint32_t c, uint32_t i) { return 32u * c + i; }
+    __device__ static void load_x(const float* x, uint32_t c, float* xv) {
+        const float4* p = reinterpret_cast<const float4*>(x + 32u * c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float4 a = p[i];
+            xv[4 * i] = a.x; xv[4 * i + 1] = a.y; xv[4 * i + 2] = a.z; xv[4 * i + 3] = a.w;
+        }
+    }
+};
+
+// ------------------------------------------------------------------- F32 (0)
+template <>
+struct Fmt<0> : Contig {
+    static constexpr uint32_t BLOCK = 1, BYTES = 4;
+    struct Raw {
+        float4 v[8];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        Raw r;
+        const float4* p = reinterpret_cast<const float4*>(row + 128u * c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.v[i] = p[i];
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w[4 * i] = r.v[i].x; w[4 * i + 1] = r.v[i].y; w[4 * i + 2] = r.v[i].z; w[4 * i + 3] = r.v[i].w;
+        }
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
+        Raw r = load_raw(row, c);
+        float w[32];
+        dequant_raw(r, c, w);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s = __builtin_fmaf(w[i], xv[i], s);
+        return s;
+    }
+};
+
+// ------------------------------------------------------------------ Q8_0 (8)
+template <>
+struct Fmt<8> : Contig {
+    static constexpr uint32_t BLOCK = 32, BYTES = 34;
+    struct Raw {
+        uint32_t d;
+        uint32_t q[8];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + c * BYTES;
+        Raw r;
+        r.d = ld_u16(b);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.q[i] = ld_u32_a2(b + 2 + 4 * i);
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[4 * i + j] = d * sbyte_f(r.q[i], j);
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
+        Raw r = load_raw(row, c);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s = __builtin_fmaf(sbyte_f(r.q[i], j), xv[4 * i + j], s);
+        return half_bits_to_float(r.d) * s;
+    }
+};
+
+// ------------------------------------------------- Q4_0 (2) and IQ4_NL (20)
+// 18-byte blocks: fp16 d, 16 bytes of nibbles; value i < 16 is the low nibble
+// of byte i, value i >= 16 the high nibble of byte i - 16.
+template <bool NL>
+struct Nibble32 : Contig {
+    static constexpr uint32_t BLOCK = 32, BYTES = 18;
+    struct Raw {
+        uint32_t d;
+        uint32_t q[4];
+    };
+    __device__ static float value(uint32_t nib) {
+        if constexpr (NL) return (float)ingot_kvalues_iq4nl[nib];
+        else return (float)((int)nib - 8);
+    }
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + c * BYTES;
+        Raw r;
+        r.d = ld_u16(b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.q[i] = ld_u32_a2(b + 2 + 4 * i);
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t byte = byte_of(r.q[i], j);
+                w[4 * i + j] = d * value(byte & 15u);
+                w[16 + 4 * i + j] = d * value(byte >> 4);
+            }
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
+        Raw r = load_raw(row, c);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t byte = byte_of(r.q[i], j);
+                s = __builtin_fmaf(value(byte & 15u), xv[4 * i + j], s);
+                s = __builtin_fmaf(value(byte >> 4), xv[16 + 4 * i + j], s);
+            }
+        return half_bits_to_float(r.d) * s;
+    }
+};
+template <>
+struct Fmt<2> : Nibble32<false> {};
+template <>
+struct Fmt<20> : Nibble32<true> {};
+
+// --------------------------------------------------------------- IQ2_XS (17)
+// 74-byte superblocks (2-byte aligned): fp16 d @0, 32 u16 codes @2 (9-bit grid
+// index | 7-bit sign index << 9, one per 8 values), 8 scale bytes @66 (4 bits
+// per 16 values). w = d * (0.5 + s) * 0.25 * grid * sign.
+template <>
+struct Fmt<17> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 74;
+    struct Raw {
+        uint32_t d, scale;
+        uint32_t code[4];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        uint32_t g = c & 7u;
+        Raw r;
+        r.d = ld_u16(b);
+        r.scale = b[66 + g];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) r.code[l] = ld_u16(b + 2 + 8 * g + 2 * l);
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            float db = d * (0.5f + (float)((r.scale >> (4 * (l / 2))) & 15u)) * 0.25f;
+            uint64_t grid = ingot_iq2xs_grid[r.code[l] & 511u];
+            uint32_t sg = ingot_ksign(r.code[l] >> 9);
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                w[8 * l + v] = flip_sign(db * (float)((grid >> (8 * v)) & 255u), (sg >> v) & 1u);
+        }
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
+        Raw r = load_raw(row, c);
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            uint64_t grid = ingot_iq2xs_grid[r.code[l] & 511u];
+            uint32_t sg = ingot_ksign(r.code[l] >> 9);
+            float t = 0.f;
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                t = __builtin_fmaf((float)((grid >> (8 * v)) & 255u), flip_sign(xv[8 * l + v], (sg >> v) & 1u), t);
+            s = __builtin_fmaf(0.5f + (float)((r.scale >> (4 * (l / 2))) & 15u), t, s);
+        }
+        return half_bits_to_float(r.d) * 0.25f * s;
+    }
+};
+
+// -------------------------------------------------------------- IQ3_XXS (18)
+// 98-byte superblocks (2-byte aligned): fp16 d @0, 64 grid bytes @2 (one
+// 4-value codebook entry each), 8 u32 @66 (four 7-bit sign indices and a
+// 4-bit scale in bits 28..31 per 32 values). w = d * (0.5 + s) * 0.5 * grid * sign.
+template <>
+struct Fmt<18> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 98;
+    struct Raw {
+        uint32_t d, aux;
+        uint32_t gb[4];  // 8 grid bytes, two per u16 word
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        uint32_t g = c & 7u;
+        Raw r;
+        r.d = ld_u16(b);
+        r.aux = ld_u32_a2(b + 66 + 4 * g);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) r.gb[l] = ld_u16(b + 2 + 8 * g + 2 * l);
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        float db = half_bits_to_float(r.d) * (0.5f + (float)(r.aux >> 28)) * 0.5f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            uint32_t sg = ingot_ksign((r.aux >> (7 * l)) & 127u);
+            uint32_t lo = ingot_iq3xxs_grid[r.gb[l] & 255u], hi = ingot_iq3xxs_grid[r.gb[l] >> 8];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                w[8 * l + v] = flip_sign(db * ubyte_f(lo, v), (sg >> v) & 1u);
+                w[8 * l + 4 + v] = flip_sign(db * ubyte_f(hi, v), (sg >> (4 + v)) & 1u);
+            }
+        }
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
+        Raw r = load_raw(row, c);
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            uint32_t sg = ingot_ksign((r.aux >> (7 * l)) & 127u);
+            uint32_t lo = ingot_iq3xxs_grid[r.gb[l] & 255u], hi = ingot_iq3xxs_grid[r.gb[l] >> 8];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                s = __builtin_fmaf(ubyte_f(lo, v), flip_sign(xv[8 * l + v], (sg >> v) & 1u), s);
+                s = __builtin_fmaf(ubyte_f(hi, v), flip_sign(xv[8 * l + 4 + v], (sg >> (4 + v)) & 1u), s);
+            }
+        }
+        return half_bits_to_float(r.d) * (0.5f + (float)(r.aux >> 28)) * 0.5f * s;
+    }
+};
+
+// Scalar decode of weight j of a row, any supported kind (slow path for the
+// generic projection / dequant drop-ins).
+__device__ inline float dequant_value(const uint8_t* row, uint32_t kind, uint32_t j) {
+    switch (kind) {
+        case 0: return reinterpret_cast<const float*>(row)[j];
+        case 1: return half_bits_to_float(ld_u16(row + 2 * j));
+        case 2: {
+            const uint8_t* b = row + (j / 32) * 18;
+            uint32_t k = j % 32;
+            return half_bits_to_float(ld_u16(b)) * (float)((int)((b[2 + k % 16] >> (4 * (k / 16))) & 15) - 8);
+        }
+        case 8: {
+            const uint8_t* b = row + (j / 32) * 34;
+            return half_bits_to_float(ld_u16(b)) * (float)(int8_t)b[2 + j % 32];
+        }
+        case 20: {
+            const uint8_t* b = row + (j / 32) * 18;
+            uint32_t k = j % 32;
+            return half_bits_to_float(ld_u16(b)) * (float)ingot_kvalues_iq4nl[(b[2 + k % 16] >> (4 * (k / 16))) & 15];
+        }
+        case 12: {
+            const uint8_t* b = row + (j / 256) * 144;
+            uint32_t k = j % 256, g = k / 32, sc, m;
+            const uint8_t* s = b + 4;
+            if (g < 4) {
+                sc = s[g] & 63;
+                m = s[g + 4] & 63;
+            } else {
+                sc = (s[g + 4] & 15) | ((s[g - 4] >> 6) << 4);
+                m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+            }
+            uint32_t q = (b[16 + 32 * (k / 64) + k % 32] >> (4 * (g % 2))) & 15;
+            float d1 = half_bits_to_float(ld_u16(b)) * (float)sc, m1 = half_bits_to_float(ld_u16(b + 2)) * (float)m;
+            return d1 * (float)q - m1;
+        }
+        case 17: {
+            const uint8_t* b = row + (j / 256) * 74;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            uint32_t q = ld_u16(b + 2 + 2 * (4 * g + l));
+            float grid = (float)((ingot_iq2xs_grid[q & 511] >> (8 * v)) & 255);
+            float db = half_bits_to_float(ld_u16(b)) * (0.5f + (float)((b[66 + g] >> (4 * (l / 2))) & 15)) * 0.25f;
+            return flip_sign(db * grid, (ingot_ksign(q >> 9) >> v) & 1u);
+        }
+        case 18: {
+            const uint8_t* b = row + (j / 256) * 98;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            uint32_t aux = ld_u32_a2(b + 66 + 4 * g);
+            float grid = (float)((ingot_iq3xxs_grid[b[2 + 8 * g + 2 * l + v / 4]] >> (8 * (v % 4))) & 255);
+            float db = half_bits_to_float(ld_u16(b)) * (0.5f + (float)(aux >> 28)) * 0.5f;
+            return flip_sign(db * grid, (ingot_ksign((aux >> (7 * l)) & 127) >> v) & 1u);
+        }
+        default: return __builtin_nanf("");
+    }
+}
+
+}  // namespace ingot

@@ -1,0 +1,1015 @@
+// C ABI of the MI355X MoE-layer backend (declared in include/ingot_moe.h).
+// Host code: argument validation with the reference's error contract,
+// device residency of expert weights, workspace, kernel selection, HIP graphs
+// and event timing. Kernels live in moe_kernels.cuh.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "../../include/ingot_moe.h"
+#include "moe_kernels.cuh"
+
+using namespace ingot;
+
+struct ingot_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;
+    hipStream_t stream = nullptr;
+    bool poisoned = false;
+    std::string err;
+    std::string name;
+    uint32_t* d_flags = nullptr;
+};
+
+struct ingot_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+int fail(ingot_ctx* ctx, int status, const std::string& msg) {
+    if (ctx) {
+        ctx->err = msg;
+        if (status == INGOT_DEVICE) ctx->poisoned = true;
+    }
+    return status;
+}
+
+#define HIP_TRY(ctx, call)                                                                        \
+    do {                                                                                          \
+        hipError_t e_ = (call);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return fail((ctx), INGOT_DEVICE, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define CHECK_CTX(ctx)                                                                       \
+    do {                                                                                     \
+        if (!(ctx)) return INGOT_INVALID;                                                    \
+        if ((ctx)->poisoned) return fail((ctx), INGOT_DEVICE, "device failed earlier: recreate the context"); \
+        HIP_TRY((ctx), hipSetDevice((ctx)->device));                                         \
+    } while (0)
+
+#define LAUNCH_CHECK(ctx)                                                                         \
+    do {                                                                                          \
+        hipError_t e_ = hipGetLastError();                                                        \
+        if (e_ != hipSuccess) return fail((ctx), INGOT_DEVICE, std::string("kernel launch: ") + hipGetErrorString(e_)); \
+    } while (0)
+
+bool all_finite(const float* v, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i)
+        if (!std::isfinite(v[i])) return false;
+    return true;
+}
+
+int geometry(uint32_t kind, uint32_t* block, uint32_t* bytes) {
+    uint32_t b = 0, n = 0;
+    switch (kind) {  // src/gguf.rs:470-491
+        case 0: b = 1; n = 4; break;
+        case 1: case 30: b = 1; n = 2; break;
+        case 2: b = 32; n = 18; break;
+        case 8: b = 32; n = 34; break;
+        case 10: b = 256; n = 84; break;
+        case 12: b = 256; n = 144; break;
+        case 13: b = 256; n = 176; break;
+        case 14: b = 256; n = 210; break;
+        case 16: b = 256; n = 66; break;
+        case 17: b = 256; n = 74; break;
+        case 18: b = 256; n = 98; break;
+        case 20: b = 32; n = 18; break;
+        case 21: b = 256; n = 110; break;
+        case 22: b = 256; n = 82; break;
+        case 23: b = 256; n = 136; break;
+        case 29: b = 256; n = 56; break;
+        case 42: b = 64; n = 18; break;
+        default: return INGOT_INVALID;
+    }
+    if (block) *block = b;
+    if (bytes) *bytes = n;
+    return INGOT_OK;
+}
+
+bool supported(uint32_t kind) {
+    return kind == 0 || kind == 1 || kind == 2 || kind == 8 || kind == 12 || kind == 17 || kind == 18 || kind == 20;
+}
+
+// src/metal.rs:1602-1621.
+int validate(const ingot_matrix* m) {
+    uint32_t block, bytes;
+    if (!m || geometry(m->kind, &block, &bytes) != INGOT_OK) return INGOT_INVALID;
+    if (m->cols == 0 || m->rows == 0 || m->count == 0 || m->cols % block) return INGOT_INVALID;
+    if (m->stride != m->cols / block * bytes) return INGOT_INVALID;
+    unsigned __int128 total = (unsigned __int128)m->stride * m->rows * m->count;
+    if (total != m->nbytes) return INGOT_INVALID;
+    const uint64_t lim = 0xffffffffull;
+    if (m->cols > lim || m->rows > lim || m->count > lim || m->stride > lim) return INGOT_INVALID;
+    if (!m->data) return INGOT_INVALID;
+    return INGOT_OK;
+}
+
+struct DevMatrix {
+    uint8_t* d = nullptr;
+    uint64_t nbytes = 0, cols = 0, rows = 0, count = 0, stride = 0;
+    uint32_t kind = 0;
+};
+
+int upload_matrix(ingot_ctx* ctx, const ingot_matrix* m, DevMatrix* out) {
+    HIP_TRY(ctx, hipMalloc(&out->d, m->nbytes));
+    HIP_TRY(ctx, hipMemcpy(out->d, m->data, m->nbytes, hipMemcpyHostToDevice));
+    out->nbytes = m->nbytes;
+    out->cols = m->cols;
+    out->rows = m->rows;
+    out->count = m->count;
+    out->stride = m->stride;
+    out->kind = m->kind;
+    return INGOT_OK;
+}
+
+template <typename T>
+int upload(ingot_ctx* ctx, const T* h, uint64_t n, T** d) {
+    HIP_TRY(ctx, hipMalloc(reinterpret_cast<void**>(d), sizeof(T) * n));
+    HIP_TRY(ctx, hipMemcpy(*d, h, sizeof(T) * n, hipMemcpyHostToDevice));
+    return INGOT_OK;
+}
+
+// ------------------------------------------------------------------ launchers
+// Each returns false if no instantiation covers the shape.
+
+bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_sg, const float* x, const float* W,
+                   const float* sgvec, const float* gain, float eps, float* logits, float* sgl, float* xn) {
+    const uint32_t rows = E + (has_sg ? 1u : 0u);
+    const bool decode = T <= 4;
+    const uint32_t epw = decode ? 1u : 8u;
+    const uint32_t gy = (rows + 4 * epw - 1) / (4 * epw);
+#define ROUTER(TOK, HBV)                                                                                       \
+    do {                                                                                                       \
+        dim3 grid((T + TOK - 1) / TOK, gy);                                                                    \
+        hipLaunchKernelGGL((k_router<TOK, HBV>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, epw,     \
+                           logits, sgl, xn);                                                                   \
+        return true;                                                                                           \
+    } while (0)
+    if (HB == 8) {
+        if (decode) ROUTER(1, 8);
+        ROUTER(4, 8);
+    }
+    if (HB == 16) {
+        if (decode) ROUTER(1, 16);
+        ROUTER(2, 16);
+    }
+    if (HB == 4) {
+        if (decode) ROUTER(1, 4);
+        ROUTER(4, 4);
+    }
+#undef ROUTER
+    return false;
+}
+
+constexpr int GEMV_RPW = 4;
+
+// Top-K routing, keys per lane NE = E/64 rounded up to a power of two.
+void launch_route(hipStream_t s, const float* logits, const float* bias, uint32_t T, uint32_t E, uint32_t K,
+                  uint32_t mode, float scale, uint32_t* ids, float* w, uint32_t* flags) {
+    dim3 grid((T + 3) / 4);
+    const uint32_t ne = (E + 63) / 64;
+#define ROUTE(NEV) hipLaunchKernelGGL((k_route<NEV>), grid, dim3(256), 0, s, logits, bias, T, E, K, mode, scale, ids, w, flags)
+    if (ne <= 1) ROUTE(1);
+    else if (ne <= 2) ROUTE(2);
+    else if (ne <= 4) ROUTE(4);
+    else if (ne <= 8) ROUTE(8);
+    else ROUTE(16);
+#undef ROUTE
+}
+
+template <int KIND>
+bool gate_up_cpl(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* g, const uint8_t* u, uint64_t gs, uint64_t us,
+                 uint32_t F, uint32_t H, const float* x, const uint32_t* ids, uint32_t K, float limit, float* act) {
+    if (cpl == 1) {
+        hipLaunchKernelGGL((k_gemv_gate_up<KIND, 1, GEMV_RPW>), grid, dim3(256), 0, s, g, u, gs, us, F, H, x, ids, K,
+                           limit, act);
+        return true;
+    }
+    if (cpl == 2) {
+        hipLaunchKernelGGL((k_gemv_gate_up<KIND, 2, GEMV_RPW>), grid, dim3(256), 0, s, g, u, gs, us, F, H, x, ids, K,
+                           limit, act);
+        return true;
+    }
+    return false;
+}
+
+bool launch_gemv_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const uint8_t* u, uint64_t gs, uint64_t us,
+                         uint32_t F, uint32_t H, uint32_t pairs, const float* x, const uint32_t* ids, uint32_t K,
+                         float limit, float* act) {
+    const uint32_t cpl = (H / 32 + 63) / 64;
+    dim3 grid((F + 4 * GEMV_RPW - 1) / (4 * GEMV_RPW), pairs);
+    switch (kind) {
+        case 0: return gate_up_cpl<0>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        case 2: return gate_up_cpl<2>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        case 8: return gate_up_cpl<8>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        case 12: return gate_up_cpl<12>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        case 17: return gate_up_cpl<17>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        case 18: return gate_up_cpl<18>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        case 20: return gate_up_cpl<20>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+        default: return false;
+    }
+}
+
+struct DownArgs {
+    const uint8_t *down, *sdown;
+    uint64_t dstride, sdstride;
+    uint32_t H, F, SF;
+    const float *act, *sact;
+    const uint32_t* ids;
+    const float *wts, *sgl;
+    uint32_t K;
+    const float* res;
+    float* out;
+};
+
+template <int KD, int KS, int VPL>
+void down_launch(hipStream_t s, dim3 grid, const DownArgs& a) {
+    hipLaunchKernelGGL((k_gemv_down<KD, KS, VPL, GEMV_RPW>), grid, dim3(256), 0, s, a.down, a.dstride, a.sdown,
+                       a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.wts, a.sgl, a.K, a.res, a.out);
+}
+
+template <int KD, int KS>
+bool down_vpl(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
+    switch (vpl) {
+        case 1: down_launch<KD, KS, 1>(s, grid, a); return true;
+        case 2: down_launch<KD, KS, 2>(s, grid, a); return true;
+        case 3: down_launch<KD, KS, 3>(s, grid, a); return true;
+        case 4: down_launch<KD, KS, 4>(s, grid, a); return true;
+        case 5: down_launch<KD, KS, 5>(s, grid, a); return true;
+        case 6: down_launch<KD, KS, 6>(s, grid, a); return true;
+        case 7: down_launch<KD, KS, 7>(s, grid, a); return true;
+        case 8: down_launch<KD, KS, 8>(s, grid, a); return true;
+        default: return false;
+    }
+}
+
+template <int KS>
+bool shared_add_cpl(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H, uint32_t SF,
+                    const float* sact, const float* sgl, float* out) {
+    if (cpl == 1) {
+        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 1>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
+        return true;
+    }
+    if (cpl == 2) {
+        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 2>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
+        return true;
+    }
+    return false;
+}
+
+bool launch_shared_down_add(hipStream_t s, uint32_t ks, const uint8_t* sd, uint64_t sds, uint32_t H, uint32_t SF,
+                            uint32_t T, const float* sact, const float* sgl, float* out) {
+    const uint32_t cpl = (SF / 32 + 63) / 64;
+    dim3 grid((H + 3) / 4, T);
+    switch (ks) {
+        case 0: return shared_add_cpl<0>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        case 2: return shared_add_cpl<2>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        case 8: return shared_add_cpl<8>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        case 12: return shared_add_cpl<12>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        case 17: return shared_add_cpl<17>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        case 18: return shared_add_cpl<18>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        case 20: return shared_add_cpl<20>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        default: return false;
+    }
+}
+
+template <bool GATEUP>
+bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, const uint8_t* w1, uint64_t s0,
+                 uint64_t s1, uint32_t rows, uint32_t kdim, const float* a, const uint32_t* pairs, uint32_t K,
+                 const uint32_t* tiles, uint32_t ldo, float limit, float* out) {
+#define GEMM(KV)                                                                                                 \
+    case KV:                                                                                                     \
+        hipLaunchKernelGGL((k_gemm<KV, GATEUP>), grid, dim3(256), 0, s, w0, w1, s0, s1, rows, kdim, a, pairs, K, \
+                           tiles, ldo, limit, out);                                                              \
+        return true;
+    switch (kind) {
+        GEMM(0)
+        GEMM(2)
+        GEMM(8)
+        GEMM(12)
+        GEMM(17)
+        GEMM(18)
+        GEMM(20)
+        default: return false;
+    }
+#undef GEMM
+}
+
+}  // namespace
+
+// Decode down + combine: routed-only for every kind, plus a fused shared expert
+// for the format pairs the configurations use (can_fuse_shared). Returns false
+// if no instantiation covers the shape.
+static bool can_fuse_shared(uint32_t kd, int ks) {
+    return (kd == 17 && ks == 8) || (kd == 12 && ks == 12) || (kd == 20 && ks == 20) || (kd == 8 && ks == 8);
+}
+
+static bool gemv_down(hipStream_t s, uint32_t kd, int ks, const DownArgs& a, uint32_t T) {
+    const uint32_t nv = a.K * (a.F / 32) + (ks >= 0 ? a.SF / 32 : 0);
+    const uint32_t vpl = (nv + 63) / 64;
+    dim3 grid((a.H + 4 * GEMV_RPW - 1) / (4 * GEMV_RPW), T);
+    if (ks < 0) {
+        switch (kd) {
+            case 0: return down_vpl<0, -1>(s, vpl, grid, a);
+            case 2: return down_vpl<2, -1>(s, vpl, grid, a);
+            case 8: return down_vpl<8, -1>(s, vpl, grid, a);
+            case 12: return down_vpl<12, -1>(s, vpl, grid, a);
+            case 17: return down_vpl<17, -1>(s, vpl, grid, a);
+            case 18: return down_vpl<18, -1>(s, vpl, grid, a);
+            case 20: return down_vpl<20, -1>(s, vpl, grid, a);
+            default: return false;
+        }
+    }
+    if (kd == 17 && ks == 8) return down_vpl<17, 8>(s, vpl, grid, a);
+    if (kd == 12 && ks == 12) return down_vpl<12, 12>(s, vpl, grid, a);
+    if (kd == 20 && ks == 20) return down_vpl<20, 20>(s, vpl, grid, a);
+    if (kd == 8 && ks == 8) return down_vpl<8, 8>(s, vpl, grid, a);
+    return false;
+}
+
+// ------------------------------------------------------------------ layer
+enum Stage { ST_ROUTER = 0, ST_ROUTE = 1, ST_GATEUP = 2, ST_DOWN = 3, ST_COMBINE = 4, ST_DISPATCH = 5, ST_N = 6 };
+
+struct ingot_layer {
+    ingot_ctx* ctx = nullptr;
+    uint32_t H = 0, E = 0, K = 0, F = 0, SF = 0, routing = 0;
+    float scale = 1.f, limit = 0.f, eps = 0.f;
+    bool has_shared = false, has_sgvec = false, has_norm = false, has_bias = false;
+    float *router = nullptr, *bias = nullptr, *sgvec = nullptr, *gain = nullptr;
+    DevMatrix gate, up, down, sgate, sup, sdown;
+    // workspace
+    uint32_t cap_T = 0;
+    void* ws = nullptr;
+    float *xn = nullptr, *logits = nullptr, *sgl = nullptr, *wts = nullptr, *act = nullptr, *sact = nullptr,
+          *Y = nullptr, *Ys = nullptr;
+    uint32_t *ids = nullptr, *counts = nullptr, *first = nullptr, *tiles = nullptr, *pairs = nullptr,
+             *inverse = nullptr, *stiles = nullptr;
+    uint32_t tile_cap = 0, stile_cap = 0;
+    std::function<void(hipStream_t)> stage[ST_N];
+    const char* stage_name[ST_N] = {};
+};
+
+static void free_dev(ingot_layer* L) {
+    for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown})
+        if (m->d) (void)hipFree(m->d);
+    for (float* p : {L->router, L->bias, L->sgvec, L->gain})
+        if (p) (void)hipFree(p);
+    if (L->ws) (void)hipFree(L->ws);
+}
+
+static int reserve(ingot_layer* L, uint32_t T) {
+    ingot_ctx* ctx = L->ctx;
+    if (T <= L->cap_T) return INGOT_OK;
+    const uint64_t P = (uint64_t)T * L->K;
+    const uint32_t tile_cap = (uint32_t)((P + TM - 1) / TM + L->E);
+    const uint32_t stile_cap = (T + TM - 1) / TM;
+    struct Part {
+        void** p;
+        uint64_t bytes;
+    };
+    std::vector<Part> parts = {
+        {(void**)&L->xn, 4ull * T * L->H},       {(void**)&L->logits, 4ull * T * L->E},
+        {(void**)&L->sgl, 4ull * T},             {(void**)&L->ids, 4ull * P},
+        {(void**)&L->wts, 4ull * P},             {(void**)&L->act, 4ull * P * L->F},
+        {(void**)&L->sact, 4ull * T * (L->SF ? L->SF : 1)},
+        {(void**)&L->Y, 4ull * P * L->H},        {(void**)&L->Ys, 4ull * T * L->H},
+        {(void**)&L->counts, 4ull * L->E},       {(void**)&L->first, 4ull * L->E},
+        {(void**)&L->tiles, 16ull * tile_cap},   {(void**)&L->pairs, 4ull * P},
+        {(void**)&L->inverse, 4ull * P},         {(void**)&L->stiles, 16ull * stile_cap},
+    };
+    uint64_t total = 0;
+    for (auto& p : parts) total += (p.bytes + 255) & ~255ull;
+    void* ws = nullptr;
+    if (L->ws) (void)hipFree(L->ws);
+    L->ws = nullptr;
+    L->cap_T = 0;
+    HIP_TRY(ctx, hipMalloc(&ws, total));
+    L->ws = ws;
+    uint64_t off = 0;
+    for (auto& p : parts) {
+        *p.p = static_cast<char*>(ws) + off;
+        off += (p.bytes + 255) & ~255ull;
+    }
+    L->cap_T = T;
+    L->tile_cap = tile_cap;
+    L->stile_cap = stile_cap;
+    return INGOT_OK;
+}
+
+// ------------------------------------------------------------------ C ABI
+extern "C" {
+
+int ingot_geometry(uint32_t kind, uint32_t* block_values, uint32_t* block_bytes) {
+    return geometry(kind, block_values, block_bytes);
+}
+int ingot_validate_matrix(const ingot_matrix* m) { return validate(m); }
+int ingot_kind_supported(uint32_t kind) { return supported(kind) ? 1 : 0; }
+
+const char* ingot_status_string(int status) {
+    switch (status) {
+        case INGOT_OK: return "ok";
+        case INGOT_INVALID: return "invalid argument, shape or format";
+        case INGOT_NONFINITE: return "non-finite values";
+        case INGOT_DEVICE: return "device failure";
+        case INGOT_UNSUPPORTED: return "unsupported format or shape";
+        default: return "unknown status";
+    }
+}
+
+int ingot_ctx_create(int device, ingot_ctx** out) {
+    if (!out) return INGOT_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return INGOT_DEVICE;
+    if (device < 0 || device >= n) return INGOT_INVALID;
+    ingot_ctx* ctx = new ingot_ctx();
+    ctx->device = device;
+    auto bad = [&](hipError_t e) {
+        if (e == hipSuccess) return false;
+        delete ctx;
+        return true;
+    };
+    if (bad(hipSetDevice(device))) return INGOT_DEVICE;
+    hipDeviceProp_t prop;
+    if (bad(hipGetDeviceProperties(&prop, device))) return INGOT_DEVICE;
+    ctx->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    if (bad(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking))) return INGOT_DEVICE;
+    ctx->stream = ctx->own;
+    if (bad(hipMalloc(&ctx->d_flags, 256))) return INGOT_DEVICE;
+    if (bad(hipMemset(ctx->d_flags, 0, 256))) return INGOT_DEVICE;
+    *out = ctx;
+    return INGOT_OK;
+}
+
+void ingot_ctx_destroy(ingot_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->d_flags) (void)hipFree(ctx->d_flags);
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+const char* ingot_last_error(const ingot_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+
+int ingot_ctx_set_stream(ingot_ctx* ctx, void* hip_stream) {
+    CHECK_CTX(ctx);
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+    return INGOT_OK;
+}
+void* ingot_ctx_stream(const ingot_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int ingot_ctx_synchronize(ingot_ctx* ctx) {
+    CHECK_CTX(ctx);
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return INGOT_OK;
+}
+
+const char* ingot_device_name(ingot_ctx* ctx) { return ctx ? ctx->name.c_str() : ""; }
+
+int ingot_ctx_check_device_flags(ingot_ctx* ctx) {
+    CHECK_CTX(ctx);
+    uint32_t flags = 0, zero = 0;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemcpy(&flags, ctx->d_flags, 4, hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, hipMemcpy(ctx->d_flags, &zero, 4, hipMemcpyHostToDevice));
+    if (flags & FLAG_NONFINITE) return fail(ctx, INGOT_NONFINITE, "non-finite router logits");
+    return INGOT_OK;
+}
+
+int ingot_malloc(ingot_ctx* ctx, uint64_t bytes, void** d_ptr) {
+    CHECK_CTX(ctx);
+    if (!d_ptr) return INGOT_INVALID;
+    HIP_TRY(ctx, hipMalloc(d_ptr, bytes ? bytes : 1));
+    return INGOT_OK;
+}
+int ingot_free(ingot_ctx* ctx, void* d_ptr) {
+    CHECK_CTX(ctx);
+    if (d_ptr) HIP_TRY(ctx, hipFree(d_ptr));
+    return INGOT_OK;
+}
+int ingot_memcpy_h2d(ingot_ctx* ctx, void* d_dst, const void* h_src, uint64_t bytes) {
+    CHECK_CTX(ctx);
+    HIP_TRY(ctx, hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return INGOT_OK;
+}
+int ingot_memcpy_d2h(ingot_ctx* ctx, void* h_dst, const void* d_src, uint64_t bytes) {
+    CHECK_CTX(ctx);
+    HIP_TRY(ctx, hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return INGOT_OK;
+}
+
+// ---- route() drop-in (src/lib.rs:43-60) ----
+int ingot_route(ingot_ctx* ctx, const float* logits, uint32_t E, uint32_t K, uint32_t* ids, float* weights) {
+    if (!logits || !ids || !weights || K == 0 || K > E) return fail(ctx, INGOT_INVALID, "invalid router scores or expert count");
+    if (!all_finite(logits, E)) return fail(ctx, INGOT_INVALID, "invalid router scores or expert count");
+    CHECK_CTX(ctx);
+    if (E > 1024 || K > 64) return fail(ctx, INGOT_UNSUPPORTED, "more than 1024 experts or 64 selected");
+    float* d = nullptr;
+    HIP_TRY(ctx, hipMalloc(&d, 4ull * E + 8ull * K));
+    uint32_t* dids = reinterpret_cast<uint32_t*>(d + E);
+    float* dw = d + E + K;
+    int st = INGOT_OK;
+    if (hipMemcpy(d, logits, 4ull * E, hipMemcpyHostToDevice) != hipSuccess) st = INGOT_DEVICE;
+    if (st == INGOT_OK) {
+        launch_route(ctx->stream, d, nullptr, 1u, E, K, 0u, 1.0f, dids, dw, ctx->d_flags);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(ctx->stream) != hipSuccess ||
+            hipMemcpy(ids, dids, 4ull * K, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(weights, dw, 4ull * K, hipMemcpyDeviceToHost) != hipSuccess)
+            st = INGOT_DEVICE;
+    }
+    (void)hipFree(d);
+    if (st != INGOT_OK) return fail(ctx, st, "route: device failure");
+    return INGOT_OK;
+}
+
+int ingot_route_batch(ingot_ctx* ctx, const float* d_logits, const float* d_bias, uint32_t T, uint32_t E, uint32_t K,
+                      uint32_t routing, float scale, uint32_t* d_ids, float* d_weights) {
+    CHECK_CTX(ctx);
+    if (!d_logits || !d_ids || !d_weights || T == 0 || K == 0 || K > E || routing > 1)
+        return fail(ctx, INGOT_INVALID, "invalid router scores or expert count");
+    if (E > 1024 || K > 64) return fail(ctx, INGOT_UNSUPPORTED, "more than 1024 experts or 64 selected");
+    launch_route(ctx->stream, d_logits, d_bias, T, E, K, routing, routing ? scale : 1.0f, d_ids, d_weights,
+                 ctx->d_flags);
+    LAUNCH_CHECK(ctx);
+    return INGOT_OK;
+}
+
+// ---- Gpu::project / Gpu::dequant drop-ins ----
+int ingot_project(ingot_ctx* ctx, const ingot_matrix* m, const float* x, float* y) {
+    if (validate(m) != INGOT_OK) return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
+    if (!x || !y || m->count != 1 || !all_finite(x, m->cols)) return fail(ctx, INGOT_INVALID, "projection shape mismatch");
+    CHECK_CTX(ctx);
+    if (!supported(m->kind)) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+    DevMatrix dm;
+    float* d = nullptr;
+    int st = upload_matrix(ctx, m, &dm);
+    if (st != INGOT_OK) return st;
+    HIP_TRY(ctx, hipMalloc(&d, 4ull * (m->cols + m->rows)));
+    HIP_TRY(ctx, hipMemcpy(d, x, 4ull * m->cols, hipMemcpyHostToDevice));
+    hipLaunchKernelGGL(k_project_generic, dim3((uint32_t)((m->rows + 3) / 4), 1), dim3(256), 0, ctx->stream, dm.d,
+                       m->stride, m->kind, (uint32_t)m->cols, (uint32_t)m->rows, d, 0ull, d + m->cols);
+    LAUNCH_CHECK(ctx);
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemcpy(y, d + m->cols, 4ull * m->rows, hipMemcpyDeviceToHost));
+    (void)hipFree(d);
+    (void)hipFree(dm.d);
+    if (!all_finite(y, m->rows)) return fail(ctx, INGOT_NONFINITE, "output contains non-finite values");
+    return INGOT_OK;
+}
+
+int ingot_dequant(ingot_ctx* ctx, const ingot_matrix* m, float* out) {
+    if (validate(m) != INGOT_OK || !out) return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
+    CHECK_CTX(ctx);
+    if (!supported(m->kind)) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+    DevMatrix dm;
+    int st = upload_matrix(ctx, m, &dm);
+    if (st != INGOT_OK) return st;
+    const uint64_t nrows = m->rows * m->count, n = nrows * m->cols;
+    float* d = nullptr;
+    HIP_TRY(ctx, hipMalloc(&d, 4ull * n));
+    hipLaunchKernelGGL(k_dequant_generic, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, ctx->stream, dm.d,
+                       m->stride, m->kind, (uint32_t)m->cols, nrows, d);
+    LAUNCH_CHECK(ctx);
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemcpy(out, d, 4ull * n, hipMemcpyDeviceToHost));
+    (void)hipFree(d);
+    (void)hipFree(dm.d);
+    if (!all_finite(out, n)) return fail(ctx, INGOT_NONFINITE, "output contains non-finite values");
+    return INGOT_OK;
+}
+
+// ---- Gpu::moe drop-in (src/metal.rs:1634-1713): gate, up, SwiGLU, per-expert
+// down for the K selected experts, the same for the shared expert, the shared
+// gate projection and the combine, as one ordered sequence on the stream. ----
+int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* shared,
+              const ingot_matrix* shared_gate, const float* x, const float* weights, uint32_t K, float* out) {
+    if (!routed || !x || !weights || !out) return fail(ctx, INGOT_INVALID, "MoE input shape mismatch");
+    const bool has_shared = shared != nullptr;
+    if (has_shared != (shared_gate != nullptr)) return fail(ctx, INGOT_INVALID, "MoE input shape mismatch");
+    for (int i = 0; i < 3; ++i)
+        if (validate(&routed[i]) != INGOT_OK || (has_shared && validate(&shared[i]) != INGOT_OK))
+            return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
+    if (has_shared && validate(shared_gate) != INGOT_OK) return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
+    const uint64_t H = routed[0].cols;
+    if (!all_finite(x, H) || !all_finite(weights, K) || routed[0].count != K ||
+        (has_shared && (shared[0].cols != H || shared[0].count != 1 || shared_gate->cols != H ||
+                        shared_gate->rows != 1 || shared_gate->count != 1)))
+        return fail(ctx, INGOT_INVALID, "MoE input shape mismatch");
+    auto ffn_ok = [](const ingot_matrix* m) {
+        return m[0].cols == m[1].cols && m[0].rows == m[1].rows && m[0].count == m[1].count &&
+               m[2].cols == m[0].rows && m[2].rows == m[0].cols && m[2].count == m[0].count;
+    };
+    if (!ffn_ok(routed) || (has_shared && !ffn_ok(shared))) return fail(ctx, INGOT_INVALID, "FFN matrix shapes do not match");
+    CHECK_CTX(ctx);
+    for (int i = 0; i < 3; ++i)
+        if (!supported(routed[i].kind) || (has_shared && !supported(shared[i].kind)) ||
+            (has_shared && !supported(shared_gate->kind)))
+            return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+    const uint32_t F = (uint32_t)routed[0].rows, SF = has_shared ? (uint32_t)shared[0].rows : 0;
+    DevMatrix dr[3], ds[3], dg;
+    int st = INGOT_OK;
+    for (int i = 0; i < 3 && st == INGOT_OK; ++i) st = upload_matrix(ctx, &routed[i], &dr[i]);
+    for (int i = 0; i < 3 && st == INGOT_OK && has_shared; ++i) st = upload_matrix(ctx, &shared[i], &ds[i]);
+    if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, shared_gate, &dg);
+    if (st != INGOT_OK) return st;
+    // scratch: x[H] w[K] g,u,a [K F] y [K H] sg,su,sa [SF] sy [H] slogit [1] out [H]
+    const uint64_t n = H + K + 3ull * K * F + (uint64_t)K * H + 3ull * SF + H + 1 + H;
+    float* d = nullptr;
+    HIP_TRY(ctx, hipMalloc(&d, 4 * n));
+    float *dx = d, *dw = dx + H, *g = dw + K, *u = g + (uint64_t)K * F, *a = u + (uint64_t)K * F,
+          *y = a + (uint64_t)K * F, *sg = y + (uint64_t)K * H, *su = sg + SF, *sa = su + SF, *sy = sa + SF,
+          *sl = sy + H, *dout = sl + 1;
+    hipStream_t s = ctx->stream;
+    HIP_TRY(ctx, hipMemcpy(dx, x, 4 * H, hipMemcpyHostToDevice));
+    HIP_TRY(ctx, hipMemcpy(dw, weights, 4ull * K, hipMemcpyHostToDevice));
+    auto project = [&](const DevMatrix& m, const float* in, uint64_t instride, float* o) {
+        hipLaunchKernelGGL(k_project_generic, dim3((uint32_t)((m.rows + 3) / 4), (uint32_t)m.count), dim3(256), 0, s,
+                           m.d, m.stride, m.kind, (uint32_t)m.cols, (uint32_t)m.rows, in, instride, o);
+    };
+    project(dr[0], dx, 0, g);
+    project(dr[1], dx, 0, u);
+    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((K * F + 255) / 256)), dim3(256), 0, s, g, u, (uint64_t)K * F, a);
+    project(dr[2], a, F, y);
+    if (has_shared) {
+        project(ds[0], dx, 0, sg);
+        project(ds[1], dx, 0, su);
+        hipLaunchKernelGGL(k_swiglu, dim3((SF + 255) / 256), dim3(256), 0, s, sg, su, (uint64_t)SF, sa);
+        project(ds[2], sa, SF, sy);
+        project(dg, dx, 0, sl);
+    }
+    hipLaunchKernelGGL(k_combine_host, dim3((uint32_t)((H + 255) / 256)), dim3(256), 0, s, y,
+                       has_shared ? sy : nullptr, dw, sl, (uint32_t)H, K, dout);
+    LAUNCH_CHECK(ctx);
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    HIP_TRY(ctx, hipMemcpy(out, dout, 4 * H, hipMemcpyDeviceToHost));
+    (void)hipFree(d);
+    for (int i = 0; i < 3; ++i) {
+        (void)hipFree(dr[i].d);
+        if (ds[i].d) (void)hipFree(ds[i].d);
+    }
+    if (dg.d) (void)hipFree(dg.d);
+    if (!all_finite(out, H)) return fail(ctx, INGOT_NONFINITE, "output contains non-finite values");
+    return INGOT_OK;
+}
+
+// ---- resident layer ----
+int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* d, ingot_layer** out) {
+    if (!d || !out) return fail(ctx, INGOT_INVALID, "null layer description");
+    *out = nullptr;
+    const uint32_t H = d->hidden, E = d->experts, K = d->top_k;
+    if (H == 0 || E == 0 || K == 0 || K > E || !d->router || d->routing > 1)
+        return fail(ctx, INGOT_INVALID, "invalid layer geometry or routing");
+    for (const ingot_matrix* m : {&d->gate, &d->up, &d->down})
+        if (validate(m) != INGOT_OK) return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
+    const uint32_t F = (uint32_t)d->gate.rows;
+    if (d->gate.cols != H || d->up.cols != H || d->up.rows != F || d->down.cols != F || d->down.rows != H ||
+        d->gate.count != E || d->up.count != E || d->down.count != E)
+        return fail(ctx, INGOT_INVALID, "FFN matrix shapes do not match");
+    const bool has_shared = d->shared_gate.data != nullptr;
+    uint32_t SF = 0;
+    if (has_shared) {
+        for (const ingot_matrix* m : {&d->shared_gate, &d->shared_up, &d->shared_down})
+            if (validate(m) != INGOT_OK) return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
+        SF = (uint32_t)d->shared_gate.rows;
+        if (d->shared_gate.cols != H || d->shared_up.cols != H || d->shared_up.rows != SF ||
+            d->shared_down.cols != SF || d->shared_down.rows != H || d->shared_gate.count != 1 ||
+            d->shared_up.count != 1 || d->shared_down.count != 1)
+            return fail(ctx, INGOT_INVALID, "FFN matrix shapes do not match");
+    } else if (d->shared_gate_vec) {
+        return fail(ctx, INGOT_INVALID, "shared gate vector without a shared expert");
+    }
+    if (!all_finite(d->router, (uint64_t)E * H) || (d->router_bias && !all_finite(d->router_bias, E)) ||
+        (d->shared_gate_vec && !all_finite(d->shared_gate_vec, H)) || (d->norm_gain && !all_finite(d->norm_gain, H)))
+        return fail(ctx, INGOT_INVALID, "non-finite router, bias or gain");
+    CHECK_CTX(ctx);
+    if (E > 1024 || K > 64) return fail(ctx, INGOT_UNSUPPORTED, "more than 1024 experts or 64 selected");
+    if (H % 256 || !(H / 256 == 4 || H / 256 == 8 || H / 256 == 16))
+        return fail(ctx, INGOT_UNSUPPORTED, "hidden size must be 1024, 2048 or 4096");
+    if (F % 64 || (has_shared && SF % 64)) return fail(ctx, INGOT_UNSUPPORTED, "expert ffn size must be a multiple of 64");
+    if (d->gate.kind != d->up.kind || (has_shared && d->shared_gate.kind != d->shared_up.kind))
+        return fail(ctx, INGOT_UNSUPPORTED, "gate and up must share a format");
+    for (const ingot_matrix* m : {&d->gate, &d->down})
+        if (!supported(m->kind) || m->kind == 1) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+    if (has_shared)
+        for (const ingot_matrix* m : {&d->shared_gate, &d->shared_down})
+            if (!supported(m->kind) || m->kind == 1) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+
+    ingot_layer* L = new ingot_layer();
+    L->ctx = ctx;
+    L->H = H; L->E = E; L->K = K; L->F = F; L->SF = SF; L->routing = d->routing;
+    L->scale = d->routing ? d->route_scale : 1.0f;
+    L->limit = d->swiglu_limit;
+    L->eps = d->norm_eps;
+    L->has_shared = has_shared;
+    L->has_sgvec = d->shared_gate_vec != nullptr;
+    L->has_norm = d->norm_gain != nullptr;
+    L->has_bias = d->router_bias != nullptr;
+    int st = upload(ctx, d->router, (uint64_t)E * H, &L->router);
+    if (st == INGOT_OK && L->has_bias) st = upload(ctx, d->router_bias, E, &L->bias);
+    if (st == INGOT_OK && L->has_sgvec) st = upload(ctx, d->shared_gate_vec, H, &L->sgvec);
+    if (st == INGOT_OK && L->has_norm) st = upload(ctx, d->norm_gain, H, &L->gain);
+    if (st == INGOT_OK) st = upload_matrix(ctx, &d->gate, &L->gate);
+    if (st == INGOT_OK) st = upload_matrix(ctx, &d->up, &L->up);
+    if (st == INGOT_OK) st = upload_matrix(ctx, &d->down, &L->down);
+    if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_gate, &L->sgate);
+    if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_up, &L->sup);
+    if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_down, &L->sdown);
+    if (st != INGOT_OK) {
+        free_dev(L);
+        delete L;
+        return st;
+    }
+    *out = L;
+    return INGOT_OK;
+}
+
+int ingot_layer_clone(const ingot_layer* src, ingot_layer** out) {
+    if (!src || !out) return INGOT_INVALID;
+    ingot_ctx* ctx = src->ctx;
+    CHECK_CTX(ctx);
+    ingot_layer* L = new ingot_layer();
+    L->ctx = ctx;
+    L->H = src->H; L->E = src->E; L->K = src->K; L->F = src->F; L->SF = src->SF; L->routing = src->routing;
+    L->scale = src->scale; L->limit = src->limit; L->eps = src->eps;
+    L->has_shared = src->has_shared; L->has_sgvec = src->has_sgvec; L->has_norm = src->has_norm;
+    L->has_bias = src->has_bias;
+    auto dup = [&](const void* s, uint64_t bytes, void** dst) -> int {
+        if (!s) return INGOT_OK;
+        HIP_TRY(ctx, hipMalloc(dst, bytes));
+        HIP_TRY(ctx, hipMemcpy(*dst, s, bytes, hipMemcpyDeviceToDevice));
+        return INGOT_OK;
+    };
+    int st = dup(src->router, 4ull * src->E * src->H, (void**)&L->router);
+    if (st == INGOT_OK) st = dup(src->bias, 4ull * src->E, (void**)&L->bias);
+    if (st == INGOT_OK) st = dup(src->sgvec, 4ull * src->H, (void**)&L->sgvec);
+    if (st == INGOT_OK) st = dup(src->gain, 4ull * src->H, (void**)&L->gain);
+    const DevMatrix* sm[6] = {&src->gate, &src->up, &src->down, &src->sgate, &src->sup, &src->sdown};
+    DevMatrix* dm[6] = {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown};
+    for (int i = 0; i < 6 && st == INGOT_OK; ++i) {
+        *dm[i] = *sm[i];
+        dm[i]->d = nullptr;
+        st = dup(sm[i]->d, sm[i]->nbytes, (void**)&dm[i]->d);
+    }
+    if (st != INGOT_OK) {
+        free_dev(L);
+        delete L;
+        return st;
+    }
+    *out = L;
+    return INGOT_OK;
+}
+
+void ingot_layer_destroy(ingot_layer* L) {
+    if (!L) return;
+    (void)hipSetDevice(L->ctx->device);
+    (void)hipStreamSynchronize(L->ctx->stream);
+    free_dev(L);
+    delete L;
+}
+
+uint64_t ingot_layer_weight_bytes(const ingot_layer* L) {
+    if (!L) return 0;
+    uint64_t b = 4ull * L->E * L->H;
+    for (const DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) b += m->nbytes;
+    return b;
+}
+
+int ingot_layer_reserve(ingot_layer* L, uint32_t T) {
+    if (!L || T == 0) return INGOT_INVALID;
+    CHECK_CTX(L->ctx);
+    return reserve(L, T);
+}
+
+// Pairs up to this count take the GEMV (decode) kernels; more take the
+// dispatch + grouped MFMA GEMM (prefill) kernels.
+static const uint32_t GEMV_MAX_PAIRS = 64;
+
+int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids, float* d_weights) {
+    if (!L) return INGOT_INVALID;
+    ingot_ctx* ctx = L->ctx;
+    CHECK_CTX(ctx);
+    if (!d_x || !d_out || T == 0) return fail(ctx, INGOT_INVALID, "MoE input shape mismatch");
+    int st = reserve(L, T);
+    if (st != INGOT_OK) return st;
+    hipStream_t s = ctx->stream;
+    const uint32_t H = L->H, E = L->E, K = L->K, F = L->F, SF = L->SF, P = T * K;
+    const float* xin = L->has_norm ? L->xn : d_x;
+    const float* res = L->has_norm ? d_x : nullptr;
+    const float* sgl = L->has_sgvec ? L->sgl : nullptr;
+    for (auto& f : L->stage) f = nullptr;
+
+    // 1. router (+ RMSNorm, + shared gate logit)
+    {
+        const float *x = d_x, *W = L->router, *sgv = L->sgvec, *g = L->gain;
+        float *lg = L->logits, *sl = L->sgl, *xn = L->xn;
+        float eps = L->eps;
+        bool has_sg = L->has_sgvec;
+        uint32_t HB = H / 256;
+        L->stage[ST_ROUTER] = [=](hipStream_t ss) { launch_router(ss, HB, T, E, has_sg, x, W, sgv, g, eps, lg, sl, xn); };
+        L->stage_name[ST_ROUTER] = "k_router";
+    }
+    // 2. route
+    {
+        const float *lg = L->logits, *b = L->bias;
+        uint32_t* ids = L->ids;
+        float* w = L->wts;
+        uint32_t mode = L->routing;
+        float scale = L->scale;
+        uint32_t* flags = ctx->d_flags;
+        L->stage[ST_ROUTE] = [=](hipStream_t ss) {
+            launch_route(ss, lg, b, T, E, K, mode, scale, ids, w, flags);
+        };
+        L->stage_name[ST_ROUTE] = "k_route";
+    }
+    if (P <= GEMV_MAX_PAIRS) {
+        const DevMatrix gate = L->gate, up = L->up, down = L->down, sgate = L->sgate, sup = L->sup, sdown = L->sdown;
+        const uint32_t* ids = L->ids;
+        const float* wts = L->wts;
+        float *act = L->act, *sact = L->sact, limit = L->limit;
+        bool hs = L->has_shared;
+        L->stage[ST_GATEUP] = [=](hipStream_t ss) {
+            launch_gemv_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, P, xin, ids, K, limit, act);
+            if (hs)
+                launch_gemv_gate_up(ss, sgate.kind, sgate.d, sup.d, sgate.stride, sup.stride, SF, H, T, xin, nullptr, 1,
+                                    limit, sact);
+        };
+        L->stage_name[ST_GATEUP] = "k_gemv_gate_up";
+        DownArgs a{down.d, sdown.d, down.stride, sdown.stride, H, F, SF, act, sact, ids, wts, sgl, K, res, d_out};
+        const int ks = hs ? (int)sdown.kind : -1;
+        const uint32_t nvf = K * (F / 32) + (hs ? SF / 32 : 0);
+        const bool fuse = hs && can_fuse_shared(down.kind, ks) && (nvf + 63) / 64 <= 8;
+        if (!hs || fuse) {
+            if ((nvf + 63) / 64 > 8) return fail(ctx, INGOT_UNSUPPORTED, "decode down product too wide for one wave");
+            L->stage[ST_DOWN] = [=](hipStream_t ss) { gemv_down(ss, down.kind, ks, a, T); };
+        } else {
+            if ((K * (F / 32) + 63) / 64 > 8) return fail(ctx, INGOT_UNSUPPORTED, "decode down product too wide for one wave");
+            DownArgs ar = a;
+            ar.sdown = nullptr;
+            L->stage[ST_DOWN] = [=](hipStream_t ss) {
+                gemv_down(ss, down.kind, -1, ar, T);
+                launch_shared_down_add(ss, sdown.kind, sdown.d, sdown.stride, H, SF, T, sact, sgl, d_out);
+            };
+        }
+        L->stage_name[ST_DOWN] = "k_gemv_down";
+    } else {
+        const DevMatrix gate = L->gate, up = L->up, down = L->down, sgate = L->sgate, sup = L->sup, sdown = L->sdown;
+        const uint32_t *ids = L->ids;
+        uint32_t *counts = L->counts, *first = L->first, *tiles = L->tiles, *pairs = L->pairs, *inverse = L->inverse,
+                 *stiles = L->stiles;
+        const uint32_t cap = (P + TM - 1) / TM + E, scap = (T + TM - 1) / TM;
+        float *act = L->act, *sact = L->sact, *Y = L->Y, *Ys = L->Ys, limit = L->limit;
+        const float* wts = L->wts;
+        bool hs = L->has_shared;
+        L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
+            hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, ss, ids, P, E, TM, cap, counts, first, tiles);
+            hipLaunchKernelGGL(k_dispatch_place, dim3(E), dim3(256), 0, ss, ids, P, counts, first, pairs, inverse);
+            if (hs) hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
+        };
+        L->stage_name[ST_DISPATCH] = "k_dispatch_count";
+        L->stage[ST_GATEUP] = [=](hipStream_t ss) {
+            launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin, pairs,
+                              K, tiles, F, limit, act);
+            if (hs)
+                launch_gemm<true>(ss, sgate.kind, dim3(SF / 64, scap), sgate.d, sup.d, sgate.stride, sup.stride, SF, H,
+                                  xin, nullptr, 1, stiles, SF, limit, sact);
+        };
+        L->stage_name[ST_GATEUP] = "k_gemm<gate_up>";
+        L->stage[ST_DOWN] = [=](hipStream_t ss) {
+            launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act, nullptr,
+                               K, tiles, H, 0.f, Y);
+            if (hs)
+                launch_gemm<false>(ss, sdown.kind, dim3(H / 128, scap), sdown.d, nullptr, sdown.stride, 0, H, SF, sact,
+                                   nullptr, 1, stiles, H, 0.f, Ys);
+        };
+        L->stage_name[ST_DOWN] = "k_gemm<down>";
+        L->stage[ST_COMBINE] = [=](hipStream_t ss) {
+            uint64_t n4 = (uint64_t)T * H / 4;
+            hipLaunchKernelGGL(k_combine, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, ss, Y, hs ? Ys : nullptr,
+                               inverse, wts, sgl, res, T, H, K, d_out);
+        };
+        L->stage_name[ST_COMBINE] = "k_combine";
+    }
+    const int order[] = {ST_ROUTER, ST_ROUTE, ST_DISPATCH, ST_GATEUP, ST_DOWN, ST_COMBINE};
+    for (int i : order)
+        if (L->stage[i]) L->stage[i](s);
+    LAUNCH_CHECK(ctx);
+    if (d_ids) HIP_TRY(ctx, hipMemcpyAsync(d_ids, L->ids, 4ull * P, hipMemcpyDeviceToDevice, s));
+    if (d_weights) HIP_TRY(ctx, hipMemcpyAsync(d_weights, L->wts, 4ull * P, hipMemcpyDeviceToDevice, s));
+    return INGOT_OK;
+}
+
+int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t stage, uint32_t reps, float* ms) {
+    if (!layers || n == 0 || !ms || stage >= ST_N || reps == 0) return INGOT_INVALID;
+    ingot_ctx* ctx = layers[0]->ctx;
+    CHECK_CTX(ctx);
+    for (uint32_t i = 0; i < n; ++i)
+        if (!layers[i] || layers[i]->ctx != ctx || !layers[i]->stage[stage])
+            return fail(ctx, INGOT_INVALID, "stage did not run in the last forward");
+    hipStream_t s = ctx->stream;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    HIP_TRY(ctx, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (uint32_t i = 0; i < reps; ++i) layers[i % n]->stage[stage](s);
+    hipError_t le = hipGetLastError();
+    hipError_t ce = hipStreamEndCapture(s, &graph);
+    if (le != hipSuccess || ce != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return fail(ctx, INGOT_DEVICE, std::string("stage capture: ") + hipGetErrorString(le != hipSuccess ? le : ce));
+    }
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    float t = 0;
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e == hipSuccess) e = hipGraphLaunch(exec, s);  // warm-up
+    if (e == hipSuccess) e = hipEventRecord(a, s);
+    if (e == hipSuccess) e = hipGraphLaunch(exec, s);
+    if (e == hipSuccess) e = hipEventRecord(b, s);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(ctx, INGOT_DEVICE, std::string("stage timing: ") + hipGetErrorString(e));
+    *ms = t / reps;
+    return INGOT_OK;
+}
+
+int ingot_layer_time_stage(ingot_layer* L, uint32_t stage, uint32_t reps, float* ms) {
+    return ingot_layers_time_stage(&L, 1, stage, reps, ms);
+}
+
+const char* ingot_layer_stage_kernel(const ingot_layer* L, uint32_t stage) {
+    if (!L || stage >= ST_N || !L->stage[stage]) return "";
+    return L->stage_name[stage];
+}
+
+// ---- graphs ----
+int ingot_graph_begin(ingot_ctx* ctx) {
+    CHECK_CTX(ctx);
+    HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return INGOT_OK;
+}
+
+int ingot_graph_end(ingot_ctx* ctx, ingot_graph** out) {
+    CHECK_CTX(ctx);
+    if (!out) return INGOT_INVALID;
+    ingot_graph* g = new ingot_graph();
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+    if (e != hipSuccess) {
+        delete g;
+        return fail(ctx, INGOT_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    }
+    e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g->graph);
+        delete g;
+        return fail(ctx, INGOT_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
+    *out = g;
+    return INGOT_OK;
+}
+
+int ingot_graph_launch(ingot_ctx* ctx, ingot_graph* g) {
+    CHECK_CTX(ctx);
+    if (!g) return INGOT_INVALID;
+    HIP_TRY(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    return INGOT_OK;
+}
+
+void ingot_graph_destroy(ingot_graph* g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
+int ingot_graph_time(ingot_ctx* ctx, ingot_graph* g, uint32_t launches, float* ms) {
+    CHECK_CTX(ctx);
+    if (!g || !ms || launches == 0) return INGOT_INVALID;
+    hipEvent_t a, b;
+    HIP_TRY(ctx, hipEventCreate(&a));
+    HIP_TRY(ctx, hipEventCreate(&b));
+    HIP_TRY(ctx, hipEventRecord(a, ctx->stream));
+    for (uint32_t i = 0; i < launches; ++i) HIP_TRY(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    HIP_TRY(ctx, hipEventRecord(b, ctx->stream));
+    HIP_TRY(ctx, hipEventSynchronize(b));
+    HIP_TRY(ctx, hipEventElapsedTime(ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return INGOT_OK;
+}
+
+}  // extern "C"

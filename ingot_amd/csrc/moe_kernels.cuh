@@ -1,0 +1,715 @@
+// HIP kernels of the MoE-layer hot path for gfx950 (wave64, MFMA, 160 KB LDS).
+//
+// Decode (few pairs) and prefill (many pairs) take different kernels:
+//   router   k_router        logits = W_r x (fixed fp32 order), optional fused
+//                            RMSNorm, optional shared-expert gate logit
+//   route    k_route         per-token top-K on 64-bit (orderable value, ~id)
+//                            keys; softmax or sigmoid+bias weights
+//   decode   k_gemv_gate_up  act[p] = SwiGLU(G_e x_t, U_e x_t) for each pair
+//            k_gemv_down     out[t] = sum_k w_k D_e act[p] (+ shared, + residual)
+//   prefill  k_dispatch_count / k_dispatch_place   stable expert grouping
+//            k_gemm<GATEUP>  MFMA f32 grouped GEMM, dequantised weights in LDS
+//            k_combine       out[t] = sum_k w_k Y[inverse[p]] (+ shared, + residual)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "det_math.h"
+#include "formats.cuh"
+
+namespace ingot {
+
+constexpr int WAVE = 64;
+constexpr uint32_t FLAG_NONFINITE = 1u;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ float swiglu(float g, float u, float limit) {
+    if (limit > 0.f) {
+        g = fminf(g, limit);
+        u = fminf(fmaxf(u, -limit), limit);
+    }
+    return g / (1.0f + expf(-g)) * u;
+}
+
+// ---------------------------------------------------------------- router
+// One wave per (group of TOK tokens, group of experts). Lane l holds the
+// columns 4l + 256i + c (i < HB = H/256, c < 4) of each of its tokens, which
+// is the slot layout of the fixed reduction order (det_math.h): each logit is
+// the lane's fused multiply-add chain followed by the xor butterfly, so it is
+// bit-identical to the CPU's ingot_router_partial + ingot_butterfly64.
+// With a norm gain the wave first computes RMSNorm of its tokens in the same
+// order (sum of squares over the slots, butterfly, 1/sqrt(ss/H + eps), (x*r)*g)
+// and writes the normalised rows (block (.., 0), wave 0 only).
+// Expert index E (when sgvec != NULL) is the shared-expert gate vector: its
+// product goes to sgl[t].
+template <int TOK, int HB>
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ W,
+                                                const float* __restrict__ sgvec, const float* __restrict__ gain,
+                                                float eps, uint32_t T, uint32_t E, uint32_t epw,
+                                                float* __restrict__ logits, float* __restrict__ sgl,
+                                                float* __restrict__ xn) {
+    INGOT_NO_CONTRACT
+    constexpr uint32_t H = 256u * HB;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t0 = blockIdx.x * TOK;
+    float xr[TOK][HB * 4];
+#pragma unroll
+    for (int t = 0; t < TOK; ++t) {
+        uint32_t tt = min(t0 + t, T - 1);
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            float4 v = *reinterpret_cast<const float4*>(x + (uint64_t)tt * H + 4u * lane + 256u * i);
+            xr[t][4 * i] = v.x; xr[t][4 * i + 1] = v.y; xr[t][4 * i + 2] = v.z; xr[t][4 * i + 3] = v.w;
+        }
+    }
+    if (gain) {
+        float g[HB * 4];
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            float4 v = *reinterpret_cast<const float4*>(gain + 4u * lane + 256u * i);
+            g[4 * i] = v.x; g[4 * i + 1] = v.y; g[4 * i + 2] = v.z; g[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < HB * 4; ++j) ss = __builtin_fmaf(xr[t][j], xr[t][j], ss);
+            ss = wave_sum(ss);
+            float mean = ss / (float)H;
+            float r = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+            for (int j = 0; j < HB * 4; ++j) xr[t][j] = (xr[t][j] * r) * g[j];
+        }
+        if (blockIdx.y == 0 && wave == 0) {
+#pragma unroll
+            for (int t = 0; t < TOK; ++t) {
+                if (t0 + t >= T) break;
+#pragma unroll
+                for (int i = 0; i < HB; ++i)
+                    *reinterpret_cast<float4*>(xn + (uint64_t)(t0 + t) * H + 4u * lane + 256u * i) =
+                        make_float4(xr[t][4 * i], xr[t][4 * i + 1], xr[t][4 * i + 2], xr[t][4 * i + 3]);
+            }
+        }
+    }
+    const uint32_t rows = E + (sgvec ? 1u : 0u);
+    const uint32_t e0 = (blockIdx.y * 4u + wave) * epw;
+    for (uint32_t k = 0; k < epw; ++k) {
+        uint32_t e = e0 + k;
+        if (e >= rows) break;
+        const float* wr = e < E ? W + (uint64_t)e * H : sgvec;
+        float wv[HB * 4];
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            float4 v = *reinterpret_cast<const float4*>(wr + 4u * lane + 256u * i);
+            wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < HB * 4; ++j) acc = __builtin_fmaf(wv[j], xr[t][j], acc);
+            acc = wave_sum(acc);
+            if (lane == 0 && t0 + t < T) {
+                if (e < E) logits[(uint64_t)(t0 + t) * E + e] = acc;
+                else sgl[t0 + t] = acc;
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------- route
+// One wave per token, E <= 64 * NE. Softmax mode (src/lib.rs:43-60):
+// selection and weights on l (+ bias when given), w_k = exp(v_k - v_top) /
+// sum. Sigmoid mode (kernels/glm.metal:81-98): selection on sigmoid(l) + bias,
+// w_k = sigmoid(l_k) / sum * scale. Keys (orderable(v) << 32 | ~id) make the
+// wave maximum unique and resolve ties toward the lower id, exactly as a
+// stable descending sort with f32::total_cmp does (+0 above -0). Everything
+// stays in registers: the winner's weight input is fetched from its owning
+// lane, lane k keeps the k-th selection, and lane 0 sums the weights in
+// selection order. A non-finite logit or bias raises FLAG_NONFINITE; the ids
+// written are still valid expert indices. K <= 64.
+template <int NE>
+__global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, const float* __restrict__ bias,
+                                               uint32_t T, uint32_t E, uint32_t K, uint32_t sigmoid_mode,
+                                               float scale, uint32_t* __restrict__ ids, float* __restrict__ wts,
+                                               uint32_t* __restrict__ flags) {
+    INGOT_NO_CONTRACT
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const float* l = logits + (uint64_t)t * E;
+    uint64_t key[NE];
+    float wv[NE];  // weight input of each candidate: l + bias (softmax) or sigmoid(l)
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        uint32_t e = lane + 64u * j;
+        key[j] = 0;
+        wv[j] = 0.f;
+        if (e < E) {
+            float v = l[e];
+            float b = bias ? bias[e] : 0.f;
+            bad |= !isfinite(v) || !isfinite(b);
+            float s;
+            if (sigmoid_mode) {
+                wv[j] = ingot_det_sigmoid(v);
+                s = bias ? wv[j] + b : wv[j];
+            } else {
+                s = bias ? v + b : v;
+                wv[j] = s;
+            }
+            key[j] = ingot_select_key(s, e);
+        }
+    }
+    if (__any(bad) && lane == 0) atomicOr(flags, FLAG_NONFINITE);
+    uint32_t my_id = 0;
+    float my_v = 0.f;
+    for (uint32_t k = 0; k < K; ++k) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) best = key[j] > best ? key[j] : best;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            uint64_t o = shfl_xor_u64(best, m);
+            best = o > best ? o : best;
+        }
+        const uint32_t id = 0xffffffffu - (uint32_t)best;
+        const uint32_t owner = id & 63u, slot = id >> 6;
+        float mine = 0.f;
+#pragma unroll
+        for (int j = 0; j < NE; ++j)
+            if ((uint32_t)j == slot) {
+                mine = wv[j];
+                if (lane == owner) key[j] = 0;
+            }
+        const float v = __shfl(mine, (int)owner);
+        if (lane == k) {
+            my_id = id;
+            my_v = v;
+        }
+    }
+    // lane k < K: weight numerator of selection k
+    const float top = __shfl(my_v, 0);
+    const float num = sigmoid_mode ? my_v : ingot_det_expf(my_v - top);
+    float total = 0.f;
+    for (uint32_t k = 0; k < K; ++k) total += __shfl(num, (int)k);
+    if (lane < K) {
+        ids[(uint64_t)t * K + lane] = my_id;
+        wts[(uint64_t)t * K + lane] = sigmoid_mode ? num / total * scale : num / total;
+    }
+}
+
+// ----------------------------------------------------------- decode: gate/up
+// grid (ceil(F / (4*RPW)), pairs); a wave owns RPW rows of one pair. Lane l
+// owns chunks l + 64j (j < CPL) of the H columns: their 32 inputs stay in
+// registers for all the wave's rows, and each row costs the lane one header
+// and one 16-byte nibble load per chunk (Q4_K). ids == NULL: shared-expert
+// mode (expert 0, token = pair).
+template <int KIND, int CPL, int RPW>
+__global__ __launch_bounds__(256) void k_gemv_gate_up(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+                                                      uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
+                                                      const float* __restrict__ x, const uint32_t* __restrict__ ids,
+                                                      uint32_t K, float limit, float* __restrict__ act) {
+    using Fm = Fmt<KIND>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t p = blockIdx.y;
+    const uint32_t e = ids ? ids[p] : 0u, t = ids ? p / K : p;
+    const uint32_t nch = H / 32u;
+    float xv[CPL][32], xs0[CPL], xs1[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        uint32_t c = lane + 64u * j;
+        xs0[j] = xs1[j] = 0.f;
+        if (c < nch) {
+            Fm::load_x(x + (uint64_t)t * H, c, xv[j]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                xs0[j] += xv[j][i];
+                xs1[j] += xv[j][16 + i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xv[j][i] = 0.f;
+        }
+    }
+    const uint32_t r0 = (blockIdx.x * 4u + wave) * RPW;
+    float gs[RPW], us[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        gs[i] = us[i] = 0.f;
+        uint32_t r = min(r0 + i, F - 1);
+        const uint8_t* grow = gate + ((uint64_t)e * F + r) * gstride;
+        const uint8_t* urow = up + ((uint64_t)e * F + r) * ustride;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            uint32_t c = lane + 64u * j;
+            if (c < nch) {
+                gs[i] += Fm::dot(grow, c, xv[j], xs0[j], xs1[j]);
+                us[i] += Fm::dot(urow, c, xv[j], xs0[j], xs1[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        float g = wave_sum(gs[i]), u = wave_sum(us[i]);
+        if (lane == (uint32_t)i && r0 + i < F) act[(uint64_t)p * F + r0 + i] = swiglu(g, u, limit);
+    }
+}
+
+// ------------------------------------------------------ decode: down+combine
+// grid (ceil(H / (4*RPW)), T); a wave owns RPW output rows of one token. The
+// token's K routed pairs (and the shared expert, if any) form one virtual row
+// of K*F/32 (+SF/32) chunks spread over the lanes (VPL per lane); each lane
+// keeps its chunks' activations in registers, pre-multiplied by the pair's
+// routing weight, so the wave sum is directly sum_k w_k (D_e act_k)[i].
+// The shared expert (format KS, KS < 0: none here) is scaled by
+// sigmoid(sgl[t]) when sgl != NULL, else by 1. res != NULL adds a residual.
+template <int KD, int KS, int VPL, int RPW>
+__global__ __launch_bounds__(256) void k_gemv_down(const uint8_t* __restrict__ down, uint64_t dstride,
+                                                   const uint8_t* __restrict__ sdown, uint64_t sdstride,
+                                                   uint32_t H, uint32_t F, uint32_t SF,
+                                                   const float* __restrict__ act, const float* __restrict__ sact,
+                                                   const uint32_t* __restrict__ ids, const float* __restrict__ wts,
+                                                   const float* __restrict__ sgl, uint32_t K,
+                                                   const float* __restrict__ res, float* __restrict__ out) {
+    using Fd = Fmt<KD>;
+    using Fs = Fmt<(KS < 0 ? KD : KS)>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
+    const uint32_t nv = K * nchF + nchS;
+    float xv[VPL][32], xs0[VPL], xs1[VPL];
+    const uint8_t* base[VPL];
+    uint32_t cc[VPL];
+    bool isS[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        uint32_t v = lane + 64u * j;
+        base[j] = nullptr;
+        cc[j] = 0;
+        isS[j] = false;
+        float w = 0.f;
+        xs0[j] = xs1[j] = 0.f;
+        if (v < K * nchF) {
+            uint32_t k = v / nchF, c = v % nchF, p = t * K + k;
+            base[j] = down + (uint64_t)ids[p] * H * dstride;
+            cc[j] = c;
+            w = wts[p];
+            Fd::load_x(act + (uint64_t)p * F, c, xv[j]);
+        } else if (v < nv) {
+            uint32_t c = v - K * nchF;
+            base[j] = sdown;
+            cc[j] = c;
+            isS[j] = true;
+            w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
+            Fs::load_x(sact + (uint64_t)t * SF, c, xv[j]);
+        }
+        if (base[j]) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xv[j][i] *= w;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                xs0[j] += xv[j][i];
+                xs1[j] += xv[j][16 + i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xv[j][i] = 0.f;
+        }
+    }
+    const uint32_t r0 = (blockIdx.x * 4u + wave) * RPW;
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        acc[i] = 0.f;
+        uint32_t r = min(r0 + i, H - 1);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            if (!base[j]) continue;
+            if (KS >= 0 && isS[j]) acc[i] += Fs::dot(base[j] + (uint64_t)r * sdstride, cc[j], xv[j], xs0[j], xs1[j]);
+            else acc[i] += Fd::dot(base[j] + (uint64_t)r * dstride, cc[j], xv[j], xs0[j], xs1[j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        float s = wave_sum(acc[i]);
+        uint32_t r = r0 + i;
+        if (lane == (uint32_t)i && r < H) {
+            if (res) s += res[(uint64_t)t * H + r];
+            out[(uint64_t)t * H + r] = s;
+        }
+    }
+}
+
+// Adds a separately computed shared-expert down product to out (used when the
+// shared down format has no fused instantiation): out[t] += s * S_down sact[t].
+template <int KS, int CPL>
+__global__ __launch_bounds__(256) void k_gemv_shared_down_add(const uint8_t* __restrict__ sdown, uint64_t sdstride,
+                                                              uint32_t H, uint32_t SF, const float* __restrict__ sact,
+                                                              const float* __restrict__ sgl, float* __restrict__ out) {
+    using Fs = Fmt<KS>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y, r = blockIdx.x * 4u + wave;
+    if (r >= H) return;
+    const uint32_t nch = SF / 32u;
+    float w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        uint32_t c = lane + 64u * j;
+        if (c >= nch) continue;
+        float xv[32], s0 = 0.f, s1 = 0.f;
+        Fs::load_x(sact + (uint64_t)t * SF, c, xv);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xv[i] *= w;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            s0 += xv[i];
+            s1 += xv[16 + i];
+        }
+        acc += Fs::dot(sdown + (uint64_t)r * sdstride, c, xv, s0, s1);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) out[(uint64_t)t * H + r] += acc;
+}
+
+// ------------------------------------------------------- prefill: dispatch
+// Block-wide exclusive scan of one value per thread (blockDim 1024 = 16 waves).
+__device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        uint32_t o = __shfl_up(inc, d);
+        if (lane >= (uint32_t)d) inc += o;
+    }
+    if (lane == 63) wsum[wave] = inc;
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t s = lane < 16 ? wsum[lane] : 0u, si = s;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            uint32_t o = __shfl_up(si, d);
+            if (lane >= (uint32_t)d) si += o;
+        }
+        if (lane < 16) wsum[16 + lane] = si - s;
+        if (lane == 15) *total = si;
+    }
+    __syncthreads();
+    return inc - v + wsum[16 + wave];
+}
+
+// One block of 1024 threads, E <= 1024. Counts pairs per expert, writes
+// counts[E], first[E] (exclusive scan: experts ascending) and the tile list:
+// for each expert ceil(n/TM) tiles {expert, first pair of the tile, n in tile,
+// 0}, experts ascending, padded with zero tiles to cap (the layout of
+// kernels/prefill.metal:7-23 with TM-pair tiles).
+__global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
+                                                         uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
+                                                         uint32_t* __restrict__ first, uint32_t* __restrict__ tiles) {
+    __shared__ uint32_t cnt[1024];
+    __shared__ uint32_t wsum[32];
+    __shared__ uint32_t tot[2];
+    const uint32_t tid = threadIdx.x;
+    cnt[tid] = 0;
+    __syncthreads();
+    for (uint32_t p = tid; p < P; p += 1024u) atomicAdd(&cnt[ids[p]], 1u);
+    __syncthreads();
+    uint32_t n = tid < E ? cnt[tid] : 0u;
+    uint32_t nt = (n + TM - 1) / TM;
+    uint32_t f = block_exclusive_scan_1024(n, wsum, &tot[0]);
+    __syncthreads();
+    uint32_t t0 = block_exclusive_scan_1024(nt, wsum, &tot[1]);
+    if (tid < E) {
+        counts[tid] = n;
+        first[tid] = f;
+        for (uint32_t k = 0; k < nt && t0 + k < cap; ++k) {
+            uint32_t* tl = tiles + 4u * (t0 + k);
+            tl[0] = tid;
+            tl[1] = f + k * TM;
+            tl[2] = min(TM, n - k * TM);
+            tl[3] = 0;
+        }
+    }
+    __syncthreads();
+    for (uint32_t t = tot[1] + tid; t < cap; t += 1024u) {
+        uint32_t* tl = tiles + 4u * t;
+        tl[0] = tl[1] = tl[2] = tl[3] = 0;
+    }
+}
+
+// One block (256 threads) per expert: pair indices of the expert in ascending
+// order at pairs[first[e]...], and each pair's packed position in inverse[p]
+// (kernels/prefill.metal:25-38).
+__global__ __launch_bounds__(256) void k_dispatch_place(const uint32_t* __restrict__ ids, uint32_t P,
+                                                        const uint32_t* __restrict__ counts,
+                                                        const uint32_t* __restrict__ first, uint32_t* __restrict__ pairs,
+                                                        uint32_t* __restrict__ inverse) {
+    const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    if (counts[e] == 0) return;
+    __shared__ uint32_t ws[4];
+    const uint32_t chunk = (P + 255u) / 256u, s = min(P, tid * chunk), end = min(P, s + chunk);
+    uint32_t mine = 0;
+    for (uint32_t i = s; i < end; ++i) mine += ids[i] == e;
+    uint32_t inc = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        uint32_t o = __shfl_up(inc, d);
+        if (lane >= (uint32_t)d) inc += o;
+    }
+    if (lane == 63) ws[wave] = inc;
+    __syncthreads();
+    uint32_t before = inc - mine;
+    for (uint32_t w = 0; w < wave; ++w) before += ws[w];
+    uint32_t at = first[e] + before;
+    for (uint32_t i = s; i < end; ++i)
+        if (ids[i] == e) {
+            inverse[i] = at;
+            pairs[at++] = i;
+        }
+}
+
+// ---------------------------------------------------- prefill: grouped GEMM
+// One block (256 threads, 4 waves) per (row tile, token tile). A token tile
+// {expert, first, n} covers packed positions first..first+n-1 (n <= 64).
+//   GATEUP: A = input rows x[token(pairs[q])] (H cols), B = 64 gate rows and
+//           the same 64 up rows of the expert; out act[q][row] = SwiGLU.
+//   !GATEUP: A = act[q] (F cols), B = 128 down rows; out Y[q][row].
+// The K dimension runs in 64-column slabs: the block stages A (64 x 64 fp32)
+// and B (128 rows x 64, dequantised from two 32-value chunks per row) in LDS,
+// with the next slab's global loads issued before the current slab's MFMAs.
+// Each wave computes a 64 x 32 output block (4 x 2 tiles of
+// v_mfma_f32_16x16x4f32). The MFMA k-index of lane i at step ks is
+// 4*(i/16)+ks inside a 16-column group, so each lane fetches 4 consecutive
+// columns of A and B with one 128-bit LDS read.
+constexpr uint32_t TM = 64, LDS_STRIDE = 68;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int KIND, bool GATEUP>
+__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+                                              uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
+                                              uint32_t kdim, const float* __restrict__ a_src,
+                                              const uint32_t* __restrict__ pairs, uint32_t K,
+                                              const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
+                                              float* __restrict__ out) {
+    using Fm = Fmt<KIND>;
+    __shared__ float As[TM * LDS_STRIDE];
+    __shared__ float Bs[128 * LDS_STRIDE];
+    const uint32_t* tile = tiles + 4u * blockIdx.y;
+    const uint32_t n = tile[2];
+    if (n == 0) return;
+    const uint32_t e = tile[0], q0 = tile[1];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    // Output rows of this block: GATEUP 64 (gate and up), else 128.
+    const uint32_t row0 = blockIdx.x * (GATEUP ? 64u : 128u);
+
+    // A loader: 4 float4 per thread; element idx = tid + 256 i -> row idx/16, col4 idx%16.
+    const float* arow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t m = (tid + 256u * i) >> 4;
+        arow[i] = nullptr;
+        if (m < n) {
+            uint32_t q = q0 + m;
+            uint64_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
+            arow[i] = a_src + r * kdim;
+        }
+    }
+    const uint32_t acol = 4u * (tid & 15u);
+    // B loader: thread -> (B row brow = tid/2, chunk half h = tid%2).
+    const uint32_t brow = tid >> 1, bh = tid & 1u;
+    const uint8_t* bptr;
+    if (GATEUP) {
+        const uint8_t* base = brow < 64 ? w0 : w1;
+        uint64_t st = brow < 64 ? stride0 : stride1;
+        uint32_t r = row0 + (brow & 63u);
+        bptr = base + ((uint64_t)e * rows_per_expert + r) * st;
+    } else {
+        bptr = w0 + ((uint64_t)e * rows_per_expert + row0 + brow) * stride0;
+    }
+
+    floatx4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    float4 ar[4];
+    typename Fm::Raw br;
+    auto load = [&](uint32_t s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ar[i] = arow[i] ? *reinterpret_cast<const float4*>(arow[i] + 64u * s + acol) : make_float4(0.f, 0.f, 0.f, 0.f);
+        br = Fm::load_raw(bptr, 2u * s + bh);
+    };
+    const uint32_t slabs = kdim / 64u;
+    load(0);
+    for (uint32_t s = 0; s < slabs; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t m = (tid + 256u * i) >> 4;
+            *reinterpret_cast<float4*>(&As[m * LDS_STRIDE + acol]) = ar[i];
+        }
+        {
+            float wv[32];
+            Fm::dequant_raw(br, 2u * s + bh, wv);
+            float* dst = &Bs[brow * LDS_STRIDE];
+            // Chunk value i -> slab column: Fm::col(chunk, i) - 64 s.
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                uint32_t cl = Fm::col(2u * s + bh, i) - 64u * s;
+                *reinterpret_cast<float4*>(dst + cl) = make_float4(wv[i], wv[i + 1], wv[i + 2], wv[i + 3]);
+            }
+        }
+        __syncthreads();
+        if (s + 1 < slabs) load(s + 1);
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4; ++kk) {
+            const uint32_t kc = kk * 16u + 4u * (lane >> 4);
+            float4 a[4], b[2];
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+                a[mb] = *reinterpret_cast<const float4*>(&As[(mb * 16u + (lane & 15u)) * LDS_STRIDE + kc]);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                // GATEUP: nb 0 = gate rows 16w.., nb 1 = up rows 64+16w..; else rows 32w + 16nb..
+                uint32_t br_ = GATEUP ? (nb * 64u + 16u * wave) : (32u * wave + 16u * nb);
+                b[nb] = *reinterpret_cast<const float4*>(&Bs[(br_ + (lane & 15u)) * LDS_STRIDE + kc]);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        float av = ks == 0 ? a[mb].x : ks == 1 ? a[mb].y : ks == 2 ? a[mb].z : a[mb].w;
+                        float bv = ks == 0 ? b[nb].x : ks == 1 ? b[nb].y : ks == 2 ? b[nb].z : b[nb].w;
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[mb][nb], 0, 0, 0);
+                    }
+        }
+        __syncthreads();
+    }
+    // Epilogue: lane holds D[m = 4*(lane/16) + j][n = lane%16] of each tile.
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t m = mb * 16u + 4u * (lane >> 4) + j;
+            if (m >= n) continue;
+            uint64_t q = q0 + m;
+            if (GATEUP) {
+                uint32_t r = row0 + 16u * wave + (lane & 15u);
+                out[q * ldo + r] = swiglu(acc[mb][0][j], acc[mb][1][j], limit);
+            } else {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    uint32_t r = row0 + 32u * wave + 16u * nb + (lane & 15u);
+                    out[q * ldo + r] = acc[mb][nb][j];
+                }
+            }
+        }
+}
+
+// Dense token tiles for the shared expert: tile t = {0, 64 t, min(64, T - 64 t), 0}.
+__global__ void k_dense_tiles(uint32_t T, uint32_t cap, uint32_t* __restrict__ tiles) {
+    uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= cap) return;
+    uint32_t first = t * TM;
+    tiles[4 * t] = 0;
+    tiles[4 * t + 1] = first < T ? first : 0;
+    tiles[4 * t + 2] = first < T ? min(TM, T - first) : 0;
+    tiles[4 * t + 3] = 0;
+}
+
+// ------------------------------------------------------- prefill: combine
+// out[t][i] = sum_k w[t,k] Y[inverse[t*K+k]][i] in route order (kernels/prefill.metal:39),
+// + sigmoid(sgl[t]) (or 1) * Ys[t][i] for a shared expert, + res[t][i].
+__global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, const float* __restrict__ Ys,
+                                                 const uint32_t* __restrict__ inverse, const float* __restrict__ wts,
+                                                 const float* __restrict__ sgl, const float* __restrict__ res,
+                                                 uint32_t T, uint32_t H, uint32_t K, float* __restrict__ out) {
+    const uint64_t i4 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t per = H / 4u;
+    if (i4 >= (uint64_t)T * per) return;
+    const uint32_t t = (uint32_t)(i4 / per), c = (uint32_t)(i4 % per) * 4u;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t k = 0; k < K; ++k) {
+        uint32_t p = t * K + k;
+        float w = wts[p];
+        float4 y = *reinterpret_cast<const float4*>(Y + (uint64_t)inverse[p] * H + c);
+        s.x += w * y.x; s.y += w * y.y; s.z += w * y.z; s.w += w * y.w;
+    }
+    if (Ys) {
+        float w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
+        float4 y = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
+        s.x += y.x * w; s.y += y.y * w; s.z += y.z * w; s.w += y.w * w;
+    }
+    if (res) {
+        float4 r = *reinterpret_cast<const float4*>(res + (uint64_t)t * H + c);
+        s.x += r.x; s.y += r.y; s.z += r.z; s.w += r.w;
+    }
+    *reinterpret_cast<float4*>(out + (uint64_t)t * H + c) = s;
+}
+
+// ---------------------------------------------- generic (drop-in) kernels
+// y[g][r] = sum_j W_g[r][j] x_g[j], one wave per (row, matrix g); scalar
+// decode of any supported kind. The input of matrix g starts at x + g*xstride.
+__global__ __launch_bounds__(256) void k_project_generic(const uint8_t* __restrict__ w, uint64_t stride, uint32_t kind,
+                                                         uint32_t cols, uint32_t rows, const float* __restrict__ x,
+                                                         uint64_t xstride, float* __restrict__ y) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6), g = blockIdx.y;
+    if (r >= rows) return;
+    const uint8_t* row = w + ((uint64_t)g * rows + r) * stride;
+    const float* xv = x + (uint64_t)g * xstride;
+    float s = 0.f;
+    for (uint32_t j = lane; j < cols; j += 64u) s += dequant_value(row, kind, j) * xv[j];
+    s = wave_sum(s);
+    if (lane == 0) y[(uint64_t)g * rows + r] = s;
+}
+
+__global__ void k_dequant_generic(const uint8_t* __restrict__ w, uint64_t stride, uint32_t kind, uint32_t cols,
+                                  uint64_t nrows, float* __restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nrows * cols) return;
+    const uint64_t r = i / cols;
+    out[i] = dequant_value(w + r * stride, kind, (uint32_t)(i % cols));
+}
+
+__global__ void k_swiglu(const float* __restrict__ g, const float* __restrict__ u, uint64_t n, float* __restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = swiglu(g[i], u[i], 0.f);
+}
+
+// Gpu::moe combine (kernels/moe.metal:412-422): out[i] = sum_e routed[e][i] w[e]
+// + shared[i] sigmoid(shared_logit) (shared may be NULL).
+__global__ void k_combine_host(const float* __restrict__ routed, const float* __restrict__ shared,
+                               const float* __restrict__ w, const float* __restrict__ slogit, uint32_t H, uint32_t K,
+                               float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    float s = 0.f;
+    for (uint32_t e = 0; e < K; ++e) s += routed[(uint64_t)e * H + i] * w[e];
+    if (shared) s += shared[i] / (1.0f + expf(-slogit[0]));
+    out[i] = s;
+}
+
+// Non-finite scan of a device buffer: sets FLAG_NONFINITE in flags.
+__global__ void k_check_finite(const float* __restrict__ v, uint64_t n, uint32_t* __restrict__ flags) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool bad = i < n && !isfinite(v[i]);
+    if (__any(bad) && (threadIdx.x & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
+}
+
+}  // namespace ingot
