@@ -82,6 +82,22 @@ def time_graph(gpu, layers, dx, T, dout, steps, warmup):
     return ms
 
 
+def time_stages(layers, dx, T, dout, reps):
+    """Mean us per launch of every stage that ran in the layers' last forward."""
+    from ingot_amd.moe import (STAGE_COMBINE, STAGE_DISPATCH, STAGE_DOWN, STAGE_GATEUP, STAGE_ROUTE, STAGE_ROUTER,
+                               time_stage)
+    for l in layers:
+        l.forward(dx, T, dout)
+    out = {}
+    for name, st in (("router", STAGE_ROUTER), ("route", STAGE_ROUTE), ("dispatch", STAGE_DISPATCH),
+                     ("gate_up", STAGE_GATEUP), ("down", STAGE_DOWN), ("combine", STAGE_COMBINE)):
+        kernel = layers[0].stage_kernel(st)
+        if kernel:
+            out[name] = {"us": 1e3 * time_stage(layers, st, reps), "kernel": kernel}
+    layers[0].gpu.synchronize()
+    return out
+
+
 def cpu_baseline(spec, x, budget_s, label):
     from oracle import pyoracle as O
     cores = len(os.sched_getaffinity(0))
@@ -116,8 +132,7 @@ def main():
         sys.exit(2)
 
     from ingot_amd import configs as CF
-    from ingot_amd.moe import (STAGE_DISPATCH, STAGE_DOWN, STAGE_GATEUP, STAGE_ROUTE, STAGE_ROUTER, STAGE_COMBINE,
-                               Gpu, MoeLayer, time_stage)
+    from ingot_amd.moe import Gpu, MoeLayer
 
     gpu = Gpu(0)
     log(f"device: {gpu.name()}")
@@ -140,13 +155,7 @@ def main():
     ms_step = ms / args.steps
     log(f"prefill: {ms_step * 1e3:.1f} us/step over {args.steps} steps, {args.copies} copies")
     work = prefill_stage_work(spec1, ids, T)
-    stages = {}
-    for name, st in (("router", STAGE_ROUTER), ("route", STAGE_ROUTE), ("dispatch", STAGE_DISPATCH),
-                     ("gate_up", STAGE_GATEUP), ("down", STAGE_DOWN), ("combine", STAGE_COMBINE)):
-        for l in layers:
-            l.forward(dx, T, dout)
-        stages[name] = {"us": 1e3 * time_stage(layers, st, 40), "kernel": base.stage_kernel(st)}
-    gpu.synchronize()
+    stages = time_stages(layers, dx, T, dout, 40)
     log("prefill stages (us): " + ", ".join(f"{k} {v['us']:.1f}" for k, v in stages.items()))
     dom = max(("gate_up", "down"), key=lambda k: stages[k]["us"])
     dflops = work[dom]["flops"]
@@ -165,13 +174,7 @@ def main():
     d_bytes = 4 * 128 * 2048 + 8 * spec0.weight_bytes_per_expert() + 2 * 4 * 2048
     gu_bytes = 8 * (spec0.gate.rows * spec0.gate.stride + spec0.up.rows * spec0.up.stride) + 4 * 2048
     dn_bytes = 8 * spec0.down.rows * spec0.down.stride + 8 * 4 * 768 + 4 * 2048
-    dstages = {}
-    for name, st in (("router", STAGE_ROUTER), ("route", STAGE_ROUTE), ("gate_up", STAGE_GATEUP),
-                     ("down", STAGE_DOWN)):
-        for l in dl:
-            l.forward(dx0, 1, dout0)
-        dstages[name] = {"us": 1e3 * time_stage(dl, st, 256), "kernel": d0.stage_kernel(st)}
-    gpu.synchronize()
+    dstages = time_stages(dl, dx0, 1, dout0, 256)
     log(f"decode: {dms_step * 1e3:.2f} us/step; stages (us): " +
         ", ".join(f"{k} {v['us']:.2f}" for k, v in dstages.items()))
     decode = {
@@ -187,8 +190,7 @@ def main():
                         "achieved_GBs": gu_bytes / (dstages["gate_up"]["us"] * 1e-6) / 1e9},
             "down": {"kernel": dstages["down"]["kernel"], "us": dstages["down"]["us"], "bytes": dn_bytes,
                      "achieved_GBs": dn_bytes / (dstages["down"]["us"] * 1e-6) / 1e9},
-            "router": {"kernel": dstages["router"]["kernel"], "us": dstages["router"]["us"]},
-            "route": {"kernel": dstages["route"]["kernel"], "us": dstages["route"]["us"]},
+            **{k: v for k, v in dstages.items() if k not in ("gate_up", "down")},
         },
     }
 

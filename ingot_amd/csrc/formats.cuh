@@ -86,14 +86,22 @@ struct Fmt<12> {
         m0 = dm * ubyte_f(mw, g0);
         m1 = dm * ubyte_f(mw, g0 + 1);
     }
-    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float xs0, float xs1) {
+    // Raw bytes of a chunk for the GEMM staging path: {header, nibbles}.
+    struct Raw {
+        uint4 a, b;
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
         const uint8_t* b = row + (c >> 3) * BYTES;
         uint32_t q = c & 7u;
-        uint4 hdr = *reinterpret_cast<const uint4*>(b);
-        uint4 qs = *reinterpret_cast<const uint4*>(b + 16 + 32 * (q >> 1) + 16 * (q & 1u));
+        Raw r;
+        r.a = *reinterpret_cast<const uint4*>(b);
+        r.b = *reinterpret_cast<const uint4*>(b + 16 + 32 * (q >> 1) + 16 * (q & 1u));
+        return r;
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float xs0, float xs1) {
         float d0, m0, d1, m1;
-        scales(hdr, c, d0, m0, d1, m1);
-        uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+        scales(r.a, c, d0, m0, d1, m1);
+        uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -106,17 +114,8 @@ struct Fmt<12> {
         }
         return (d0 * slo + d1 * shi) - (m0 * xs0 + m1 * xs1);
     }
-    // Raw bytes of a chunk for the GEMM staging path: {header, nibbles}.
-    struct Raw {
-        uint4 a, b;
-    };
-    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
-        const uint8_t* b = row + (c >> 3) * BYTES;
-        uint32_t q = c & 7u;
-        Raw r;
-        r.a = *reinterpret_cast<const uint4*>(b);
-        r.b = *reinterpret_cast<const uint4*>(b + 16 + 32 * (q >> 1) + 16 * (q & 1u));
-        return r;
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float xs0, float xs1) {
+        return dot_raw(load_raw(row, c), c, xv, xs0, xs1);
     }
     __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
         float d0, m0, d1, m1;
@@ -168,14 +167,16 @@ struct Fmt<0> : Contig {
             w[4 * i] = r.v[i].x; w[4 * i + 1] = r.v[i].y; w[4 * i + 2] = r.v[i].z; w[4 * i + 3] = r.v[i].w;
         }
     }
-    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
-        Raw r = load_raw(row, c);
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float, float) {
         float w[32];
         dequant_raw(r, c, w);
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) s = __builtin_fmaf(w[i], xv[i], s);
         return s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
     }
 };
 
@@ -202,14 +203,16 @@ struct Fmt<8> : Contig {
 #pragma unroll
             for (int j = 0; j < 4; ++j) w[4 * i + j] = d * sbyte_f(r.q[i], j);
     }
-    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
-        Raw r = load_raw(row, c);
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) s = __builtin_fmaf(sbyte_f(r.q[i], j), xv[4 * i + j], s);
         return half_bits_to_float(r.d) * s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
     }
 };
 
@@ -246,8 +249,10 @@ struct Nibble32 : Contig {
                 w[16 + 4 * i + j] = d * value(byte >> 4);
             }
     }
-    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
-        Raw r = load_raw(row, c);
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -298,8 +303,10 @@ struct Fmt<17> : Contig {
                 w[8 * l + v] = flip_sign(db * (float)((grid >> (8 * v)) & 255u), (sg >> v) & 1u);
         }
     }
-    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
-        Raw r = load_raw(row, c);
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
         float s = 0.f;
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
@@ -349,8 +356,10 @@ struct Fmt<18> : Contig {
             }
         }
     }
-    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float, float) {
-        Raw r = load_raw(row, c);
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
         float s = 0.f;
 #pragma unroll
         for (int l = 0; l < 4; ++l) {

@@ -230,27 +230,6 @@ struct DownArgs {
     float* out;
 };
 
-template <int KD, int KS, int VPL>
-void down_launch(hipStream_t s, dim3 grid, const DownArgs& a) {
-    hipLaunchKernelGGL((k_gemv_down<KD, KS, VPL, GEMV_RPW>), grid, dim3(256), 0, s, a.down, a.dstride, a.sdown,
-                       a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.wts, a.sgl, a.K, a.res, a.out);
-}
-
-template <int KD, int KS>
-bool down_vpl(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
-    switch (vpl) {
-        case 1: down_launch<KD, KS, 1>(s, grid, a); return true;
-        case 2: down_launch<KD, KS, 2>(s, grid, a); return true;
-        case 3: down_launch<KD, KS, 3>(s, grid, a); return true;
-        case 4: down_launch<KD, KS, 4>(s, grid, a); return true;
-        case 5: down_launch<KD, KS, 5>(s, grid, a); return true;
-        case 6: down_launch<KD, KS, 6>(s, grid, a); return true;
-        case 7: down_launch<KD, KS, 7>(s, grid, a); return true;
-        case 8: down_launch<KD, KS, 8>(s, grid, a); return true;
-        default: return false;
-    }
-}
-
 template <int KS>
 bool shared_add_cpl(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H, uint32_t SF,
                     const float* sact, const float* sgl, float* out) {
@@ -305,6 +284,54 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 
 }  // namespace
 
+// Decode gate/up after router routing (k_dec_gate_up2): 2 rows x every pair per 8-wave block.
+constexpr int GU_RPW = 2;
+constexpr int DEC_RPW = 1;  // down rows per wave
+
+template <int KIND>
+static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, dim3 grid, const uint8_t* g, const uint8_t* u,
+                            uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x, const float* logits,
+                            const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale, float limit,
+                            uint32_t* ids, float* w, uint32_t* flags, float* act) {
+#define DGU(C, N)                                                                                                 \
+    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, GU_RPW, N>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x,        \
+                       logits, bias, E, K, mode, scale, limit, ids, w, flags, act)
+    if (cpl == 1 && np == 1) { DGU(1, 1); return true; }
+    if (cpl == 1 && np == 2) { DGU(1, 2); return true; }
+    if (cpl == 2 && np == 1) { DGU(2, 1); return true; }
+    if (cpl == 2 && np == 2) { DGU(2, 2); return true; }
+#undef DGU
+    return false;
+}
+
+static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const uint8_t* u, uint64_t gs,
+                               uint64_t us, uint32_t F, uint32_t H, uint32_t T, const float* x, const float* logits,
+                               const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale, float limit,
+                               uint32_t* ids, float* w, uint32_t* flags, float* act) {
+    const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
+    dim3 grid((F + GU_RPW - 1) / GU_RPW, T);
+    switch (kind) {
+#define K_(KV) case KV: return dec_gate_up_cpl<KV>(s, cpl, np, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act);
+        K_(0) K_(2) K_(8) K_(12) K_(17) K_(18) K_(20)
+#undef K_
+        default: return false;
+    }
+}
+
+template <int KD, int KS>
+static bool dec_down_vpl(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
+#define DD(V)                                                                                                      \
+    case V:                                                                                                        \
+        hipLaunchKernelGGL((k_dec_down<KD, KS, V, DEC_RPW>), grid, dim3(256), 0, s, a.down, a.dstride, a.sdown,    \
+                           a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.wts, a.sgl, a.K, a.res, a.out);     \
+        return true;
+    switch (vpl) {
+        DD(1) DD(2) DD(3) DD(4) DD(5) DD(6) DD(7) DD(8)
+        default: return false;
+    }
+#undef DD
+}
+
 // Decode down + combine: routed-only for every kind, plus a fused shared expert
 // for the format pairs the configurations use (can_fuse_shared). Returns false
 // if no instantiation covers the shape.
@@ -315,23 +342,23 @@ static bool can_fuse_shared(uint32_t kd, int ks) {
 static bool gemv_down(hipStream_t s, uint32_t kd, int ks, const DownArgs& a, uint32_t T) {
     const uint32_t nv = a.K * (a.F / 32) + (ks >= 0 ? a.SF / 32 : 0);
     const uint32_t vpl = (nv + 63) / 64;
-    dim3 grid((a.H + 4 * GEMV_RPW - 1) / (4 * GEMV_RPW), T);
+    dim3 grid((a.H + 4 * DEC_RPW - 1) / (4 * DEC_RPW), T);
     if (ks < 0) {
         switch (kd) {
-            case 0: return down_vpl<0, -1>(s, vpl, grid, a);
-            case 2: return down_vpl<2, -1>(s, vpl, grid, a);
-            case 8: return down_vpl<8, -1>(s, vpl, grid, a);
-            case 12: return down_vpl<12, -1>(s, vpl, grid, a);
-            case 17: return down_vpl<17, -1>(s, vpl, grid, a);
-            case 18: return down_vpl<18, -1>(s, vpl, grid, a);
-            case 20: return down_vpl<20, -1>(s, vpl, grid, a);
+            case 0: return dec_down_vpl<0, -1>(s, vpl, grid, a);
+            case 2: return dec_down_vpl<2, -1>(s, vpl, grid, a);
+            case 8: return dec_down_vpl<8, -1>(s, vpl, grid, a);
+            case 12: return dec_down_vpl<12, -1>(s, vpl, grid, a);
+            case 17: return dec_down_vpl<17, -1>(s, vpl, grid, a);
+            case 18: return dec_down_vpl<18, -1>(s, vpl, grid, a);
+            case 20: return dec_down_vpl<20, -1>(s, vpl, grid, a);
             default: return false;
         }
     }
-    if (kd == 17 && ks == 8) return down_vpl<17, 8>(s, vpl, grid, a);
-    if (kd == 12 && ks == 12) return down_vpl<12, 12>(s, vpl, grid, a);
-    if (kd == 20 && ks == 20) return down_vpl<20, 20>(s, vpl, grid, a);
-    if (kd == 8 && ks == 8) return down_vpl<8, 8>(s, vpl, grid, a);
+    if (kd == 17 && ks == 8) return dec_down_vpl<17, 8>(s, vpl, grid, a);
+    if (kd == 12 && ks == 12) return dec_down_vpl<12, 12>(s, vpl, grid, a);
+    if (kd == 20 && ks == 20) return dec_down_vpl<20, 20>(s, vpl, grid, a);
+    if (kd == 8 && ks == 8) return dec_down_vpl<8, 8>(s, vpl, grid, a);
     return false;
 }
 
@@ -809,6 +836,13 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
     const float* sgl = L->has_sgvec ? L->sgl : nullptr;
     for (auto& f : L->stage) f = nullptr;
 
+    const bool hs_ = L->has_shared;
+    const int ks_ = hs_ ? (int)L->sdown.kind : -1;
+    const bool fuse_shared = hs_ && can_fuse_shared(L->down.kind, ks_);
+    const uint32_t nv_ = K * (F / 32) + (fuse_shared ? SF / 32 : 0);
+    const bool decode = P <= GEMV_MAX_PAIRS && K <= 2 * GU_WAVES && (uint64_t)K * F + (hs_ ? SF : 0) <= DOWN_LDS_FLOATS &&
+                        (nv_ + 63) / 64 <= 8 && (!hs_ || fuse_shared || (SF / 32 + 63) / 64 <= 2) && H <= 4096;
+
     // 1. router (+ RMSNorm, + shared gate logit)
     {
         const float *x = d_x, *W = L->router, *sgv = L->sgvec, *g = L->gain;
@@ -816,11 +850,13 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         float eps = L->eps;
         bool has_sg = L->has_sgvec;
         uint32_t HB = H / 256;
-        L->stage[ST_ROUTER] = [=](hipStream_t ss) { launch_router(ss, HB, T, E, has_sg, x, W, sgv, g, eps, lg, sl, xn); };
+        L->stage[ST_ROUTER] = [=](hipStream_t ss) {
+            launch_router(ss, HB, T, E, has_sg, x, W, sgv, g, eps, lg, sl, xn);
+        };
         L->stage_name[ST_ROUTER] = "k_router";
     }
-    // 2. route
-    {
+    // 2. route (prefill)
+    if (!decode) {
         const float *lg = L->logits, *b = L->bias;
         uint32_t* ids = L->ids;
         float* w = L->wts;
@@ -832,28 +868,30 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         };
         L->stage_name[ST_ROUTE] = "k_route";
     }
-    if (P <= GEMV_MAX_PAIRS) {
+    if (decode) {
+        // router -> routed gate/up (block routing) [+ shared gate/up] -> down + combine
         const DevMatrix gate = L->gate, up = L->up, down = L->down, sgate = L->sgate, sup = L->sup, sdown = L->sdown;
-        const uint32_t* ids = L->ids;
-        const float* wts = L->wts;
+        uint32_t* ids = L->ids;
+        float* wts = L->wts;
         float *act = L->act, *sact = L->sact, limit = L->limit;
-        bool hs = L->has_shared;
+        const float *lg = L->logits, *b = L->bias;
+        const uint32_t mode = L->routing;
+        const float scale = L->scale;
+        uint32_t* flags = ctx->d_flags;
+        const bool hs = hs_;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
-            launch_gemv_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, P, xin, ids, K, limit, act);
+            launch_dec_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, T, xin, lg, b, E, K, mode,
+                               scale, limit, ids, wts, flags, act);
             if (hs)
                 launch_gemv_gate_up(ss, sgate.kind, sgate.d, sup.d, sgate.stride, sup.stride, SF, H, T, xin, nullptr, 1,
                                     limit, sact);
         };
-        L->stage_name[ST_GATEUP] = "k_gemv_gate_up";
+        L->stage_name[ST_GATEUP] = "k_dec_gate_up2";
         DownArgs a{down.d, sdown.d, down.stride, sdown.stride, H, F, SF, act, sact, ids, wts, sgl, K, res, d_out};
-        const int ks = hs ? (int)sdown.kind : -1;
-        const uint32_t nvf = K * (F / 32) + (hs ? SF / 32 : 0);
-        const bool fuse = hs && can_fuse_shared(down.kind, ks) && (nvf + 63) / 64 <= 8;
-        if (!hs || fuse) {
-            if ((nvf + 63) / 64 > 8) return fail(ctx, INGOT_UNSUPPORTED, "decode down product too wide for one wave");
+        if (!hs || fuse_shared) {
+            const int ks = hs ? ks_ : -1;
             L->stage[ST_DOWN] = [=](hipStream_t ss) { gemv_down(ss, down.kind, ks, a, T); };
         } else {
-            if ((K * (F / 32) + 63) / 64 > 8) return fail(ctx, INGOT_UNSUPPORTED, "decode down product too wide for one wave");
             DownArgs ar = a;
             ar.sdown = nullptr;
             L->stage[ST_DOWN] = [=](hipStream_t ss) {
@@ -861,7 +899,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
                 launch_shared_down_add(ss, sdown.kind, sdown.d, sdown.stride, H, SF, T, sact, sgl, d_out);
             };
         }
-        L->stage_name[ST_DOWN] = "k_gemv_down";
+        L->stage_name[ST_DOWN] = "k_dec_down";
     } else {
         const DevMatrix gate = L->gate, up = L->up, down = L->down, sgate = L->sgate, sup = L->sup, sdown = L->sdown;
         const uint32_t *ids = L->ids;

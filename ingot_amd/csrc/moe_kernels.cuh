@@ -5,8 +5,10 @@
 //                            RMSNorm, optional shared-expert gate logit
 //   route    k_route         per-token top-K on 64-bit (orderable value, ~id)
 //                            keys; softmax or sigmoid+bias weights
-//   decode   k_gemv_gate_up  act[p] = SwiGLU(G_e x_t, U_e x_t) for each pair
-//            k_gemv_down     out[t] = sum_k w_k D_e act[p] (+ shared, + residual)
+//   decode   k_dec_gate_up2  routing of the block's token (block_route), then
+//                            act[p] = SwiGLU(G_e x_t, U_e x_t), one wave per pair
+//            k_gemv_gate_up  the same for the shared expert (no routing)
+//            k_dec_down      out[t] = sum_k w_k D_e act[p] (+ shared, + residual)
 //   prefill  k_dispatch_count / k_dispatch_place   stable expert grouping
 //            k_gemm<GATEUP>  MFMA f32 grouped GEMM, dequantised weights in LDS
 //            k_combine       out[t] = sum_k w_k Y[inverse[p]] (+ shared, + residual)
@@ -28,6 +30,26 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave sum through DPP (no LDS crossbar): quad xor 1 and xor 2, half-row and
+// row mirrors give every lane its 16-lane row sum; the four row sums are read
+// with readlane. Fixed order, so deterministic; it is not the router's order
+// (the router keeps wave_sum, whose tree the CPU replays).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add<0xb1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4e>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);  // row_half_mirror
+    v = dpp_add<0x140>(v);  // row_mirror
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
     return ((uint64_t)hi << 32) | lo;
@@ -39,6 +61,73 @@ __device__ __forceinline__ float swiglu(float g, float u, float limit) {
         u = fminf(fmaxf(u, -limit), limit);
     }
     return g / (1.0f + expf(-g)) * u;
+}
+
+// ------------------------------------------------------ block-level routing
+// The same selection and weights as k_route for one token, computed by a
+// whole block without a serial chain: every candidate's rank is the number of
+// larger keys (keys are unique), so candidate i with rank r < K is the r-th
+// selection. LDS: keys [E] u64, vals [E] f32, sel_id/sel_v/w [K].
+struct RouteLds {
+    uint64_t* keys;
+    float* vals;
+    uint32_t* sel_id;
+    float* sel_v;
+    float* w;
+};
+
+__device__ inline void block_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
+                                   uint32_t sigmoid_mode, float scale, RouteLds s, uint32_t* __restrict__ flags) {
+    INGOT_NO_CONTRACT
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    bool bad = false;
+    for (uint32_t e = tid; e < E; e += nt) {
+        float v = l[e];
+        float b = bias ? bias[e] : 0.f;
+        bad |= !isfinite(v) || !isfinite(b);
+        float key_v, wv;
+        if (sigmoid_mode) {
+            wv = ingot_det_sigmoid(v);
+            key_v = bias ? wv + b : wv;
+        } else {
+            key_v = bias ? v + b : v;
+            wv = key_v;
+        }
+        s.keys[e] = ingot_select_key(key_v, e);
+        s.vals[e] = wv;
+    }
+    const uint32_t E16 = (E + 15u) & ~15u;
+    for (uint32_t e = E + tid; e < E16; e += nt) s.keys[e] = 0;  // below every real key
+    if (flags && __any(bad) && (tid & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += nt) {
+        const uint64_t mine = s.keys[e];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < E16; j += 16) {
+            ulonglong2 kv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) kv[q] = *reinterpret_cast<const ulonglong2*>(&s.keys[j + 2 * q]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) rank += (kv[q].x > mine ? 1u : 0u) + (kv[q].y > mine ? 1u : 0u);
+        }
+        if (rank < K) {
+            s.sel_id[rank] = e;
+            s.sel_v[rank] = s.vals[e];
+        }
+    }
+    __syncthreads();
+    float num = 0.f, total = 0.f;
+    if (tid < K) {
+        const float top = s.sel_v[0];
+        num = sigmoid_mode ? s.sel_v[tid] : ingot_det_expf(s.sel_v[tid] - top);
+        s.w[tid] = num;
+    }
+    __syncthreads();
+    if (tid < K)
+        for (uint32_t k = 0; k < K; ++k) total += s.w[k];  // selection order, as the CPU sums
+    __syncthreads();  // every numerator read before any weight is written
+    if (tid < K) s.w[tid] = sigmoid_mode ? num / total * scale : num / total;
+    __syncthreads();
 }
 
 // ---------------------------------------------------------------- router
@@ -209,6 +298,207 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
     }
 }
 
+// ---------------------------------------------- decode: routed gate/up
+// grid (ceil(F / RPW), T), 512 threads (8 waves). The block routes its token
+// (block_route; block 0 of each token writes ids/weights for the down kernel)
+// while it stages the token's input in LDS. Wave w then computes rows
+// [RPW*bx, +RPW) of the gate and up projections of pairs k = w, w+8, ...;
+// each lane keeps its input chunks in registers.
+constexpr uint32_t GU_WAVES = 8;
+
+template <int KIND, int CPL, int RPW, int NP>
+__global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+                                                      uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
+                                                      const float* __restrict__ x, const float* __restrict__ logits,
+                                                      const float* __restrict__ bias, uint32_t E, uint32_t K,
+                                                      uint32_t sigmoid_mode, float scale, float limit,
+                                                      uint32_t* __restrict__ ids, float* __restrict__ wts,
+                                                      uint32_t* __restrict__ flags, float* __restrict__ act) {
+    using Fm = Fmt<KIND>;
+    __shared__ float s_x[4096];
+    __shared__ uint64_t s_keys[1024];
+    __shared__ float s_vals[1024];
+    __shared__ uint32_t s_id[64];
+    __shared__ float s_v[64], s_w[64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t nch = H / 32u;
+    const uint32_t r0 = blockIdx.x * RPW;
+    // Stage the token's input while the block routes it.
+    {
+        const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)t * H);
+        for (uint32_t i = threadIdx.x; i < H / 4u; i += 512u) reinterpret_cast<float4*>(s_x)[i] = x4[i];
+    }
+    block_route(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, scale, RouteLds{s_keys, s_vals, s_id, s_v, s_w},
+                blockIdx.x == 0 ? flags : nullptr);
+    if (blockIdx.x == 0 && threadIdx.x < K) {
+        ids[(uint64_t)t * K + threadIdx.x] = s_id[threadIdx.x];
+        wts[(uint64_t)t * K + threadIdx.x] = s_w[threadIdx.x];
+    }
+    // Weight loads of the wave's pairs k = wave + 8n (n < NP; K <= 8 NP);
+    // a pair beyond K re-reads pair 0's rows and is not stored.
+    typename Fm::Raw rg[NP][RPW][CPL], ru[NP][RPW][CPL];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const uint32_t k = wave + GU_WAVES * n;
+        const uint32_t e = s_id[k < K ? k : 0u];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const uint32_t r = min(r0 + i, F - 1);
+            const uint8_t* grow = gate + ((uint64_t)e * F + r) * gstride;
+            const uint8_t* urow = up + ((uint64_t)e * F + r) * ustride;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = min(lane + 64u * j, nch - 1);
+                rg[n][i][j] = Fm::load_raw(grow, c);
+                ru[n][i][j] = Fm::load_raw(urow, c);
+            }
+        }
+    }
+    float xv[CPL][32], xs0[CPL], xs1[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t c = min(lane + 64u * j, nch - 1);
+        Fm::load_x(s_x, c, xv[j]);
+        xs0[j] = xs1[j] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            xs0[j] += xv[j][q];
+            xs1[j] += xv[j][16 + q];
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const uint32_t k = wave + GU_WAVES * n;
+        float gs[RPW], us[RPW];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            gs[i] = us[i] = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                if (lane + 64u * j >= nch) continue;
+                const uint32_t c = lane + 64u * j;
+                gs[i] += Fm::dot_raw(rg[n][i][j], c, xv[j], xs0[j], xs1[j]);
+                us[i] += Fm::dot_raw(ru[n][i][j], c, xv[j], xs0[j], xs1[j]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
+            if (k < K && lane == (uint32_t)i && r0 + i < F) act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit);
+        }
+    }
+}
+
+// ------------------------------------------------ decode: down + combine
+// grid (ceil(H / (4*RPW)), T), 256 threads. The token's K activations (and
+// the shared expert's) are staged in LDS once per block; each wave owns RPW
+// output rows. The K pairs' chunks (plus the shared expert's) form one
+// virtual row spread over the lanes (VPL chunks per lane), with each pair's
+// routing weight folded into its activations, so the wave sum is
+// sum_k w_k (D_e act_k)[i] (+ gate * (S_down sact)[i]) directly.
+constexpr uint32_t DOWN_LDS_FLOATS = 12288;  // 48 KB of staged activations
+
+template <int KD, int KS, int VPL, int RPW>
+__global__ __launch_bounds__(256) void k_dec_down(const uint8_t* __restrict__ down, uint64_t dstride,
+                                                  const uint8_t* __restrict__ sdown, uint64_t sdstride, uint32_t H,
+                                                  uint32_t F, uint32_t SF, const float* __restrict__ act,
+                                                  const float* __restrict__ sact, const uint32_t* __restrict__ ids,
+                                                  const float* __restrict__ wts, const float* __restrict__ sgl,
+                                                  uint32_t K, const float* __restrict__ res, float* __restrict__ out) {
+    using Fd = Fmt<KD>;
+    using Fs = Fmt<(KS < 0 ? KD : KS)>;
+    __shared__ float s_act[DOWN_LDS_FLOATS];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
+    const uint32_t nv = K * nchF + nchS;
+    const uint32_t r0 = (blockIdx.x * 4u + wave) * RPW;
+    // 1. this lane's chunks of the virtual row: expert row base, chunk, weight
+    const uint8_t* base[VPL];
+    uint32_t cc[VPL], aoff[VPL];
+    float w[VPL];
+    bool isS[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const uint32_t v = lane + 64u * j;
+        base[j] = nullptr;
+        cc[j] = 0;
+        aoff[j] = 0;
+        w[j] = 0.f;
+        isS[j] = false;
+        if (v < K * nchF) {
+            const uint32_t k = v / nchF, p = t * K + k;
+            base[j] = down + (uint64_t)ids[p] * H * dstride;
+            cc[j] = v % nchF;
+            aoff[j] = k * F;
+            w[j] = wts[p];
+        } else if (v < nv) {
+            base[j] = sdown;
+            cc[j] = v - K * nchF;
+            aoff[j] = K * F;
+            isS[j] = true;
+            w[j] = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
+        }
+    }
+    // 2. weight loads for all RPW rows, issued before the activations arrive
+    typename Fd::Raw rd[RPW][VPL];
+    typename Fs::Raw rs[KS >= 0 ? RPW : 1][KS >= 0 ? VPL : 1];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const uint32_t r = min(r0 + i, H - 1);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            if (!base[j]) continue;
+            if (KS >= 0 && isS[j]) rs[KS >= 0 ? i : 0][KS >= 0 ? j : 0] = Fs::load_raw(base[j] + (uint64_t)r * sdstride, cc[j]);
+            else rd[i][j] = Fd::load_raw(base[j] + (uint64_t)r * dstride, cc[j]);
+        }
+    }
+    // 3. stage the token's activations
+    {
+        const float4* a4 = reinterpret_cast<const float4*>(act + (uint64_t)t * K * F);
+        float4* d4 = reinterpret_cast<float4*>(s_act);
+        for (uint32_t i = tid; i < K * F / 4u; i += 256u) d4[i] = a4[i];
+        if (KS >= 0) {
+            const float4* s4 = reinterpret_cast<const float4*>(sact + (uint64_t)t * SF);
+            for (uint32_t i = tid; i < SF / 4u; i += 256u) d4[K * F / 4u + i] = s4[i];
+        }
+    }
+    __syncthreads();
+    // 4. weighted activations of each chunk into registers, then the dot products
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        if (!base[j]) continue;
+        float xv[32], xs0 = 0.f, xs1 = 0.f;
+        if (KS >= 0 && isS[j]) Fs::load_x(s_act + aoff[j], cc[j], xv);
+        else Fd::load_x(s_act + aoff[j], cc[j], xv);
+#pragma unroll
+        for (int q = 0; q < 32; ++q) xv[q] *= w[j];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            xs0 += xv[q];
+            xs1 += xv[16 + q];
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            if (KS >= 0 && isS[j]) acc[i] += Fs::dot_raw(rs[KS >= 0 ? i : 0][KS >= 0 ? j : 0], cc[j], xv, xs0, xs1);
+            else acc[i] += Fd::dot_raw(rd[i][j], cc[j], xv, xs0, xs1);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        float sum = wave_sum_dpp(acc[i]);
+        const uint32_t r = r0 + i;
+        if (lane == (uint32_t)i && r < H) {
+            if (res) sum += res[(uint64_t)t * H + r];
+            out[(uint64_t)t * H + r] = sum;
+        }
+    }
+}
+
 // ----------------------------------------------------------- decode: gate/up
 // grid (ceil(F / (4*RPW)), pairs); a wave owns RPW rows of one pair. Lane l
 // owns chunks l + 64j (j < CPL) of the H columns: their 32 inputs stay in
@@ -263,91 +553,6 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(const uint8_t* __restrict_
     for (int i = 0; i < RPW; ++i) {
         float g = wave_sum(gs[i]), u = wave_sum(us[i]);
         if (lane == (uint32_t)i && r0 + i < F) act[(uint64_t)p * F + r0 + i] = swiglu(g, u, limit);
-    }
-}
-
-// ------------------------------------------------------ decode: down+combine
-// grid (ceil(H / (4*RPW)), T); a wave owns RPW output rows of one token. The
-// token's K routed pairs (and the shared expert, if any) form one virtual row
-// of K*F/32 (+SF/32) chunks spread over the lanes (VPL per lane); each lane
-// keeps its chunks' activations in registers, pre-multiplied by the pair's
-// routing weight, so the wave sum is directly sum_k w_k (D_e act_k)[i].
-// The shared expert (format KS, KS < 0: none here) is scaled by
-// sigmoid(sgl[t]) when sgl != NULL, else by 1. res != NULL adds a residual.
-template <int KD, int KS, int VPL, int RPW>
-__global__ __launch_bounds__(256) void k_gemv_down(const uint8_t* __restrict__ down, uint64_t dstride,
-                                                   const uint8_t* __restrict__ sdown, uint64_t sdstride,
-                                                   uint32_t H, uint32_t F, uint32_t SF,
-                                                   const float* __restrict__ act, const float* __restrict__ sact,
-                                                   const uint32_t* __restrict__ ids, const float* __restrict__ wts,
-                                                   const float* __restrict__ sgl, uint32_t K,
-                                                   const float* __restrict__ res, float* __restrict__ out) {
-    using Fd = Fmt<KD>;
-    using Fs = Fmt<(KS < 0 ? KD : KS)>;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t t = blockIdx.y;
-    const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
-    const uint32_t nv = K * nchF + nchS;
-    float xv[VPL][32], xs0[VPL], xs1[VPL];
-    const uint8_t* base[VPL];
-    uint32_t cc[VPL];
-    bool isS[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        uint32_t v = lane + 64u * j;
-        base[j] = nullptr;
-        cc[j] = 0;
-        isS[j] = false;
-        float w = 0.f;
-        xs0[j] = xs1[j] = 0.f;
-        if (v < K * nchF) {
-            uint32_t k = v / nchF, c = v % nchF, p = t * K + k;
-            base[j] = down + (uint64_t)ids[p] * H * dstride;
-            cc[j] = c;
-            w = wts[p];
-            Fd::load_x(act + (uint64_t)p * F, c, xv[j]);
-        } else if (v < nv) {
-            uint32_t c = v - K * nchF;
-            base[j] = sdown;
-            cc[j] = c;
-            isS[j] = true;
-            w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
-            Fs::load_x(sact + (uint64_t)t * SF, c, xv[j]);
-        }
-        if (base[j]) {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) xv[j][i] *= w;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                xs0[j] += xv[j][i];
-                xs1[j] += xv[j][16 + i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) xv[j][i] = 0.f;
-        }
-    }
-    const uint32_t r0 = (blockIdx.x * 4u + wave) * RPW;
-    float acc[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        acc[i] = 0.f;
-        uint32_t r = min(r0 + i, H - 1);
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            if (!base[j]) continue;
-            if (KS >= 0 && isS[j]) acc[i] += Fs::dot(base[j] + (uint64_t)r * sdstride, cc[j], xv[j], xs0[j], xs1[j]);
-            else acc[i] += Fd::dot(base[j] + (uint64_t)r * dstride, cc[j], xv[j], xs0[j], xs1[j]);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-        float s = wave_sum(acc[i]);
-        uint32_t r = r0 + i;
-        if (lane == (uint32_t)i && r < H) {
-            if (res) s += res[(uint64_t)t * H + r];
-            out[(uint64_t)t * H + r] = s;
-        }
     }
 }
 
