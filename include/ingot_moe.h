@@ -169,6 +169,12 @@ int ingot_layer_reserve(ingot_layer* layer, uint32_t T);
  * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL. */
 int ingot_layer_forward(ingot_layer* layer, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
                         float* d_weights);
+/* Prefill GEMM arithmetic. INGOT_GEMM_AUTO (default): Q4_K experts use the
+ * split-precision f16 MFMA GEMM (fp32-accurate to ~2^-21 relative; needs
+ * |activations| < 65504), other formats the fp32 MFMA GEMM.
+ * INGOT_GEMM_FP32: always the fp32 MFMA GEMM. */
+enum ingot_gemm_mode { INGOT_GEMM_AUTO = 0, INGOT_GEMM_FP32 = 1 };
+int ingot_layer_set_gemm_mode(ingot_layer* layer, uint32_t mode);
 /* Device bytes held by the layer's weights. */
 uint64_t ingot_layer_weight_bytes(const ingot_layer* layer);
 

@@ -370,6 +370,7 @@ struct ingot_layer {
     uint32_t H = 0, E = 0, K = 0, F = 0, SF = 0, routing = 0;
     float scale = 1.f, limit = 0.f, eps = 0.f;
     bool has_shared = false, has_sgvec = false, has_norm = false, has_bias = false;
+    uint32_t gemm_mode = INGOT_GEMM_AUTO;
     float *router = nullptr, *bias = nullptr, *sgvec = nullptr, *gain = nullptr;
     DevMatrix gate, up, down, sgate, sup, sdown;
     // workspace
@@ -379,6 +380,7 @@ struct ingot_layer {
           *Y = nullptr, *Ys = nullptr;
     uint32_t *ids = nullptr, *counts = nullptr, *first = nullptr, *tiles = nullptr, *pairs = nullptr,
              *inverse = nullptr, *stiles = nullptr;
+    _Float16 *xh = nullptr, *xl = nullptr, *acth = nullptr, *actl = nullptr;
     uint32_t tile_cap = 0, stile_cap = 0;
     std::function<void(hipStream_t)> stage[ST_N];
     const char* stage_name[ST_N] = {};
@@ -411,6 +413,8 @@ static int reserve(ingot_layer* L, uint32_t T) {
         {(void**)&L->counts, 4ull * L->E},       {(void**)&L->first, 4ull * L->E},
         {(void**)&L->tiles, 16ull * tile_cap},   {(void**)&L->pairs, 4ull * P},
         {(void**)&L->inverse, 4ull * P},         {(void**)&L->stiles, 16ull * stile_cap},
+        {(void**)&L->xh, 2ull * T * L->H},      {(void**)&L->xl, 2ull * T * L->H},
+        {(void**)&L->acth, 2ull * P * L->F},     {(void**)&L->actl, 2ull * P * L->F},
     };
     uint64_t total = 0;
     for (auto& p : parts) total += (p.bytes + 255) & ~255ull;
@@ -771,6 +775,7 @@ int ingot_layer_clone(const ingot_layer* src, ingot_layer** out) {
     L->scale = src->scale; L->limit = src->limit; L->eps = src->eps;
     L->has_shared = src->has_shared; L->has_sgvec = src->has_sgvec; L->has_norm = src->has_norm;
     L->has_bias = src->has_bias;
+    L->gemm_mode = src->gemm_mode;
     auto dup = [&](const void* s, uint64_t bytes, void** dst) -> int {
         if (!s) return INGOT_OK;
         HIP_TRY(ctx, hipMalloc(dst, bytes));
@@ -803,6 +808,12 @@ void ingot_layer_destroy(ingot_layer* L) {
     (void)hipStreamSynchronize(L->ctx->stream);
     free_dev(L);
     delete L;
+}
+
+int ingot_layer_set_gemm_mode(ingot_layer* L, uint32_t mode) {
+    if (!L || mode > INGOT_GEMM_FP32) return INGOT_INVALID;
+    L->gemm_mode = mode;
+    return INGOT_OK;
 }
 
 uint64_t ingot_layer_weight_bytes(const ingot_layer* L) {
@@ -915,22 +926,36 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
             if (hs) hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch_count";
+        const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && gate.kind == 12 && down.kind == 12;
+        _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
-            launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin, pairs,
-                              K, tiles, F, limit, act);
+            if (f16) {
+                const uint64_t n = (uint64_t)T * H;
+                hipLaunchKernelGGL(k_split_f16, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256), 0, ss, xin, n, xh, xl);
+                hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(F / 64, cap), dim3(256), 0, ss, gate.d, up.d,
+                                   gate.stride, up.stride, F, H, xh, xl, pairs, K, tiles, F, limit, nullptr, acth,
+                                   actl);
+            } else {
+                launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
+                                  pairs, K, tiles, F, limit, act);
+            }
             if (hs)
                 launch_gemm<true>(ss, sgate.kind, dim3(SF / 64, scap), sgate.d, sup.d, sgate.stride, sup.stride, SF, H,
                                   xin, nullptr, 1, stiles, SF, limit, sact);
         };
-        L->stage_name[ST_GATEUP] = "k_gemm<gate_up>";
+        L->stage_name[ST_GATEUP] = f16 ? "k_gemm_q4k_f16<gate_up>" : "k_gemm<gate_up>";
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
-            launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act, nullptr,
-                               K, tiles, H, 0.f, Y);
+            if (f16)
+                hipLaunchKernelGGL((k_gemm_q4k_f16<false>), dim3(H / 128, cap), dim3(256), 0, ss, down.d, nullptr,
+                                   down.stride, 0ull, H, F, acth, actl, nullptr, K, tiles, H, 0.f, Y, nullptr, nullptr);
+            else
+                launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act,
+                                   nullptr, K, tiles, H, 0.f, Y);
             if (hs)
                 launch_gemm<false>(ss, sdown.kind, dim3(H / 128, scap), sdown.d, nullptr, sdown.stride, 0, H, SF, sact,
                                    nullptr, 1, stiles, H, 0.f, Ys);
         };
-        L->stage_name[ST_DOWN] = "k_gemm<down>";
+        L->stage_name[ST_DOWN] = f16 ? "k_gemm_q4k_f16<down>" : "k_gemm<down>";
         L->stage[ST_COMBINE] = [=](hipStream_t ss) {
             uint64_t n4 = (uint64_t)T * H / 4;
             hipLaunchKernelGGL(k_combine, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, ss, Y, hs ? Ys : nullptr,

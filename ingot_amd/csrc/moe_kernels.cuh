@@ -826,6 +826,170 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
         }
 }
 
+// -------------------------------- prefill: split-precision f16 MFMA GEMM (Q4_K)
+// Same tiling and tile list as k_gemm, on v_mfma_f32_16x16x32_f16 with fp32
+// accumulation. Each operand is split into f16 hi + lo (v = hi + lo with
+// |v - hi - lo| <= 2^-22 |v| in the f16 normal range) and every product is
+// taken as hi*hi + hi*lo + lo*hi, so the result matches fp32 operands to about
+// 2^-21 relative while running at the f16 MFMA rate.
+//   A (inputs or activations) arrives pre-split in HBM (ah, al: [rows][kdim] f16)
+//   and is staged per 64-column slab in LDS.
+//   B (weights) is decoded by each wave straight into MFMA fragments: lane l
+//   owns row (l % 16) of an N-block and columns 8*(l/16)..+7 of each 32-column
+//   group; for Q4_K the slab's two groups are the low and high nibbles of the
+//   same 8 bytes (kernels/iq3_mix.metal:19-23 layout).
+// GATEUP writes act = SwiGLU(gate, up) already split (out_h, out_l: [P][F] f16);
+// the down GEMM writes fp32 Y.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+constexpr uint32_t A16_STRIDE = 72;  // halves per LDS row: 64 + 8 pad (144 B) against bank conflicts
+
+__device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
+}
+
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+                                                      uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
+                                                      uint32_t kdim, const _Float16* __restrict__ ah,
+                                                      const _Float16* __restrict__ al, const uint32_t* __restrict__ pairs,
+                                                      uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo,
+                                                      float limit, float* __restrict__ out, _Float16* __restrict__ out_h,
+                                                      _Float16* __restrict__ out_l) {
+    __shared__ _Float16 Ash[TM * A16_STRIDE];
+    __shared__ _Float16 Asl[TM * A16_STRIDE];
+    const uint32_t* tile = tiles + 4u * blockIdx.y;
+    const uint32_t n = tile[2];
+    if (n == 0) return;
+    const uint32_t e = tile[0], q0 = tile[1];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, kq = lane >> 4;
+    const uint32_t row0 = blockIdx.x * (GATEUP ? 64u : 128u);
+
+    // A loader: thread -> row tid/4, 16 halves at column 16*(tid%4) of the slab
+    const uint32_t am = tid >> 2, acol = 16u * (tid & 3u);
+    const _Float16 *arow_h = nullptr, *arow_l = nullptr;
+    if (am < n) {
+        const uint32_t q = q0 + am;
+        const uint64_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
+        arow_h = ah + r * kdim;
+        arow_l = al + r * kdim;
+    }
+    // B rows of this wave's two N-blocks
+    const uint8_t* brow[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        if (GATEUP) {
+            const uint32_t r = row0 + 16u * wave + (lane & 15u);
+            brow[nb] = (nb == 0 ? w0 : w1) + ((uint64_t)e * rows_per_expert + r) * (nb == 0 ? stride0 : stride1);
+        } else {
+            const uint32_t r = row0 + 32u * wave + 16u * nb + (lane & 15u);
+            brow[nb] = w0 + ((uint64_t)e * rows_per_expert + r) * stride0;
+        }
+    }
+
+    floatx4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    uint4 pa_h[2], pa_l[2], phdr[2];
+    uint2 pq[2];
+    auto load = [&](uint32_t s) {
+        if (arow_h) {
+            pa_h[0] = *reinterpret_cast<const uint4*>(arow_h + 64u * s + acol);
+            pa_h[1] = *reinterpret_cast<const uint4*>(arow_h + 64u * s + acol + 8);
+            pa_l[0] = *reinterpret_cast<const uint4*>(arow_l + 64u * s + acol);
+            pa_l[1] = *reinterpret_cast<const uint4*>(arow_l + 64u * s + acol + 8);
+        } else {
+            pa_h[0] = pa_h[1] = pa_l[0] = pa_l[1] = make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const uint8_t* b = brow[nb] + (s >> 2) * 144u;
+            phdr[nb] = *reinterpret_cast<const uint4*>(b);
+            pq[nb] = *reinterpret_cast<const uint2*>(b + 16u + 32u * (s & 3u) + 8u * kq);
+        }
+    };
+    const uint32_t slabs = kdim / 64u;
+    load(0);
+    for (uint32_t s = 0; s < slabs; ++s) {
+        *reinterpret_cast<uint4*>(&Ash[am * A16_STRIDE + acol]) = pa_h[0];
+        *reinterpret_cast<uint4*>(&Ash[am * A16_STRIDE + acol + 8]) = pa_h[1];
+        *reinterpret_cast<uint4*>(&Asl[am * A16_STRIDE + acol]) = pa_l[0];
+        *reinterpret_cast<uint4*>(&Asl[am * A16_STRIDE + acol + 8]) = pa_l[1];
+        // Decode this slab's B fragments: group 0 = low nibbles, group 1 = high nibbles.
+        half8 bh[2][2], bl[2][2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            float d0, m0, d1, m1;
+            Fmt<12>::scales(phdr[nb], 2u * (s & 3u), d0, m0, d1, m1);
+            const uint32_t wq[2] = {pq[nb].x, pq[nb].y};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t lo = wq[h] & 0x0f0f0f0fu, hi = (wq[h] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    _Float16 xh, xl;
+                    split_f16(d0 * ubyte_f(lo, j) - m0, xh, xl);
+                    bh[nb][0][4 * h + j] = xh;
+                    bl[nb][0][4 * h + j] = xl;
+                    split_f16(d1 * ubyte_f(hi, j) - m1, xh, xl);
+                    bh[nb][1][4 * h + j] = xh;
+                    bl[nb][1][4 * h + j] = xl;
+                }
+            }
+        }
+        __syncthreads();
+        if (s + 1 < slabs) load(s + 1);
+#pragma unroll
+        for (int gi = 0; gi < 2; ++gi) {
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const uint32_t off = (mb * 16u + (lane & 15u)) * A16_STRIDE + 32u * gi + 8u * kq;
+                const half8 a_h = *reinterpret_cast<const half8*>(&Ash[off]);
+                const half8 a_l = *reinterpret_cast<const half8*>(&Asl[off]);
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, bh[nb][gi], acc[mb][nb], 0, 0, 0);
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, bl[nb][gi], acc[mb][nb], 0, 0, 0);
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, bh[nb][gi], acc[mb][nb], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t m = mb * 16u + 4u * kq + j;
+            if (m >= n) continue;
+            const uint64_t q = q0 + m;
+            if (GATEUP) {
+                const uint32_t r = row0 + 16u * wave + (lane & 15u);
+                _Float16 xh, xl;
+                split_f16(swiglu(acc[mb][0][j], acc[mb][1][j], limit), xh, xl);
+                out_h[q * ldo + r] = xh;
+                out_l[q * ldo + r] = xl;
+            } else {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) out[q * ldo + row0 + 32u * wave + 16u * nb + (lane & 15u)] = acc[mb][nb][j];
+            }
+        }
+}
+
+// x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)).
+__global__ void k_split_f16(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
+                            _Float16* __restrict__ xl) {
+    const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4u;
+    if (i >= n) return;
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    const float a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split_f16(a[j], xh[i + j], xl[i + j]);
+}
+
 // Dense token tiles for the shared expert: tile t = {0, 64 t, min(64, T - 64 t), 0}.
 __global__ void k_dense_tiles(uint32_t T, uint32_t cap, uint32_t* __restrict__ tiles) {
     uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;

@@ -31,6 +31,9 @@ ROUTE_SOFTMAX, ROUTE_SIGMOID = 0, 1
 # GGML type ids (src/gguf.rs:470-491)
 F32, F16, Q4_0, Q8_0, Q4_K, IQ2_XS, IQ3_XXS, IQ4_NL = 0, 1, 2, 8, 12, 17, 18, 20
 
+# Prefill GEMM arithmetic (ingot_layer_set_gemm_mode)
+GEMM_AUTO, GEMM_FP32 = 0, 1
+
 # Stages of a layer forward (ingot_layer_time_stage).
 STAGE_ROUTER, STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_DISPATCH = range(6)
 
@@ -349,6 +352,10 @@ class MoeLayer:
 
     def weight_bytes(self) -> int:
         return int(self.gpu.lib.ingot_layer_weight_bytes(self.handle))
+
+    def set_gemm_mode(self, mode: int) -> None:
+        """GEMM_AUTO: split-precision f16 MFMA for Q4_K prefill; GEMM_FP32: fp32 MFMA."""
+        self.gpu._check(self.gpu.lib.ingot_layer_set_gemm_mode(self.handle, mode))
 
     def reserve(self, T: int) -> None:
         self.gpu._check(self.gpu.lib.ingot_layer_reserve(self.handle, T))

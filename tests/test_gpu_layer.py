@@ -38,6 +38,16 @@ def test_c1_prefill_full(gpu, oracle):
     layer.destroy()
 
 
+def test_c1_prefill_fp32_gemm_mode(gpu, oracle):
+    """The fp32 MFMA GEMM (the path for non-Q4_K formats) on the C1 layer."""
+    from ingot_amd.moe import GEMM_FP32
+    spec = CF.c1_layer()
+    layer = MoeLayer(gpu, spec)
+    layer.set_gemm_mode(GEMM_FP32)
+    check_layer(layer, spec, CF.inputs(1, 512, 2048, seed=1), oracle, "C1 prefill 512 fp32 GEMM")
+    layer.destroy()
+
+
 def test_c2_decode_full(gpu, oracle):
     spec = CF.c2_layer()
     layer = MoeLayer(gpu, spec)
@@ -84,7 +94,7 @@ def test_formats_decode_and_prefill(gpu, oracle, gk, dk):
 
 
 def test_hidden_4096_and_1024(gpu, oracle):
-    for H in (4096, 1024):
+    for H in (4096, 1024, 2048):
         spec = small_layer(Q4_K, Q4_K, H=H, E=8, K=2, F=256)
         layer = MoeLayer(gpu, spec)
         for T in (1, 70):
