@@ -920,13 +920,14 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         float *act = L->act, *sact = L->sact, *Y = L->Y, *Ys = L->Ys, limit = L->limit;
         const float* wts = L->wts;
         bool hs = L->has_shared;
+        const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && gate.kind == 12 && down.kind == 12;
+        const uint32_t tm = f16 ? TM16 : TM;
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
-            hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, ss, ids, P, E, TM, cap, counts, first, tiles);
+            hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, cap, counts, first, tiles);
             hipLaunchKernelGGL(k_dispatch_place, dim3(E), dim3(256), 0, ss, ids, P, counts, first, pairs, inverse);
             if (hs) hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch_count";
-        const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && gate.kind == 12 && down.kind == 12;
         _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             if (f16) {

@@ -24,9 +24,23 @@ namespace ingot {
 constexpr int WAVE = 64;
 constexpr uint32_t FLAG_NONFINITE = 1u;
 
+// The xor butterfly v_l <- v_l + v_(l xor m), m = 32, 16, ..., 1: the router's
+// fixed reduction tree (det_math.h). Each partner value is fetched by an exact
+// lane permutation: m = 32 through the LDS crossbar, m = 16 by ds_swizzle
+// (bitmask mode, xor 16 within 32 lanes), m = 8 by DPP row_ror:8 ((l + 8) mod 16
+// = l xor 8 in either rotate direction), m = 4 by DPP quad_perm [3,2,1,0]
+// (l xor 3) followed by row_half_mirror (l xor 7), m = 2 and 1 by quad_perm.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    v = v + __shfl_xor(v, 32);
+    v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+    v = v + dpp_mov<0x128>(v);
+    v = v + dpp_mov<0x141>(dpp_mov<0x1b>(v));
+    v = v + dpp_mov<0x4e>(v);
+    v = v + dpp_mov<0xb1>(v);
     return v;
 }
 
@@ -848,6 +862,23 @@ __device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(v - (float)hi);
 }
 
+// 8 fp32 values -> f16 hi and lo halves (packed pairs, round toward zero:
+// hi = rtz(v), lo = rtz(v - hi), |v - hi - lo| < 2^-20 |v|).
+__device__ __forceinline__ void split8(const float* v, uint4& hi, uint4& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto hp = __builtin_amdgcn_cvt_pkrtz(v[2 * i], v[2 * i + 1]);
+        const auto lp = __builtin_amdgcn_cvt_pkrtz(v[2 * i] - (float)hp[0], v[2 * i + 1] - (float)hp[1]);
+        h[i] = __builtin_bit_cast(uint32_t, hp);
+        l[i] = __builtin_bit_cast(uint32_t, lp);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+constexpr uint32_t TM16 = 64;  // tokens per tile of the f16 GEMM
+
 template <bool GATEUP>
 __global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
                                                       uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
@@ -856,8 +887,12 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict_
                                                       uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo,
                                                       float limit, float* __restrict__ out, _Float16* __restrict__ out_h,
                                                       _Float16* __restrict__ out_l) {
-    __shared__ _Float16 Ash[TM * A16_STRIDE];
-    __shared__ _Float16 Asl[TM * A16_STRIDE];
+    constexpr int MB = TM16 / 16;
+    // A tiles: 64 halves (128 B) per row, 16-byte chunk c of row r stored at
+    // chunk c ^ ((r >> 1) & 7): the stores (4 threads per row) and the MFMA
+    // fragment reads (16 rows at one chunk) then touch every bank once.
+    __shared__ _Float16 Ash[TM16 * 64];
+    __shared__ _Float16 Asl[TM16 * 64];
     const uint32_t* tile = tiles + 4u * blockIdx.y;
     const uint32_t n = tile[2];
     if (n == 0) return;
@@ -865,8 +900,10 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict_
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, kq = lane >> 4;
     const uint32_t row0 = blockIdx.x * (GATEUP ? 64u : 128u);
 
-    // A loader: thread -> row tid/4, 16 halves at column 16*(tid%4) of the slab
-    const uint32_t am = tid >> 2, acol = 16u * (tid & 3u);
+    // A loader: TM16 rows x 64 halves per part; thread -> row tid / (256 / TM16)
+    constexpr uint32_t TPR = 256u / TM16, HPT = 64u / TPR;  // threads per row, halves per thread
+    constexpr int AV = HPT / 8;                             // uint4 loads per part
+    const uint32_t am = tid / TPR, acol = HPT * (tid % TPR);
     const _Float16 *arow_h = nullptr, *arow_l = nullptr;
     if (am < n) {
         const uint32_t q = q0 + am;
@@ -874,7 +911,6 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict_
         arow_h = ah + r * kdim;
         arow_l = al + r * kdim;
     }
-    // B rows of this wave's two N-blocks
     const uint8_t* brow[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
@@ -887,80 +923,102 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict_
         }
     }
 
-    floatx4 acc[4][2];
+    floatx4 acc[MB][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 pa_h[2], pa_l[2], phdr[2];
-    uint2 pq[2];
-    auto load = [&](uint32_t s) {
-        if (arow_h) {
-            pa_h[0] = *reinterpret_cast<const uint4*>(arow_h + 64u * s + acol);
-            pa_h[1] = *reinterpret_cast<const uint4*>(arow_h + 64u * s + acol + 8);
-            pa_l[0] = *reinterpret_cast<const uint4*>(arow_l + 64u * s + acol);
-            pa_l[1] = *reinterpret_cast<const uint4*>(arow_l + 64u * s + acol + 8);
-        } else {
-            pa_h[0] = pa_h[1] = pa_l[0] = pa_l[1] = make_uint4(0, 0, 0, 0);
-        }
+    // A: one slab ahead (L2-resident inputs). B: one Q4_K superblock (4 slabs)
+    // ahead, because weights stream from HBM.
+    uint4 pa_h[AV], pa_l[AV];
+    auto load_a = [&](uint32_t s) {
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const uint8_t* b = brow[nb] + (s >> 2) * 144u;
-            phdr[nb] = *reinterpret_cast<const uint4*>(b);
-            pq[nb] = *reinterpret_cast<const uint2*>(b + 16u + 32u * (s & 3u) + 8u * kq);
+        for (int i = 0; i < AV; ++i) {
+            pa_h[i] = arow_h ? *reinterpret_cast<const uint4*>(arow_h + 64u * s + acol + 8u * i) : make_uint4(0, 0, 0, 0);
+            pa_l[i] = arow_l ? *reinterpret_cast<const uint4*>(arow_l + 64u * s + acol + 8u * i) : make_uint4(0, 0, 0, 0);
         }
     };
-    const uint32_t slabs = kdim / 64u;
-    load(0);
-    for (uint32_t s = 0; s < slabs; ++s) {
-        *reinterpret_cast<uint4*>(&Ash[am * A16_STRIDE + acol]) = pa_h[0];
-        *reinterpret_cast<uint4*>(&Ash[am * A16_STRIDE + acol + 8]) = pa_h[1];
-        *reinterpret_cast<uint4*>(&Asl[am * A16_STRIDE + acol]) = pa_l[0];
-        *reinterpret_cast<uint4*>(&Asl[am * A16_STRIDE + acol + 8]) = pa_l[1];
-        // Decode this slab's B fragments: group 0 = low nibbles, group 1 = high nibbles.
-        half8 bh[2][2], bl[2][2];
+    uint4 hdr[2], nhdr[2];
+    uint2 qs[2][4], nqs[2][4];
+    auto load_b = [&](uint32_t sb) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            float d0, m0, d1, m1;
-            Fmt<12>::scales(phdr[nb], 2u * (s & 3u), d0, m0, d1, m1);
-            const uint32_t wq[2] = {pq[nb].x, pq[nb].y};
+            const uint8_t* b = brow[nb] + sb * 144u;
+            nhdr[nb] = *reinterpret_cast<const uint4*>(b);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t lo = wq[h] & 0x0f0f0f0fu, hi = (wq[h] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    _Float16 xh, xl;
-                    split_f16(d0 * ubyte_f(lo, j) - m0, xh, xl);
-                    bh[nb][0][4 * h + j] = xh;
-                    bl[nb][0][4 * h + j] = xl;
-                    split_f16(d1 * ubyte_f(hi, j) - m1, xh, xl);
-                    bh[nb][1][4 * h + j] = xh;
-                    bl[nb][1][4 * h + j] = xl;
-                }
-            }
+            for (int q = 0; q < 4; ++q) nqs[nb][q] = *reinterpret_cast<const uint2*>(b + 16u + 32u * q + 8u * kq);
         }
-        __syncthreads();
-        if (s + 1 < slabs) load(s + 1);
+    };
+    const uint32_t slabs = kdim / 64u, sbs = kdim / 256u;
+    load_a(0);
+    load_b(0);
+    for (uint32_t sb = 0; sb < sbs; ++sb) {
 #pragma unroll
-        for (int gi = 0; gi < 2; ++gi) {
+        for (int nb = 0; nb < 2; ++nb) {
+            hdr[nb] = nhdr[nb];
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const uint32_t off = (mb * 16u + (lane & 15u)) * A16_STRIDE + 32u * gi + 8u * kq;
-                const half8 a_h = *reinterpret_cast<const half8*>(&Ash[off]);
-                const half8 a_l = *reinterpret_cast<const half8*>(&Asl[off]);
+            for (int q = 0; q < 4; ++q) qs[nb][q] = nqs[nb][q];
+        }
+        if (sb + 1 < sbs) load_b(sb + 1);
+#pragma unroll
+        for (uint32_t sq = 0; sq < 4; ++sq) {
+            const uint32_t s = 4u * sb + sq;
+#pragma unroll
+            for (int i = 0; i < AV; ++i) {
+                const uint32_t off = am * 64u + 8u * (((acol >> 3) + i) ^ ((am >> 1) & 7u));
+                *reinterpret_cast<uint4*>(&Ash[off]) = pa_h[i];
+                *reinterpret_cast<uint4*>(&Asl[off]) = pa_l[i];
+            }
+            // This slab's B fragments: group 0 = low nibbles, group 1 = high nibbles.
+            uint4 bh[2][2], bl[2][2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                float d0, m0, d1, m1;
+                Fmt<12>::scales(hdr[nb], 2u * sq, d0, m0, d1, m1);
+                float v0[8], v1[8];
+                const uint32_t wq[2] = {qs[nb][sq].x, qs[nb][sq].y};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t lo = wq[h] & 0x0f0f0f0fu, hi = (wq[h] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        v0[4 * h + j] = d0 * ubyte_f(lo, j) - m0;
+                        v1[4 * h + j] = d1 * ubyte_f(hi, j) - m1;
+                    }
+                }
+                split8(v0, bh[nb][0], bl[nb][0]);
+                split8(v1, bh[nb][1], bl[nb][1]);
+            }
+            __syncthreads();
+            if (s + 1 < slabs) load_a(s + 1);
+#pragma unroll
+            for (int gi = 0; gi < 2; ++gi) {
+                half8 fbh[2], fbl[2];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, bh[nb][gi], acc[mb][nb], 0, 0, 0);
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, bl[nb][gi], acc[mb][nb], 0, 0, 0);
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, bh[nb][gi], acc[mb][nb], 0, 0, 0);
+                    fbh[nb] = __builtin_bit_cast(half8, bh[nb][gi]);
+                    fbl[nb] = __builtin_bit_cast(half8, bl[nb][gi]);
+                }
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const uint32_t ar = mb * 16u + (lane & 15u);
+                    const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
+                    const half8 a_h = *reinterpret_cast<const half8*>(&Ash[off]);
+                    const half8 a_l = *reinterpret_cast<const half8*>(&Asl[off]);
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, fbh[nb], acc[mb][nb], 0, 0, 0);
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, fbl[nb], acc[mb][nb], 0, 0, 0);
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, fbh[nb], acc[mb][nb], 0, 0, 0);
+                    }
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t m = mb * 16u + 4u * kq + j;
