@@ -381,6 +381,7 @@ struct ingot_layer {
     uint32_t *ids = nullptr, *counts = nullptr, *first = nullptr, *tiles = nullptr, *pairs = nullptr,
              *inverse = nullptr, *stiles = nullptr;
     _Float16 *xh = nullptr, *xl = nullptr, *acth = nullptr, *actl = nullptr;
+    float *xs = nullptr, *acts = nullptr;  // 32-column sums of x and act (Q4_K mins term)
     uint32_t tile_cap = 0, stile_cap = 0;
     std::function<void(hipStream_t)> stage[ST_N];
     const char* stage_name[ST_N] = {};
@@ -415,6 +416,7 @@ static int reserve(ingot_layer* L, uint32_t T) {
         {(void**)&L->inverse, 4ull * P},         {(void**)&L->stiles, 16ull * stile_cap},
         {(void**)&L->xh, 2ull * T * L->H},      {(void**)&L->xl, 2ull * T * L->H},
         {(void**)&L->acth, 2ull * P * L->F},     {(void**)&L->actl, 2ull * P * L->F},
+        {(void**)&L->xs, 4ull * T * (L->H / 32)}, {(void**)&L->acts, 4ull * P * (L->F / 32)},
     };
     uint64_t total = 0;
     for (auto& p : parts) total += (p.bytes + 255) & ~255ull;
@@ -929,13 +931,15 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch_count";
         _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
+        float *xs = L->xs, *acts = L->acts;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             if (f16) {
                 const uint64_t n = (uint64_t)T * H;
-                hipLaunchKernelGGL(k_split_f16, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256), 0, ss, xin, n, xh, xl);
-                hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(F / 64, cap), dim3(256), 0, ss, gate.d, up.d,
-                                   gate.stride, up.stride, F, H, xh, xl, pairs, K, tiles, F, limit, nullptr, acth,
-                                   actl);
+                hipLaunchKernelGGL(k_split_f16, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256), 0, ss, xin, n, xh, xl,
+                                   xs);
+                hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(8 * (F / 64) * ((cap + 7) / 8)), dim3(128), 0, ss,
+                                   gate.d, up.d, gate.stride, up.stride, F, H, xh, xl, xs, pairs, K, tiles, F, limit,
+                                   nullptr, acth, actl, acts, F / 64);
             } else {
                 launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
                                   pairs, K, tiles, F, limit, act);
@@ -947,8 +951,9 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         L->stage_name[ST_GATEUP] = f16 ? "k_gemm_q4k_f16<gate_up>" : "k_gemm<gate_up>";
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
             if (f16)
-                hipLaunchKernelGGL((k_gemm_q4k_f16<false>), dim3(H / 128, cap), dim3(256), 0, ss, down.d, nullptr,
-                                   down.stride, 0ull, H, F, acth, actl, nullptr, K, tiles, H, 0.f, Y, nullptr, nullptr);
+                hipLaunchKernelGGL((k_gemm_q4k_f16<false>), dim3(8 * (H / 128) * ((cap + 7) / 8)), dim3(128), 0, ss,
+                                   down.d, nullptr, down.stride, 0ull, H, F, acth, actl, acts, nullptr, K, tiles, H,
+                                   0.f, Y, nullptr, nullptr, nullptr, H / 128);
             else
                 launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act,
                                    nullptr, K, tiles, H, 0.f, Y);

@@ -631,8 +631,8 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
 // One block of 1024 threads, E <= 1024. Counts pairs per expert, writes
 // counts[E], first[E] (exclusive scan: experts ascending) and the tile list:
 // for each expert ceil(n/TM) tiles {expert, first pair of the tile, n in tile,
-// 0}, experts ascending, padded with zero tiles to cap (the layout of
-// kernels/prefill.metal:7-23 with TM-pair tiles).
+// number of non-empty tiles}, experts ascending, padded with zero tiles to cap
+// (the layout of kernels/prefill.metal:7-23 with TM-pair tiles).
 __global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
                                                          uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
                                                          uint32_t* __restrict__ first, uint32_t* __restrict__ tiles) {
@@ -657,13 +657,14 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restr
             tl[0] = tid;
             tl[1] = f + k * TM;
             tl[2] = min(TM, n - k * TM);
-            tl[3] = 0;
+            tl[3] = min(tot[1], cap);
         }
     }
     __syncthreads();
     for (uint32_t t = tot[1] + tid; t < cap; t += 1024u) {
         uint32_t* tl = tiles + 4u * t;
-        tl[0] = tl[1] = tl[2] = tl[3] = 0;
+        tl[0] = tl[1] = tl[2] = 0;
+        tl[3] = min(tot[1], cap);
     }
 }
 
@@ -840,181 +841,271 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
         }
 }
 
-// -------------------------------- prefill: split-precision f16 MFMA GEMM (Q4_K)
-// Same tiling and tile list as k_gemm, on v_mfma_f32_16x16x32_f16 with fp32
-// accumulation. Each operand is split into f16 hi + lo (v = hi + lo with
-// |v - hi - lo| <= 2^-22 |v| in the f16 normal range) and every product is
-// taken as hi*hi + hi*lo + lo*hi, so the result matches fp32 operands to about
-// 2^-21 relative while running at the f16 MFMA rate.
-//   A (inputs or activations) arrives pre-split in HBM (ah, al: [rows][kdim] f16)
-//   and is staged per 64-column slab in LDS.
-//   B (weights) is decoded by each wave straight into MFMA fragments: lane l
-//   owns row (l % 16) of an N-block and columns 8*(l/16)..+7 of each 32-column
-//   group; for Q4_K the slab's two groups are the low and high nibbles of the
-//   same 8 bytes (kernels/iq3_mix.metal:19-23 layout).
-// GATEUP writes act = SwiGLU(gate, up) already split (out_h, out_l: [P][F] f16);
-// the down GEMM writes fp32 Y.
+// -------------------------------- prefill: Q4_K grouped GEMM on f16 MFMA
+// Same tile list as k_gemm, computed on v_mfma_f32_16x16x32_f16 with fp32
+// accumulation and no loss against fp32 operands:
+//   * A (inputs or activations, fp32) arrives split in HBM as f16 hi + lo
+//     (ah, al: [rows][kdim], a = hi + lo to 2^-22 |a|) and is staged per
+//     64-column slab in LDS; both halves enter the MFMA.
+//   * B is not dequantised. A Q4_K weight is w = d sc_g q - dmin mn_g (q a
+//     nibble, sc_g and mn_g 6-bit integers of the 32-column group g, d and
+//     dmin f16 per 256-column superblock; ggml get_scale_min_k4,
+//     kernels/iq3_mix.metal:13-23). The MFMA takes the integer q sc_g <= 945
+//     as the raw bits of an f16 subnormal, i.e. the exact value q sc_g 2^-24,
+//     so one superblock accumulates sum_c a_c q_c sc_g(c) 2^-24 exactly up to
+//     fp32 rounding, in units of D = d 2^24.
+//   * The mins term dmin sum_g mn_g S_g, with S_g = sum of a over the group
+//     (precomputed per A row: gs [rows][kdim/32]), is one more MFMA per
+//     superblock: A = (S hi, S lo) of the 8 groups, B = mn_g as subnormals.
+//   * Between superblocks the accumulator moves from units D_sb to D_sb+1:
+//     acc = acc D_sb / D_sb+1 - macc Dmin_sb / D_sb+1 (D = 1 for the true units
+//     after the last superblock; a zero d gives D = 1 and zeroes B).
+// Block = 2 waves, tile of 64 tokens x 128 rows; wave tile 64 x 64 (4 x 4
+// MFMA tiles). Lane l owns B row (l % 16) of each 16-row block and columns
+// 8 (l / 16) .. + 7 of each 32-column group (the slab's two groups are the low
+// and high nibbles of the same 8 bytes).
+//   GATEUP: block b covers act columns 64 b..+63; wave w gate and up rows
+//   64 b + 32 w ..+31 (n-blocks 0,1 gate, 2,3 up). Writes act = SwiGLU split
+//   into out_h/out_l [P][F] and its 32-column sums out_gs [P][F/32].
+//   !GATEUP: block b covers rows 128 b..+127, wave w rows 128 b + 64 w..+63;
+//   writes fp32 Y [P][ldo].
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-constexpr uint32_t A16_STRIDE = 72;  // halves per LDS row: 64 + 8 pad (144 B) against bank conflicts
+typedef short short2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
     hi = (_Float16)v;
     lo = (_Float16)(v - (float)hi);
 }
 
-// 8 fp32 values -> f16 hi and lo halves (packed pairs, round toward zero:
-// hi = rtz(v), lo = rtz(v - hi), |v - hi - lo| < 2^-20 |v|).
-__device__ __forceinline__ void split8(const float* v, uint4& hi, uint4& lo) {
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const auto hp = __builtin_amdgcn_cvt_pkrtz(v[2 * i], v[2 * i + 1]);
-        const auto lp = __builtin_amdgcn_cvt_pkrtz(v[2 * i] - (float)hp[0], v[2 * i + 1] - (float)hp[1]);
-        h[i] = __builtin_bit_cast(uint32_t, hp);
-        l[i] = __builtin_bit_cast(uint32_t, lp);
-    }
-    hi = make_uint4(h[0], h[1], h[2], h[3]);
-    lo = make_uint4(l[0], l[1], l[2], l[3]);
+// Integer scales and mins of a Q4_K superblock header {d, dmin, scales[12]}:
+// byte j of sc03/mn03 holds sc_j/mn_j for j < 4, of sc47/mn47 for j + 4.
+__device__ __forceinline__ void q4k_sc_mn(uint4 h, uint32_t& sc03, uint32_t& sc47, uint32_t& mn03, uint32_t& mn47) {
+    sc03 = h.y & 0x3f3f3f3fu;
+    mn03 = h.z & 0x3f3f3f3fu;
+    sc47 = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    mn47 = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+}
+
+// Bytes 0,1 and 2,3 of w as two u16 pairs (perm selector 0x0c = zero byte).
+__device__ __forceinline__ uint32_t bytes01(uint32_t w) { return __builtin_amdgcn_perm(0u, w, 0x0c010c00u); }
+__device__ __forceinline__ uint32_t bytes23(uint32_t w) { return __builtin_amdgcn_perm(0u, w, 0x0c030c02u); }
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2v, a) * __builtin_bit_cast(short2v, b));
+}
+
+// 8 nibbles (already masked to 0x0f0f0f0f in lo4/hi4 bytes) times the
+// replicated scale scl2 = sc | sc << 16 -> half8 of subnormal f16 bits.
+__device__ __forceinline__ half8 q4_operand(uint32_t b0, uint32_t b1, uint32_t scl2) {
+    const uint4 v = make_uint4(mul_u16x2(bytes01(b0), scl2), mul_u16x2(bytes23(b0), scl2), mul_u16x2(bytes01(b1), scl2),
+                               mul_u16x2(bytes23(b1), scl2));
+    return __builtin_bit_cast(half8, v);
 }
 
 constexpr uint32_t TM16 = 64;  // tokens per tile of the f16 GEMM
 
 template <bool GATEUP>
-__global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
-                                                      uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
-                                                      uint32_t kdim, const _Float16* __restrict__ ah,
-                                                      const _Float16* __restrict__ al, const uint32_t* __restrict__ pairs,
-                                                      uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo,
-                                                      float limit, float* __restrict__ out, _Float16* __restrict__ out_h,
-                                                      _Float16* __restrict__ out_l) {
-    constexpr int MB = TM16 / 16;
-    // A tiles: 64 halves (128 B) per row, 16-byte chunk c of row r stored at
-    // chunk c ^ ((r >> 1) & 7): the stores (4 threads per row) and the MFMA
-    // fragment reads (16 rows at one chunk) then touch every bank once.
-    __shared__ _Float16 Ash[TM16 * 64];
-    __shared__ _Float16 Asl[TM16 * 64];
-    const uint32_t* tile = tiles + 4u * blockIdx.y;
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_q4k_f16(
+    const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, uint64_t stride0, uint64_t stride1,
+    uint32_t rows_per_expert, uint32_t kdim, const _Float16* __restrict__ ah, const _Float16* __restrict__ al,
+    const float* __restrict__ gs, const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles,
+    uint32_t ldo, float limit, float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l,
+    float* __restrict__ out_gs, uint32_t nblk) {
+    constexpr int MB = 4, NB = 4;
+    // A tiles, double-buffered by slab parity: 64 halves (128 B) per row,
+    // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7) so that the
+    // stores and the MFMA fragment reads (16 rows at one chunk) touch every
+    // bank once. S tiles double-buffered by superblock parity.
+    __shared__ _Float16 Ash[2][TM16 * 64];
+    __shared__ _Float16 Asl[2][TM16 * 64];
+    __shared__ _Float16 Ss[2][TM16 * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
+    // 1-D grid of 8 * nblk * ceil(cap / 8) blocks. The hardware deals blocks to
+    // the 8 XCDs round-robin (block h runs on XCD h % 8); XCD x takes the
+    // contiguous range [x per, (x + 1) per) of the non-empty tiles with all nblk
+    // row blocks of each tile, so a tile's A rows and its expert's weights are
+    // fetched into one XCD's L2 instead of into up to eight.
+    const uint32_t nt = tiles[3], per = (nt + 7u) >> 3, slot = blockIdx.x >> 3, ti = slot / nblk;
+    if (ti >= per) return;
+    const uint32_t t = (blockIdx.x & 7u) * per + ti;
+    if (t >= nt) return;
+    const uint32_t* tile = tiles + 4u * t;
     const uint32_t n = tile[2];
     if (n == 0) return;
     const uint32_t e = tile[0], q0 = tile[1];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, kq = lane >> 4;
-    const uint32_t row0 = blockIdx.x * (GATEUP ? 64u : 128u);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, kq = lane >> 4, ln = lane & 15u;
+    const uint32_t row0 = (slot - ti * nblk) * (GATEUP ? 64u : 128u);
+    const uint32_t ngroups = kdim / 32u;
 
-    // A loader: TM16 rows x 64 halves per part; thread -> row tid / (256 / TM16)
-    constexpr uint32_t TPR = 256u / TM16, HPT = 64u / TPR;  // threads per row, halves per thread
-    constexpr int AV = HPT / 8;                             // uint4 loads per part
-    const uint32_t am = tid / TPR, acol = HPT * (tid % TPR);
-    const _Float16 *arow_h = nullptr, *arow_l = nullptr;
-    if (am < n) {
-        const uint32_t q = q0 + am;
-        const uint64_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
-        arow_h = ah + r * kdim;
-        arow_l = al + r * kdim;
-    }
-    const uint8_t* brow[2];
+    const uint32_t ac = tid & 7u, ar0 = tid >> 3;
+    uint32_t aoff[4];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t m = ar0 + 16u * j;
+        const uint32_t q = q0 + (m < n ? m : 0u);
+        const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
+        aoff[j] = r * kdim + 8u * ac;
+    }
+    const uint32_t am = tid >> 1, ahalf = tid & 1u;
+    const float* srow;
+    {
+        const uint32_t q = q0 + (am < n ? am : 0u);
+        const uint64_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
+        srow = gs + r * ngroups + 4u * ahalf;
+    }
+    const uint8_t* brow[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
         if (GATEUP) {
-            const uint32_t r = row0 + 16u * wave + (lane & 15u);
-            brow[nb] = (nb == 0 ? w0 : w1) + ((uint64_t)e * rows_per_expert + r) * (nb == 0 ? stride0 : stride1);
+            const uint32_t r = row0 + 32u * wave + 16u * (nb & 1) + ln;
+            brow[nb] = (nb < 2 ? w0 : w1) + ((uint64_t)e * rows_per_expert + r) * (nb < 2 ? stride0 : stride1);
         } else {
-            const uint32_t r = row0 + 32u * wave + 16u * nb + (lane & 15u);
+            const uint32_t r = row0 + 64u * wave + 16u * nb + ln;
             brow[nb] = w0 + ((uint64_t)e * rows_per_expert + r) * stride0;
         }
     }
 
-    floatx4 acc[MB][2];
+    floatx4 acc[MB][NB];
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // A: one slab ahead (L2-resident inputs). B: one Q4_K superblock (4 slabs)
-    // ahead, because weights stream from HBM.
-    uint4 pa_h[AV], pa_l[AV];
-    auto load_a = [&](uint32_t s) {
-#pragma unroll
-        for (int i = 0; i < AV; ++i) {
-            pa_h[i] = arow_h ? *reinterpret_cast<const uint4*>(arow_h + 64u * s + acol + 8u * i) : make_uint4(0, 0, 0, 0);
-            pa_l[i] = arow_l ? *reinterpret_cast<const uint4*>(arow_l + 64u * s + acol + 8u * i) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    uint4 hdr[2], nhdr[2];
-    uint2 qs[2][4], nqs[2][4];
-    auto load_b = [&](uint32_t sb) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const uint8_t* b = brow[nb] + sb * 144u;
-            nhdr[nb] = *reinterpret_cast<const uint4*>(b);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) nqs[nb][q] = *reinterpret_cast<const uint2*>(b + 16u + 32u * q + 8u * kq);
-        }
-    };
     const uint32_t slabs = kdim / 64u, sbs = kdim / 256u;
-    load_a(0);
-    load_b(0);
+    // Loads past the last slab or superblock re-read the last one (uniform,
+    // branch-free, never used).
+    uint4 pa_h0, pa_h1, pa_h2, pa_h3, pa_l0, pa_l1, pa_l2, pa_l3;
+    const uint32_t aoff0 = aoff[0], aoff1 = aoff[1], aoff2 = aoff[2], aoff3 = aoff[3];
+#define INGOT_LOAD_A1(J, S_) pa_h##J = *reinterpret_cast<const uint4*>(ah + aoff##J + 64u * (S_)); pa_l##J = *reinterpret_cast<const uint4*>(al + aoff##J + 64u * (S_))
+#define INGOT_LOAD_A(S) do { const uint32_t s_ = (S) < slabs ? (S) : slabs - 1u; INGOT_LOAD_A1(0, s_); INGOT_LOAD_A1(1, s_); INGOT_LOAD_A1(2, s_); INGOT_LOAD_A1(3, s_); } while (0)
+    float4 ps;
+#define INGOT_LOAD_S(SB) ps = *reinterpret_cast<const float4*>(srow + 8u * ((SB) < sbs ? (SB) : sbs - 1u))
+    uint4 hdr[NB], nhdr[NB];
+    auto load_hdr = [&](uint32_t sb) {
+        sb = sb < sbs ? sb : sbs - 1u;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) nhdr[nb] = *reinterpret_cast<const uint4*>(brow[nb] + sb * 144u);
+    };
+    uint2 nqs[2][NB];  // B nibbles of slabs s + 1 and s + 2 (ring by slab parity)
+    auto load_qs = [&](uint2* dst, uint32_t s) {
+        s = s < slabs ? s : slabs - 1u;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            dst[nb] = *reinterpret_cast<const uint2*>(brow[nb] + (s >> 2) * 144u + 16u + 32u * (s & 3u) + 8u * kq);
+    };
+    // Superblock scale D = d 2^24 (1 and B zeroed when d == 0), Dmin = dmin 2^24.
+    auto dscale = [](uint4 h) {
+        const float d = half_bits_to_float(h.x);
+        return d != 0.f ? d * 16777216.f : 1.f;
+    };
+
+    load_hdr(0);
+    load_qs(nqs[0], 0);
+    load_qs(nqs[1], 1);
+    INGOT_LOAD_A(0u);
+    INGOT_LOAD_S(0u);
     for (uint32_t sb = 0; sb < sbs; ++sb) {
+        uint32_t sc[NB][2], mn[NB][2];
+        float dsc[NB], dmn[NB];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
+        for (int nb = 0; nb < NB; ++nb) {
             hdr[nb] = nhdr[nb];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) qs[nb][q] = nqs[nb][q];
+            q4k_sc_mn(hdr[nb], sc[nb][0], sc[nb][1], mn[nb][0], mn[nb][1]);
+            dsc[nb] = dscale(hdr[nb]);
+            dmn[nb] = half_bits_to_float(hdr[nb].x >> 16) * 16777216.f;
+            if (half_bits_to_float(hdr[nb].x) == 0.f) sc[nb][0] = sc[nb][1] = 0u;
         }
-        if (sb + 1 < sbs) load_b(sb + 1);
+        load_hdr(sb + 1);
+        _Float16* const sbuf = Ss[sb & 1u];
 #pragma unroll
         for (uint32_t sq = 0; sq < 4; ++sq) {
             const uint32_t s = 4u * sb + sq;
+            _Float16* const bh = Ash[sq & 1u];
+            _Float16* const bl = Asl[sq & 1u];
+            {
+                const uint4 vh[4] = {pa_h0, pa_h1, pa_h2, pa_h3}, vl[4] = {pa_l0, pa_l1, pa_l2, pa_l3};
 #pragma unroll
-            for (int i = 0; i < AV; ++i) {
-                const uint32_t off = am * 64u + 8u * (((acol >> 3) + i) ^ ((am >> 1) & 7u));
-                *reinterpret_cast<uint4*>(&Ash[off]) = pa_h[i];
-                *reinterpret_cast<uint4*>(&Asl[off]) = pa_l[i];
-            }
-            // This slab's B fragments: group 0 = low nibbles, group 1 = high nibbles.
-            uint4 bh[2][2], bl[2][2];
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                float d0, m0, d1, m1;
-                Fmt<12>::scales(hdr[nb], 2u * sq, d0, m0, d1, m1);
-                float v0[8], v1[8];
-                const uint32_t wq[2] = {qs[nb][sq].x, qs[nb][sq].y};
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t lo = wq[h] & 0x0f0f0f0fu, hi = (wq[h] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        v0[4 * h + j] = d0 * ubyte_f(lo, j) - m0;
-                        v1[4 * h + j] = d1 * ubyte_f(hi, j) - m1;
-                    }
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t r_ = ar0 + 16u * j;
+                    const uint32_t off = r_ * 64u + 8u * (ac ^ ((r_ >> 1) & 7u));
+                    *reinterpret_cast<uint4*>(&bh[off]) = vh[j];
+                    *reinterpret_cast<uint4*>(&bl[off]) = vl[j];
                 }
-                split8(v0, bh[nb][0], bl[nb][0]);
-                split8(v1, bh[nb][1], bl[nb][1]);
+            }
+            if (sq == 0) {
+                const float v[4] = {ps.x, ps.y, ps.z, ps.w};
+                _Float16 h[4], l[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
+                *reinterpret_cast<uint2*>(&sbuf[am * 16u + 4u * ahalf]) = make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
+                *reinterpret_cast<uint2*>(&sbuf[am * 16u + 8u + 4u * ahalf]) =
+                    make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
+                INGOT_LOAD_S(sb + 1u);
+            }
+            INGOT_LOAD_A(s + 1u);
+            // B operands of this slab: group 2 sq (low nibbles) and 2 sq + 1 (high nibbles).
+            uint2 qs[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) qs[nb] = nqs[sq & 1u][nb];
+            load_qs(nqs[sq & 1u], s + 2);
+            half8 fb[NB][2];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const uint32_t scw = sc[nb][sq >> 1] >> (16u * (sq & 1u));
+                const uint32_t s0 = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
+                const uint32_t s1 = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
+                fb[nb][0] = q4_operand(qs[nb].x & 0x0f0f0f0fu, qs[nb].y & 0x0f0f0f0fu, s0);
+                fb[nb][1] = q4_operand((qs[nb].x >> 4) & 0x0f0f0f0fu, (qs[nb].y >> 4) & 0x0f0f0f0fu, s1);
             }
             __syncthreads();
-            if (s + 1 < slabs) load_a(s + 1);
 #pragma unroll
-            for (int gi = 0; gi < 2; ++gi) {
-                half8 fbh[2], fbl[2];
+            for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    fbh[nb] = __builtin_bit_cast(half8, bh[nb][gi]);
-                    fbl[nb] = __builtin_bit_cast(half8, bl[nb][gi]);
+                for (int part = 0; part < 2; ++part)
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        const uint32_t ar = mb * 16u + ln;
+                        const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
+                        const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                    }
+            if (sq == 3) {
+                // Mins of the superblock and the move to the next superblock's units.
+                half8 fm[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint4 v = kq < 2 ? make_uint4(bytes01(mn[nb][0]), bytes23(mn[nb][0]), bytes01(mn[nb][1]),
+                                                        bytes23(mn[nb][1]))
+                                           : make_uint4(0, 0, 0, 0);
+                    fm[nb] = __builtin_bit_cast(half8, v);
                 }
+                float f1[NB], f2[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const float rn = sb + 1 < sbs ? __builtin_amdgcn_rcpf(dscale(nhdr[nb])) : 1.f;
+                    f1[nb] = dsc[nb] * rn;
+                    f2[nb] = -dmn[nb] * rn;
+                }
+                // Four independent MFMAs per row block before their results are
+                // used, so the updates do not wait on each MFMA in turn.
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
-                    const uint32_t ar = mb * 16u + (lane & 15u);
-                    const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
-                    const half8 a_h = *reinterpret_cast<const half8*>(&Ash[off]);
-                    const half8 a_l = *reinterpret_cast<const half8*>(&Asl[off]);
+                    const half8 sa = *reinterpret_cast<const half8*>(&sbuf[(mb * 16u + ln) * 16u + 8u * (kq & 1u)]);
+                    floatx4 mc[NB];
 #pragma unroll
-                    for (int nb = 0; nb < 2; ++nb) {
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, fbh[nb], acc[mb][nb], 0, 0, 0);
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, fbl[nb], acc[mb][nb], 0, 0, 0);
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, fbh[nb], acc[mb][nb], 0, 0, 0);
-                    }
+                    for (int nb = 0; nb < NB; ++nb)
+                        mc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, fm[nb], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[mb][nb][j] = acc[mb][nb][j] * f1[nb] + mc[nb][j] * f2[nb];
                 }
             }
-            __syncthreads();
         }
     }
 #pragma unroll
@@ -1022,30 +1113,56 @@ __global__ __launch_bounds__(256) void k_gemm_q4k_f16(const uint8_t* __restrict_
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t m = mb * 16u + 4u * kq + j;
-            if (m >= n) continue;
             const uint64_t q = q0 + m;
             if (GATEUP) {
-                const uint32_t r = row0 + 16u * wave + (lane & 15u);
-                _Float16 xh, xl;
-                split_f16(swiglu(acc[mb][0][j], acc[mb][1][j], limit), xh, xl);
-                out_h[q * ldo + r] = xh;
-                out_l[q * ldo + r] = xl;
-            } else {
+                float gsum = 0.f;
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) out[q * ldo + row0 + 32u * wave + 16u * nb + (lane & 15u)] = acc[mb][nb][j];
+                for (int c = 0; c < 2; ++c) {
+                    const uint32_t r = row0 + 32u * wave + 16u * c + ln;
+                    const float v = swiglu(acc[mb][c][j], acc[mb][2 + c][j], limit);
+                    gsum += v;
+                    _Float16 xh, xl;
+                    split_f16(v, xh, xl);
+                    if (m < n) {
+                        out_h[q * ldo + r] = xh;
+                        out_l[q * ldo + r] = xl;
+                    }
+                }
+                // 32-column sum of act over this wave's columns (16 lanes x 2).
+                gsum += dpp_mov<0xb1>(gsum);
+                gsum += dpp_mov<0x4e>(gsum);
+                gsum += dpp_mov<0x141>(gsum);
+                gsum += dpp_mov<0x140>(gsum);
+                if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
+            } else {
+                if (m < n) {
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) out[q * ldo + row0 + 64u * wave + 16u * nb + ln] = acc[mb][nb][j];
+                }
             }
         }
+#undef INGOT_LOAD_A
+#undef INGOT_LOAD_S
 }
 
-// x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)).
-__global__ void k_split_f16(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
-                            _Float16* __restrict__ xl) {
+// x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)) and
+// the 32-column sums xs [T][H/32] used by the Q4_K mins term.
+__global__ __launch_bounds__(256) void k_split_f16(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
+                                                   _Float16* __restrict__ xl, float* __restrict__ xs) {
     const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4u;
-    if (i >= n) return;
-    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    const bool live = i < n;
+    const float4 v = live ? *reinterpret_cast<const float4*>(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float a[4] = {v.x, v.y, v.z, v.w};
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) split_f16(a[j], xh[i + j], xl[i + j]);
+        for (int j = 0; j < 4; ++j) split_f16(a[j], xh[i + j], xl[i + j]);
+    }
+    // 8 consecutive threads cover one 32-column group (n is a multiple of 32).
+    float s = (a[0] + a[1]) + (a[2] + a[3]);
+    s += dpp_mov<0xb1>(s);
+    s += dpp_mov<0x4e>(s);
+    s += dpp_mov<0x141>(s);
+    if (live && (threadIdx.x & 7u) == 0) xs[i / 32u] = s;
 }
 
 // Dense token tiles for the shared expert: tile t = {0, 64 t, min(64, T - 64 t), 0}.
@@ -1056,7 +1173,7 @@ __global__ void k_dense_tiles(uint32_t T, uint32_t cap, uint32_t* __restrict__ t
     tiles[4 * t] = 0;
     tiles[4 * t + 1] = first < T ? first : 0;
     tiles[4 * t + 2] = first < T ? min(TM, T - first) : 0;
-    tiles[4 * t + 3] = 0;
+    tiles[4 * t + 3] = min(cap, (T + TM - 1) / TM);
 }
 
 // ------------------------------------------------------- prefill: combine
