@@ -15,7 +15,9 @@ is already resident in HBM:
   copies, reported in the "decode" object.
 * roofline: the dominant kernel of the prefill step (the stage with the
   largest time), timed live by graph-captured replays with HIP events on the
-  stream it runs on; achieved = its algorithmic FLOPs (or bytes) / duration.
+  stream it runs on; achieved = its algorithmic FLOPs / duration, priced
+  against the dense fp16 MFMA peak (the instructions it issues); traffic = its
+  HBM bytes per launch from the committed rocprofv3 PMC summary in profiles/.
 * cpu_baseline: the C++ CPU restatement of the layer (oracle/liboracle.so,
   fp32 accumulation, one thread per available core) timed on a bounded sample
   of the same workload. The reference (Rust + Metal) cannot run on Linux.
@@ -35,6 +37,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, the datatype the prefill GEMMs issue
+PROFILES = os.path.join(ROOT, "profiles")
 
 
 def log(*a):
@@ -98,6 +102,57 @@ def time_stages(layers, dx, T, dout, reps):
     return out
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against the plain copy kernel), or None."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(PROFILES, "*_pmc.md"))):
+        text = open(path).read()
+        if f"kernel: {kernel}" not in text:
+            continue
+        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+        if m:
+            return int(m.group(1)), os.path.relpath(path, ROOT)
+    return None, None
+
+
+def profile_workload(args):
+    """A short eager workload for rocprofv3 (--kernel-trace or --pmc): C1 prefill
+    forwards over 8 weight copies, C0 decode forwards over 32 copies, then one
+    256 MiB device copy by the plain copy kernel (the counter calibration)."""
+    from ingot_amd import configs as CF
+    from ingot_amd.moe import Gpu, MoeLayer
+    gpu = Gpu(0)
+    base = MoeLayer(gpu, CF.c1_layer())
+    layers = [base] + [base.clone() for _ in range(args.copies - 1)]
+    dx = gpu.to_device(CF.inputs(1, 512, 2048))
+    dout = gpu.buffer(4 * 512 * 2048)
+    for rep in range(2):
+        for l in layers:
+            l.forward(dx, 512, dout)
+    gpu.synchronize()
+    log("profile: prefill done")
+    for l in layers:
+        l.destroy()
+    d0 = MoeLayer(gpu, CF.c0_layer())
+    dl = [d0] + [d0.clone() for _ in range(args.decode_copies - 1)]
+    dx0 = gpu.to_device(CF.inputs(0, 1, 2048))
+    dout0 = gpu.buffer(4 * 2048)
+    for rep in range(2):
+        for l in dl:
+            l.forward(dx0, 1, dout0)
+    gpu.synchronize()
+    log("profile: decode done")
+    n = 256 << 20
+    a, b = gpu.buffer(n), gpu.buffer(n)
+    a.upload(np.zeros(n // 4, np.float32))
+    b.copy_from(a, n)
+    b.copy_from(a, n)
+    gpu.synchronize()
+    log("profile: calibration copy of 256 MiB done")
+
+
 def cpu_baseline(spec, x, budget_s, label):
     from oracle import pyoracle as O
     cores = len(os.sched_getaffinity(0))
@@ -125,11 +180,17 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--profile", action="store_true",
+                    help="run only a short eager workload for rocprofv3 and exit (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.profile:
+        profile_workload(args)
+        return
 
     from ingot_amd import configs as CF
     from ingot_amd.moe import Gpu, MoeLayer
@@ -160,6 +221,7 @@ def main():
     dom = max(("gate_up", "down"), key=lambda k: stages[k]["us"])
     dflops = work[dom]["flops"]
     achieved = dflops / (stages[dom]["us"] * 1e-6) / 1e12
+    traffic, traffic_src = measured_traffic(stages[dom]["kernel"])
     layer_tflops = work["layer"]["flops"] / (ms_step * 1e-3) / 1e12
 
     # ---------------- decode b=1 ----------------
@@ -218,9 +280,14 @@ def main():
                    "hidden": 2048, "experts": 128, "top_k": 8, "ffn": 768, "tokens": T, "format": "Q4_K",
                    "weight_copies": args.copies, "experts_touched": work["layer"]["touched"]},
         "roofline": {"bound": "mfma", "kernel": stages[dom]["kernel"], "achieved": achieved,
-                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS,
-                     "traffic": None, "kernel_us": stages[dom]["us"], "algorithmic_flops": dflops},
-        "layer_mfma_frac": layer_tflops / MFMA_F32_PEAK_TFLOPS,
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / MFMA_F16_PEAK_TFLOPS,
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel_us": stages[dom]["us"], "algorithmic_flops": dflops,
+                     "issued_f16_frac": 2.0 * achieved / MFMA_F16_PEAK_TFLOPS,
+                     "frac_vs_fp32_mfma_peak": achieved / MFMA_F32_PEAK_TFLOPS,
+                     "note": "fp32-accurate products as two f16 MFMA products (A hi and lo) with fp32 "
+                             "accumulation; peak = dense fp16 MFMA"},
+        "layer_frac_vs_fp32_mfma_peak": layer_tflops / MFMA_F32_PEAK_TFLOPS,
         "stages_us": {k: round(v["us"], 2) for k, v in stages.items()},
         "decode": decode,
         "cpu_baseline": cpu,

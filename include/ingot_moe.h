@@ -205,6 +205,11 @@ int ingot_malloc(ingot_ctx* ctx, uint64_t bytes, void** d_ptr);
 int ingot_free(ingot_ctx* ctx, void* d_ptr);
 int ingot_memcpy_h2d(ingot_ctx* ctx, void* d_dst, const void* h_src, uint64_t bytes);
 int ingot_memcpy_d2h(ingot_ctx* ctx, void* h_dst, const void* d_src, uint64_t bytes);
+/* Device-to-device copy by a plain streaming HIP kernel (16 bytes per lane,
+ * bytes a multiple of 16). No counterpart in the reference: it is the known-size
+ * workload against which hardware byte counters (FETCH_SIZE, WRITE_SIZE) are
+ * calibrated. */
+int ingot_device_copy(ingot_ctx* ctx, void* d_dst, const void* d_src, uint64_t bytes);
 
 #ifdef __cplusplus
 }

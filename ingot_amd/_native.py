@@ -104,6 +104,7 @@ MOE_SYMBOLS = {
     "ingot_free": (I32, [P, P]),
     "ingot_memcpy_h2d": (I32, [P, P, P, U64]),
     "ingot_memcpy_d2h": (I32, [P, P, P, U64]),
+    "ingot_device_copy": (I32, [P, P, P, U64]),
 }
 
 SYNTH_SYMBOLS = {

@@ -4,6 +4,7 @@
 // and event timing. Kernels live in moe_kernels.cuh.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -542,6 +543,19 @@ int ingot_memcpy_d2h(ingot_ctx* ctx, void* h_dst, const void* d_src, uint64_t by
     return INGOT_OK;
 }
 
+int ingot_device_copy(ingot_ctx* ctx, void* d_dst, const void* d_src, uint64_t bytes) {
+    CHECK_CTX(ctx);
+    if ((bytes & 15u) || !d_dst || !d_src) return fail(ctx, INGOT_INVALID, "device_copy: bytes must be a multiple of 16");
+    const uint64_t n16 = bytes / 16u;
+    if (n16 == 0) return INGOT_OK;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((n16 + 255u) / 256u, 65536u);
+    hipLaunchKernelGGL(k_copy16, dim3(blocks), dim3(256), 0, ctx->stream, static_cast<uint4*>(d_dst),
+                       static_cast<const uint4*>(d_src), n16);
+    LAUNCH_CHECK(ctx);
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return INGOT_OK;
+}
+
 // ---- route() drop-in (src/lib.rs:43-60) ----
 int ingot_route(ingot_ctx* ctx, const float* logits, uint32_t E, uint32_t K, uint32_t* ids, float* weights) {
     if (!logits || !ids || !weights || K == 0 || K > E) return fail(ctx, INGOT_INVALID, "invalid router scores or expert count");
@@ -924,19 +938,23 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         bool hs = L->has_shared;
         const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && gate.kind == 12 && down.kind == 12;
         const uint32_t tm = f16 ? TM16 : TM;
+        _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
+        float *xs = L->xs, *acts = L->acts;
+        // Dispatch stage: expert grouping, and for the f16 GEMM the split of x
+        // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
             hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, cap, counts, first, tiles);
             hipLaunchKernelGGL(k_dispatch_place, dim3(E), dim3(256), 0, ss, ids, P, counts, first, pairs, inverse);
             if (hs) hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
-        };
-        L->stage_name[ST_DISPATCH] = "k_dispatch_count";
-        _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
-        float *xs = L->xs, *acts = L->acts;
-        L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             if (f16) {
                 const uint64_t n = (uint64_t)T * H;
                 hipLaunchKernelGGL(k_split_f16, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256), 0, ss, xin, n, xh, xl,
                                    xs);
+            }
+        };
+        L->stage_name[ST_DISPATCH] = "k_dispatch_count";
+        L->stage[ST_GATEUP] = [=](hipStream_t ss) {
+            if (f16) {
                 hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(8 * (F / 64) * ((cap + 7) / 8)), dim3(128), 0, ss,
                                    gate.d, up.d, gate.stride, up.stride, F, H, xh, xl, xs, pairs, K, tiles, F, limit,
                                    nullptr, acth, actl, acts, F / 64);

@@ -1165,6 +1165,12 @@ __global__ __launch_bounds__(256) void k_split_f16(const float* __restrict__ x, 
     if (live && (threadIdx.x & 7u) == 0) xs[i / 32u] = s;
 }
 
+// Plain grid-stride copy of n16 16-byte words (counter calibration workload).
+__global__ __launch_bounds__(256) void k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
 // Dense token tiles for the shared expert: tile t = {0, 64 t, min(64, T - 64 t), 0}.
 __global__ void k_dense_tiles(uint32_t T, uint32_t cap, uint32_t* __restrict__ tiles) {
     uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;

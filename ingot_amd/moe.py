@@ -132,6 +132,11 @@ class DeviceBuffer:
         self.gpu._check(self.gpu.lib.ingot_memcpy_d2h(self.gpu.ctx, out.ctypes.data, self.ptr, out.nbytes))
         return out
 
+    def copy_from(self, src: "DeviceBuffer", nbytes: int) -> None:
+        """Device-to-device copy by a plain HIP kernel (ingot_device_copy)."""
+        assert nbytes <= min(self.nbytes, src.nbytes)
+        self.gpu._check(self.gpu.lib.ingot_device_copy(self.gpu.ctx, self.ptr, src.ptr, int(nbytes)))
+
     def free(self) -> None:
         if self.ptr:
             self.gpu.lib.ingot_free(self.gpu.ctx, self.ptr)
