@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "det_math.h"
 #include "formats.cuh"
 
@@ -629,42 +631,68 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
 }
 
 // One block of 1024 threads, E <= 1024. Counts pairs per expert, writes
-// counts[E], first[E] (exclusive scan: experts ascending) and the tile list:
-// for each expert ceil(n/TM) tiles {expert, first pair of the tile, n in tile,
-// number of non-empty tiles}, experts ascending, padded with zero tiles to cap
-// (the layout of kernels/prefill.metal:7-23 with TM-pair tiles).
+// counts[E], first[E] (exclusive scan: experts ascending) and the tile list of
+// TM-pair tiles {expert, first pair of the tile, n in tile, number of
+// non-empty tiles} (the layout of kernels/prefill.metal:7-23), padded with
+// zero tiles to cap. Order: every expert's full tiles (experts ascending),
+// then the partial last tiles by decreasing n, so that work scheduled last is
+// the cheapest. Results do not depend on the order: each tile's rows are
+// computed independently.
 __global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
                                                          uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
                                                          uint32_t* __restrict__ first, uint32_t* __restrict__ tiles) {
     __shared__ uint32_t cnt[1024];
     __shared__ uint32_t wsum[32];
-    __shared__ uint32_t tot[2];
+    __shared__ uint32_t tot[3];
+    __shared__ uint32_t rbin[1024];  // partial tiles per remainder, then their start positions
     const uint32_t tid = threadIdx.x;
     cnt[tid] = 0;
+    rbin[tid] = 0;
     __syncthreads();
     for (uint32_t p = tid; p < P; p += 1024u) atomicAdd(&cnt[ids[p]], 1u);
     __syncthreads();
-    uint32_t n = tid < E ? cnt[tid] : 0u;
-    uint32_t nt = (n + TM - 1) / TM;
-    uint32_t f = block_exclusive_scan_1024(n, wsum, &tot[0]);
+    const uint32_t n = tid < E ? cnt[tid] : 0u;
+    const uint32_t nfull = n / TM, rem = n - nfull * TM;
+    const uint32_t f = block_exclusive_scan_1024(n, wsum, &tot[0]);
     __syncthreads();
-    uint32_t t0 = block_exclusive_scan_1024(nt, wsum, &tot[1]);
+    const uint32_t t0 = block_exclusive_scan_1024(nfull, wsum, &tot[1]);  // full tiles
+    if (rem) atomicAdd(&rbin[rem], 1u);
+    __syncthreads();
+    // Start of each remainder's run among the partial tiles (larger remainders
+    // first): exclusive scan over remainders TM-1 .. 1.
+    const uint32_t rr = tid < TM ? TM - 1u - tid : 0u;  // thread tid handles remainder rr
+    const uint32_t c = (tid < TM && rr > 0) ? rbin[rr] : 0u;
+    const uint32_t before = block_exclusive_scan_1024(c, wsum, &tot[2]);
+    const uint32_t nt_all = tot[2];
+    __syncthreads();
+    if (tid < TM && rr > 0) rbin[rr] = tot[1] + before;
+    __syncthreads();
+    const uint32_t ntiles = min(tot[1] + nt_all, cap);
     if (tid < E) {
         counts[tid] = n;
         first[tid] = f;
-        for (uint32_t k = 0; k < nt && t0 + k < cap; ++k) {
+        for (uint32_t k = 0; k < nfull && t0 + k < cap; ++k) {
             uint32_t* tl = tiles + 4u * (t0 + k);
             tl[0] = tid;
             tl[1] = f + k * TM;
-            tl[2] = min(TM, n - k * TM);
-            tl[3] = min(tot[1], cap);
+            tl[2] = TM;
+            tl[3] = ntiles;
+        }
+        if (rem) {
+            const uint32_t t = atomicAdd(&rbin[rem], 1u);
+            if (t < cap) {
+                uint32_t* tl = tiles + 4u * t;
+                tl[0] = tid;
+                tl[1] = f + nfull * TM;
+                tl[2] = rem;
+                tl[3] = ntiles;
+            }
         }
     }
-    __syncthreads();
-    for (uint32_t t = tot[1] + tid; t < cap; t += 1024u) {
+    for (uint32_t t = tot[1] + nt_all + tid; t < cap; t += 1024u) {
         uint32_t* tl = tiles + 4u * t;
         tl[0] = tl[1] = tl[2] = 0;
-        tl[3] = min(tot[1], cap);
+        tl[3] = ntiles;
     }
 }
 
@@ -915,7 +943,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const float* __restrict__ gs, const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles,
     uint32_t ldo, float limit, float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l,
     float* __restrict__ out_gs, uint32_t nblk) {
-    constexpr int MB = 4, NB = 4;
+    constexpr int NB = 4;
     // A tiles, double-buffered by slab parity: 64 halves (128 B) per row,
     // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7) so that the
     // stores and the MFMA fragment reads (16 rows at one chunk) touch every
@@ -924,13 +952,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     __shared__ _Float16 Asl[2][TM16 * 64];
     __shared__ _Float16 Ss[2][TM16 * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
     // 1-D grid of 8 * nblk * ceil(cap / 8) blocks. The hardware deals blocks to
-    // the 8 XCDs round-robin (block h runs on XCD h % 8); XCD x takes the
-    // contiguous range [x per, (x + 1) per) of the non-empty tiles with all nblk
-    // row blocks of each tile, so a tile's A rows and its expert's weights are
-    // fetched into one XCD's L2 instead of into up to eight.
-    const uint32_t nt = tiles[3], per = (nt + 7u) >> 3, slot = blockIdx.x >> 3, ti = slot / nblk;
-    if (ti >= per) return;
-    const uint32_t t = (blockIdx.x & 7u) * per + ti;
+    // the 8 XCDs round-robin (block h runs on XCD h % 8); XCD x takes tiles
+    // x, x + 8, x + 16, ... in list order (full tiles first, then partial
+    // tiles by decreasing size) with all nblk row blocks of each tile, so a
+    // tile's A rows are fetched into one XCD's L2 and the blocks each XCD
+    // runs last are its smallest tiles.
+    const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk;
+    const uint32_t t = ti * 8u + (blockIdx.x & 7u);
     if (t >= nt) return;
     const uint32_t* tile = tiles + 4u * t;
     const uint32_t n = tile[2];
@@ -968,11 +996,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     }
 
-    floatx4 acc[MB][NB];
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const uint32_t slabs = kdim / 64u, sbs = kdim / 256u;
     // Loads past the last slab or superblock re-read the last one (uniform,
@@ -1002,145 +1025,161 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         return d != 0.f ? d * 16777216.f : 1.f;
     };
 
-    load_hdr(0);
-    load_qs(nqs[0], 0);
-    load_qs(nqs[1], 1);
-    INGOT_LOAD_A(0u);
-    INGOT_LOAD_S(0u);
-    for (uint32_t sb = 0; sb < sbs; ++sb) {
-        uint32_t sc[NB][2], mn[NB][2];
-        float dsc[NB], dmn[NB];
+    // Only the first ceil(n / 16) 16-row blocks of the tile issue MFMAs; the
+    // main loop is instantiated for 1..4 active row blocks.
+    auto run = [&](auto mbe_tag) {
+        constexpr int MBE = decltype(mbe_tag)::value;
+        floatx4 acc[MBE][NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            hdr[nb] = nhdr[nb];
-            q4k_sc_mn(hdr[nb], sc[nb][0], sc[nb][1], mn[nb][0], mn[nb][1]);
-            dsc[nb] = dscale(hdr[nb]);
-            dmn[nb] = half_bits_to_float(hdr[nb].x >> 16) * 16777216.f;
-            if (half_bits_to_float(hdr[nb].x) == 0.f) sc[nb][0] = sc[nb][1] = 0u;
-        }
-        load_hdr(sb + 1);
-        _Float16* const sbuf = Ss[sb & 1u];
+        for (int i = 0; i < MBE; ++i)
 #pragma unroll
-        for (uint32_t sq = 0; sq < 4; ++sq) {
-            const uint32_t s = 4u * sb + sq;
-            _Float16* const bh = Ash[sq & 1u];
-            _Float16* const bl = Asl[sq & 1u];
-            {
-                const uint4 vh[4] = {pa_h0, pa_h1, pa_h2, pa_h3}, vl[4] = {pa_l0, pa_l1, pa_l2, pa_l3};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t r_ = ar0 + 16u * j;
-                    const uint32_t off = r_ * 64u + 8u * (ac ^ ((r_ >> 1) & 7u));
-                    *reinterpret_cast<uint4*>(&bh[off]) = vh[j];
-                    *reinterpret_cast<uint4*>(&bl[off]) = vl[j];
-                }
-            }
-            if (sq == 0) {
-                const float v[4] = {ps.x, ps.y, ps.z, ps.w};
-                _Float16 h[4], l[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
-                *reinterpret_cast<uint2*>(&sbuf[am * 16u + 4u * ahalf]) = make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
-                *reinterpret_cast<uint2*>(&sbuf[am * 16u + 8u + 4u * ahalf]) =
-                    make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
-                INGOT_LOAD_S(sb + 1u);
-            }
-            INGOT_LOAD_A(s + 1u);
-            // B operands of this slab: group 2 sq (low nibbles) and 2 sq + 1 (high nibbles).
-            uint2 qs[NB];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) qs[nb] = nqs[sq & 1u][nb];
-            load_qs(nqs[sq & 1u], s + 2);
-            half8 fb[NB][2];
-#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        load_hdr(0);
+        load_qs(nqs[0], 0);
+        load_qs(nqs[1], 1);
+        INGOT_LOAD_A(0u);
+        INGOT_LOAD_S(0u);
+        for (uint32_t sb = 0; sb < sbs; ++sb) {
+            uint32_t sc[NB][2], mn[NB][2];
+            float dsc[NB], dmn[NB];
+    #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const uint32_t scw = sc[nb][sq >> 1] >> (16u * (sq & 1u));
-                const uint32_t s0 = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
-                const uint32_t s1 = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
-                fb[nb][0] = q4_operand(qs[nb].x & 0x0f0f0f0fu, qs[nb].y & 0x0f0f0f0fu, s0);
-                fb[nb][1] = q4_operand((qs[nb].x >> 4) & 0x0f0f0f0fu, (qs[nb].y >> 4) & 0x0f0f0f0fu, s1);
+                hdr[nb] = nhdr[nb];
+                q4k_sc_mn(hdr[nb], sc[nb][0], sc[nb][1], mn[nb][0], mn[nb][1]);
+                dsc[nb] = dscale(hdr[nb]);
+                dmn[nb] = half_bits_to_float(hdr[nb].x >> 16) * 16777216.f;
+                if (half_bits_to_float(hdr[nb].x) == 0.f) sc[nb][0] = sc[nb][1] = 0u;
             }
-            __syncthreads();
-#pragma unroll
-            for (int gi = 0; gi < 2; ++gi)
-#pragma unroll
-                for (int part = 0; part < 2; ++part)
-#pragma unroll
-                    for (int mb = 0; mb < MB; ++mb) {
-                        const uint32_t ar = mb * 16u + ln;
-                        const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
-                        const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
-#pragma unroll
+            load_hdr(sb + 1);
+            _Float16* const sbuf = Ss[sb & 1u];
+    #pragma unroll
+            for (uint32_t sq = 0; sq < 4; ++sq) {
+                const uint32_t s = 4u * sb + sq;
+                _Float16* const bh = Ash[sq & 1u];
+                _Float16* const bl = Asl[sq & 1u];
+                {
+                    const uint4 vh[4] = {pa_h0, pa_h1, pa_h2, pa_h3}, vl[4] = {pa_l0, pa_l1, pa_l2, pa_l3};
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t r_ = ar0 + 16u * j;
+                        const uint32_t off = r_ * 64u + 8u * (ac ^ ((r_ >> 1) & 7u));
+                        *reinterpret_cast<uint4*>(&bh[off]) = vh[j];
+                        *reinterpret_cast<uint4*>(&bl[off]) = vl[j];
+                    }
+                }
+                if (sq == 0) {
+                    const float v[4] = {ps.x, ps.y, ps.z, ps.w};
+                    _Float16 h[4], l[4];
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
+                    *reinterpret_cast<uint2*>(&sbuf[am * 16u + 4u * ahalf]) = make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
+                    *reinterpret_cast<uint2*>(&sbuf[am * 16u + 8u + 4u * ahalf]) =
+                        make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
+                    INGOT_LOAD_S(sb + 1u);
+                }
+                INGOT_LOAD_A(s + 1u);
+                // B operands of this slab: group 2 sq (low nibbles) and 2 sq + 1 (high nibbles).
+                uint2 qs[NB];
+    #pragma unroll
+                for (int nb = 0; nb < NB; ++nb) qs[nb] = nqs[sq & 1u][nb];
+                load_qs(nqs[sq & 1u], s + 2);
+                half8 fb[NB][2];
+    #pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t scw = sc[nb][sq >> 1] >> (16u * (sq & 1u));
+                    const uint32_t s0 = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
+                    const uint32_t s1 = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
+                    fb[nb][0] = q4_operand(qs[nb].x & 0x0f0f0f0fu, qs[nb].y & 0x0f0f0f0fu, s0);
+                    fb[nb][1] = q4_operand((qs[nb].x >> 4) & 0x0f0f0f0fu, (qs[nb].y >> 4) & 0x0f0f0f0fu, s1);
+                }
+                __syncthreads();
+    #pragma unroll
+                for (int gi = 0; gi < 2; ++gi)
+    #pragma unroll
+                    for (int part = 0; part < 2; ++part)
+    #pragma unroll
+                        for (int mb = 0; mb < MBE; ++mb) {
+                            const uint32_t ar = mb * 16u + ln;
+                            const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
+                            const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
+    #pragma unroll
+                            for (int nb = 0; nb < NB; ++nb)
+                                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                        }
+                if (sq == 3) {
+                    // Mins of the superblock and the move to the next superblock's units.
+                    half8 fm[NB];
+    #pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) {
+                        const uint4 v = kq < 2 ? make_uint4(bytes01(mn[nb][0]), bytes23(mn[nb][0]), bytes01(mn[nb][1]),
+                                                            bytes23(mn[nb][1]))
+                                               : make_uint4(0, 0, 0, 0);
+                        fm[nb] = __builtin_bit_cast(half8, v);
+                    }
+                    float f1[NB], f2[NB];
+    #pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) {
+                        const float rn = sb + 1 < sbs ? __builtin_amdgcn_rcpf(dscale(nhdr[nb])) : 1.f;
+                        f1[nb] = dsc[nb] * rn;
+                        f2[nb] = -dmn[nb] * rn;
+                    }
+                    // Four independent MFMAs per row block before their results are
+                    // used, so the updates do not wait on each MFMA in turn.
+    #pragma unroll
+                    for (int mb = 0; mb < MBE; ++mb) {
+                        const half8 sa = *reinterpret_cast<const half8*>(&sbuf[(mb * 16u + ln) * 16u + 8u * (kq & 1u)]);
+                        floatx4 mc[NB];
+    #pragma unroll
                         for (int nb = 0; nb < NB; ++nb)
-                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                            mc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, fm[nb], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    #pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+    #pragma unroll
+                            for (int j = 0; j < 4; ++j) acc[mb][nb][j] = acc[mb][nb][j] * f1[nb] + mc[nb][j] * f2[nb];
                     }
-            if (sq == 3) {
-                // Mins of the superblock and the move to the next superblock's units.
-                half8 fm[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const uint4 v = kq < 2 ? make_uint4(bytes01(mn[nb][0]), bytes23(mn[nb][0]), bytes01(mn[nb][1]),
-                                                        bytes23(mn[nb][1]))
-                                           : make_uint4(0, 0, 0, 0);
-                    fm[nb] = __builtin_bit_cast(half8, v);
-                }
-                float f1[NB], f2[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const float rn = sb + 1 < sbs ? __builtin_amdgcn_rcpf(dscale(nhdr[nb])) : 1.f;
-                    f1[nb] = dsc[nb] * rn;
-                    f2[nb] = -dmn[nb] * rn;
-                }
-                // Four independent MFMAs per row block before their results are
-                // used, so the updates do not wait on each MFMA in turn.
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    const half8 sa = *reinterpret_cast<const half8*>(&sbuf[(mb * 16u + ln) * 16u + 8u * (kq & 1u)]);
-                    floatx4 mc[NB];
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-                        mc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, fm[nb], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) acc[mb][nb][j] = acc[mb][nb][j] * f1[nb] + mc[nb][j] * f2[nb];
                 }
             }
         }
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t m = mb * 16u + 4u * kq + j;
-            const uint64_t q = q0 + m;
-            if (GATEUP) {
-                float gsum = 0.f;
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const uint32_t r = row0 + 32u * wave + 16u * c + ln;
-                    const float v = swiglu(acc[mb][c][j], acc[mb][2 + c][j], limit);
-                    gsum += v;
-                    _Float16 xh, xl;
-                    split_f16(v, xh, xl);
+    #pragma unroll
+        for (int mb = 0; mb < MBE; ++mb)
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t m = mb * 16u + 4u * kq + j;
+                const uint64_t q = q0 + m;
+                if (GATEUP) {
+                    float gsum = 0.f;
+    #pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const uint32_t r = row0 + 32u * wave + 16u * c + ln;
+                        const float v = swiglu(acc[mb][c][j], acc[mb][2 + c][j], limit);
+                        gsum += v;
+                        _Float16 xh, xl;
+                        split_f16(v, xh, xl);
+                        if (m < n) {
+                            out_h[q * ldo + r] = xh;
+                            out_l[q * ldo + r] = xl;
+                        }
+                    }
+                    // 32-column sum of act over this wave's columns (16 lanes x 2).
+                    gsum += dpp_mov<0xb1>(gsum);
+                    gsum += dpp_mov<0x4e>(gsum);
+                    gsum += dpp_mov<0x141>(gsum);
+                    gsum += dpp_mov<0x140>(gsum);
+                    if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
+                } else {
                     if (m < n) {
-                        out_h[q * ldo + r] = xh;
-                        out_l[q * ldo + r] = xl;
+    #pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) out[q * ldo + row0 + 64u * wave + 16u * nb + ln] = acc[mb][nb][j];
                     }
                 }
-                // 32-column sum of act over this wave's columns (16 lanes x 2).
-                gsum += dpp_mov<0xb1>(gsum);
-                gsum += dpp_mov<0x4e>(gsum);
-                gsum += dpp_mov<0x141>(gsum);
-                gsum += dpp_mov<0x140>(gsum);
-                if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
-            } else {
-                if (m < n) {
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) out[q * ldo + row0 + 64u * wave + 16u * nb + ln] = acc[mb][nb][j];
-                }
             }
-        }
+    };
+    switch ((n + 15u) >> 4) {
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
+    }
 #undef INGOT_LOAD_A
 #undef INGOT_LOAD_S
 }
