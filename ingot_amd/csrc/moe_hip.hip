@@ -145,6 +145,14 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
                    const float* sgvec, const float* gain, float eps, float* logits, float* sgl, float* xn) {
     const uint32_t rows = E + (has_sg ? 1u : 0u);
     const bool decode = T <= 4;
+    if (!decode && E % 32u == 0 && (HB == 4 || HB == 8)) {
+        const dim3 grid((T + 7) / 8, E / 32);
+        if (HB == 8)
+            hipLaunchKernelGGL((k_router_t<8>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, logits, sgl, xn);
+        else
+            hipLaunchKernelGGL((k_router_t<4>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, logits, sgl, xn);
+        return true;
+    }
     const uint32_t epw = decode ? 1u : 8u;
     const uint32_t gy = (rows + 4 * epw - 1) / (4 * epw);
 #define ROUTER(TOK, HBV)                                                                                       \

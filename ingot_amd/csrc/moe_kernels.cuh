@@ -232,6 +232,162 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
     }
 }
 
+// Transposed xor butterfly over 64 sums at once: each lane holds v[0..63]
+// (its partial of 64 independent sums); lane l returns the full sum of output
+// l. At step m (32, 16, ..., 1) a lane keeps the half of its remaining outputs
+// selected by bit m of its lane index and adds the partner's (lane xor m)
+// partials of that half. Every partial sum is formed from the same two
+// operands as in wave_sum (fp addition is commutative), so each output equals
+// wave_sum of that output bit for bit.
+template <int M>
+__device__ __forceinline__ float xor_partner(float v) {
+    if constexpr (M == 32) return __shfl_xor(v, 32);
+    else if constexpr (M == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+    else if constexpr (M == 8) return dpp_mov<0x128>(v);
+    else if constexpr (M == 4) return dpp_mov<0x141>(dpp_mov<0x1b>(v));
+    else if constexpr (M == 2) return dpp_mov<0x4e>(v);
+    else return dpp_mov<0xb1>(v);
+}
+template <int C, int M>
+__device__ __forceinline__ void transpose_step(float* v, bool hi) {
+#pragma unroll
+    for (int i = 0; i < C / 2; ++i) {
+        const float a = v[i], b = v[i + C / 2];
+        const float keep = hi ? b : a, send = hi ? a : b;
+        v[i] = keep + xor_partner<M>(send);
+    }
+}
+__device__ __forceinline__ float transpose_sum64(float (&v)[64], uint32_t lane) {
+    transpose_step<64, 32>(v, lane & 32u);
+    transpose_step<32, 16>(v, lane & 16u);
+    transpose_step<16, 8>(v, lane & 8u);
+    transpose_step<8, 4>(v, lane & 4u);
+    transpose_step<4, 2>(v, lane & 2u);
+    transpose_step<2, 1>(v, lane & 1u);
+    return v[0];
+}
+
+// Prefill router: grid (ceil(T / 8), E / 32), 256 threads. Wave w of block
+// (bx, by) computes the logits of tokens 8 bx + 2 w, +1 for experts
+// 32 by .. +31: lane l keeps the fixed-order FMA chain of its columns
+// 4 l + 256 i + c (as k_router) for each of the 64 (token, expert) pairs, and
+// one transposed butterfly leaves pair (t, e) = (l / 32, l % 32) in lane l.
+// The block's router rows pass through LDS in double-buffered chunks of 4.
+// RMSNorm (gain: written to xn by the by == 0 blocks) and the shared-expert
+// gate logit (sgvec: by == 0 blocks, wave_sum) are computed as in k_router.
+template <int HB>
+__global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, const float* __restrict__ W,
+                                                  const float* __restrict__ sgvec, const float* __restrict__ gain,
+                                                  float eps, uint32_t T, uint32_t E, float* __restrict__ logits,
+                                                  float* __restrict__ sgl, float* __restrict__ xn) {
+    INGOT_NO_CONTRACT
+    constexpr uint32_t H = 256u * HB, Q = H / 4u;  // Q float4 per row
+    constexpr int CH = 4;                         // router rows per LDS chunk
+    __shared__ float4 sw[2][CH][Q];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const uint32_t t0 = blockIdx.x * 8u + 2u * wave, e0 = blockIdx.y * 32u;
+    float xr[2][HB * 4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t tt = min(t0 + t, T - 1);
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(x + (uint64_t)tt * H + 4u * lane + 256u * i);
+            xr[t][4 * i] = v.x; xr[t][4 * i + 1] = v.y; xr[t][4 * i + 2] = v.z; xr[t][4 * i + 3] = v.w;
+        }
+    }
+    if (gain) {
+        float g[HB * 4];
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(gain + 4u * lane + 256u * i);
+            g[4 * i] = v.x; g[4 * i + 1] = v.y; g[4 * i + 2] = v.z; g[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < HB * 4; ++j) ss = __builtin_fmaf(xr[t][j], xr[t][j], ss);
+            ss = wave_sum(ss);
+            const float mean = ss / (float)H;
+            const float r = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+            for (int j = 0; j < HB * 4; ++j) xr[t][j] = (xr[t][j] * r) * g[j];
+            if (blockIdx.y == 0 && t0 + t < T) {
+#pragma unroll
+                for (int i = 0; i < HB; ++i)
+                    *reinterpret_cast<float4*>(xn + (uint64_t)(t0 + t) * H + 4u * lane + 256u * i) =
+                        make_float4(xr[t][4 * i], xr[t][4 * i + 1], xr[t][4 * i + 2], xr[t][4 * i + 3]);
+            }
+        }
+    }
+    if (sgvec && blockIdx.y == 0) {
+        float wv[HB * 4];
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(sgvec + 4u * lane + 256u * i);
+            wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < HB * 4; ++j) acc = __builtin_fmaf(wv[j], xr[t][j], acc);
+            acc = wave_sum(acc);
+            if (lane == 0 && t0 + t < T) sgl[t0 + t] = acc;
+        }
+    }
+    // Router rows e0 .. e0 + 31 in 8 chunks of 4 through LDS.
+    constexpr uint32_t PER = CH * Q / 256u;  // float4 per thread per chunk
+    float4 stage[PER];
+    float p[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) p[i] = 0.f;
+#pragma unroll
+    for (uint32_t k = 0; k < PER; ++k) {
+        const uint32_t idx = tid + 256u * k;
+        sw[0][idx / Q][idx % Q] = reinterpret_cast<const float4*>(W + (uint64_t)(e0 + idx / Q) * H)[idx % Q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t c = 0; c < 8; ++c) {
+        if (c + 1 < 8) {
+#pragma unroll
+            for (uint32_t k = 0; k < PER; ++k) {
+                const uint32_t idx = tid + 256u * k;
+                stage[k] = reinterpret_cast<const float4*>(W + (uint64_t)(e0 + CH * (c + 1) + idx / Q) * H)[idx % Q];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < CH; ++r) {
+            float wv[HB * 4];
+#pragma unroll
+            for (int i = 0; i < HB; ++i) {
+                const float4 v = sw[c & 1u][r][lane + 64u * i];
+                wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                float acc = 0.f;
+#pragma unroll
+                for (int j = 0; j < HB * 4; ++j) acc = __builtin_fmaf(wv[j], xr[t][j], acc);
+                p[t * 32 + CH * c + r] = acc;
+            }
+        }
+        if (c + 1 < 8) {
+#pragma unroll
+            for (uint32_t k = 0; k < PER; ++k) {
+                const uint32_t idx = tid + 256u * k;
+                sw[(c + 1) & 1u][idx / Q][idx % Q] = stage[k];
+            }
+            __syncthreads();
+        }
+    }
+    const float v = transpose_sum64(p, lane);
+    const uint32_t t = t0 + (lane >> 5), e = e0 + (lane & 31u);
+    if (t < T) logits[(uint64_t)t * E + e] = v;
+}
+
 // ----------------------------------------------------------------- route
 // One wave per token, E <= 64 * NE. Softmax mode (src/lib.rs:43-60):
 // selection and weights on l (+ bias when given), w_k = exp(v_k - v_top) /
