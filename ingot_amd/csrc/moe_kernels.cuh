@@ -87,6 +87,7 @@ __device__ __forceinline__ float swiglu(float g, float u, float limit) {
 struct RouteLds {
     uint64_t* keys;
     float* vals;
+    uint32_t* rank;
     uint32_t* sel_id;
     float* sel_v;
     float* w;
@@ -111,21 +112,30 @@ __device__ inline void block_route(const float* __restrict__ l, const float* __r
         }
         s.keys[e] = ingot_select_key(key_v, e);
         s.vals[e] = wv;
+        s.rank[e] = 0;
     }
     const uint32_t E16 = (E + 15u) & ~15u;
     for (uint32_t e = E + tid; e < E16; e += nt) s.keys[e] = 0;  // below every real key
     if (flags && __any(bad) && (tid & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
     __syncthreads();
-    for (uint32_t e = tid; e < E; e += nt) {
+    // rank[e] = number of keys above key e (keys are distinct), counted over
+    // (expert, 16-key group) items spread across the block; consecutive
+    // threads share a group, so its keys are LDS broadcasts.
+    const uint32_t G = E16 / 16u;
+    for (uint32_t item = tid; item < E * G; item += nt) {
+        const uint32_t g = item / E, e = item - g * E;
         const uint64_t mine = s.keys[e];
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < E16; j += 16) {
-            ulonglong2 kv[8];
+        ulonglong2 kv[8];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) kv[q] = *reinterpret_cast<const ulonglong2*>(&s.keys[j + 2 * q]);
+        for (int q = 0; q < 8; ++q) kv[q] = *reinterpret_cast<const ulonglong2*>(&s.keys[16u * g + 2 * q]);
+        uint32_t c = 0;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) rank += (kv[q].x > mine ? 1u : 0u) + (kv[q].y > mine ? 1u : 0u);
-        }
+        for (int q = 0; q < 8; ++q) c += (kv[q].x > mine ? 1u : 0u) + (kv[q].y > mine ? 1u : 0u);
+        if (c) atomicAdd(&s.rank[e], c);
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += nt) {
+        const uint32_t rank = s.rank[e];
         if (rank < K) {
             s.sel_id[rank] = e;
             s.sel_v[rank] = s.vals[e];
@@ -490,6 +500,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     __shared__ float s_x[4096];
     __shared__ uint64_t s_keys[1024];
     __shared__ float s_vals[1024];
+    __shared__ uint32_t s_rank[1024];
     __shared__ uint32_t s_id[64];
     __shared__ float s_v[64], s_w[64];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -501,7 +512,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)t * H);
         for (uint32_t i = threadIdx.x; i < H / 4u; i += 512u) reinterpret_cast<float4*>(s_x)[i] = x4[i];
     }
-    block_route(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, scale, RouteLds{s_keys, s_vals, s_id, s_v, s_w},
+    block_route(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, scale, RouteLds{s_keys, s_vals, s_rank, s_id, s_v, s_w},
                 blockIdx.x == 0 ? flags : nullptr);
     if (blockIdx.x == 0 && threadIdx.x < K) {
         ids[(uint64_t)t * K + threadIdx.x] = s_id[threadIdx.x];
