@@ -153,6 +153,135 @@ def profile_workload(args):
     log("profile: calibration copy of 256 MiB done")
 
 
+def layer_work(spec, ids, T):
+    """Algorithmic bytes (touched weights, router, vectors, x and out) and FLOPs of one forward."""
+    H, E, K, F = spec.hidden, spec.experts, spec.top_k, spec.ffn
+    touched = int(np.unique(ids).size)
+    nbytes = touched * spec.weight_bytes_per_expert() + 4 * E * H + 2 * 4 * T * H
+    flops = 2.0 * T * K * 3 * F * H + 2.0 * T * E * H
+    if spec.router_bias is not None:
+        nbytes += 4 * E
+    if spec.shared is not None:
+        nbytes += sum(m.rows * m.stride for m in spec.shared)
+        flops += 2.0 * T * 3 * spec.shared[0].rows * H
+    if spec.shared_gate_vec is not None:
+        nbytes += 4 * H
+    if spec.norm_gain is not None:
+        nbytes += 4 * H
+    return nbytes, flops, touched
+
+
+def time_steps(gpu, step, steps, warmup):
+    """Mean ms of one step() captured `steps` times in a HIP graph (after a warm-up graph)."""
+    step()
+    gpu.synchronize()
+    gpu.check_device_flags()
+    gpu.graph_begin()
+    for _ in range(warmup):
+        step()
+    gw = gpu.graph_end()
+    gpu.graph_begin()
+    for _ in range(steps):
+        step()
+    g = gpu.graph_end()
+    gw.launch()
+    gpu.synchronize()
+    ms = g.time(1)
+    gw.destroy()
+    g.destroy()
+    return ms / steps
+
+
+def extra_configs(gpu, args):
+    """configs[2], [3] and [4] (parity-test configurations) timed the same way, for the record."""
+    from ingot_amd import configs as CF
+    from ingot_amd.moe import MoeLayer
+    out = {}
+
+    def record(name, spec, ids, T, ms, copies, bound):
+        nbytes, flops, touched = layer_work(spec, ids, T)
+        r = {"tokens": T, "us_per_step": ms * 1e3, "tokens_per_s": T / (ms * 1e-3), "experts_touched": touched,
+             "weight_copies": copies, "bytes": nbytes, "hbm_frac": nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
+             "flops": flops, "frac_vs_fp32_mfma_peak": flops / (ms * 1e-3) / (MFMA_F32_PEAK_TFLOPS * 1e12),
+             "bound": bound}
+        out[name] = r
+        log(f"{name}: {ms * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, HBM {100 * r['hbm_frac']:.1f} %, "
+            f"fp32 MFMA {100 * r['frac_vs_fp32_mfma_peak']:.1f} %")
+
+    def single(name, spec, T, copies, xin, bound):
+        base = MoeLayer(gpu, spec)
+        layers = [base] + [base.clone() for _ in range(copies - 1)]
+        dx = gpu.to_device(xin)
+        dout = gpu.buffer(4 * T * spec.hidden)
+        dids = gpu.buffer(4 * T * spec.top_k)
+        for l in layers:
+            l.reserve(T)
+        base.forward(dx, T, dout, dids)
+        gpu.synchronize()
+        ids = dids.download(np.uint32, T * spec.top_k)
+        i = [0]
+
+        def step():
+            layers[i[0] % copies].forward(dx, T, dout)
+            i[0] += 1
+        ms = time_steps(gpu, step, args.extra_steps, 10)
+        record(name, spec, ids, T, ms, copies, bound)
+        for l in layers:
+            l.destroy()
+
+    t0 = time.time()
+    spec2 = CF.c2_layer()
+    log(f"C2 layer synthesized in {time.time() - t0:.1f} s")
+    for T in (1, 4):
+        single(f"configs[2] b={T}", spec2, T, 32, CF.inputs(2, T, 2048), "hbm")
+    del spec2
+    t0 = time.time()
+    spec3 = CF.c3_layer()
+    log(f"C3 layer synthesized in {time.time() - t0:.1f} s")
+    single("configs[3] T=64", spec3, 64, 2, CF.inputs(3, 64, 4096, bf16=True), "hbm and mfma (ridge)")
+    del spec3
+    # configs[4]: 48 independent layers, h <- h + MoE_l(RMSNorm_l(h)); one step = the whole stack.
+    t0 = time.time()
+    specs = [CF.c4_layer(l) for l in range(48)]
+    layers = [MoeLayer(gpu, s) for s in specs]
+    log(f"C4 stack synthesized and uploaded in {time.time() - t0:.1f} s")
+    for T in (1, 8):
+        da = gpu.to_device(CF.inputs(4, T, 2048))
+        db = gpu.buffer(4 * T * 2048)
+        idb = [gpu.buffer(4 * T * 8) for _ in layers]
+        for l in layers:
+            l.reserve(T)
+        a, b = da, db
+        for l, ib in zip(layers, idb):
+            l.forward(a, T, b, ib)
+            a, b = b, a
+        gpu.synchronize()
+        ids = [ib.download(np.uint32, T * 8) for ib in idb]
+
+        def step():
+            a, b = da, db
+            for l in layers:
+                l.forward(a, T, b)
+                a, b = b, a
+        ms = time_steps(gpu, step, max(2, args.extra_steps // 10), 2)
+        nbytes = flops = 0
+        touched = []
+        for s, i in zip(specs, ids):
+            nb, fl, tc = layer_work(s, i, T)
+            nbytes += nb - 2 * 4 * T * 2048
+            flops += fl
+            touched.append(tc)
+        nbytes += 2 * 4 * T * 2048
+        r = {"tokens": T, "layers": 48, "us_per_step": ms * 1e3, "tokens_per_s": T / (ms * 1e-3),
+             "experts_touched_mean": float(np.mean(touched)), "bytes": nbytes,
+             "hbm_frac": nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), "flops": flops, "bound": "hbm"}
+        out[f"configs[4] 48 layers b={T}"] = r
+        log(f"C4 b={T}: {ms * 1e3:.1f} us per 48-layer step, {r['tokens_per_s']:.0f} tok/s, HBM {100 * r['hbm_frac']:.1f} %")
+    for l in layers:
+        l.destroy()
+    return out
+
+
 def cpu_baseline(spec, x, budget_s, label):
     from oracle import pyoracle as O
     cores = len(os.sched_getaffinity(0))
@@ -180,6 +309,9 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--extra", action="store_true",
+                    help="also time configs[2], [3] and [4] and add them as 'extra_configs' (slower: synthesis)")
+    ap.add_argument("--extra-steps", type=int, default=100)
     ap.add_argument("--profile", action="store_true",
                     help="run only a short eager workload for rocprofv3 and exit (no JSON line)")
     args = ap.parse_args()
@@ -256,6 +388,8 @@ def main():
         },
     }
 
+    extra = extra_configs(gpu, args) if args.extra else None
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(spec1, x1, args.cpu_seconds, "configs[1] prefill 512")
@@ -292,6 +426,8 @@ def main():
         "decode": decode,
         "cpu_baseline": cpu,
     }
+    if extra is not None:
+        line["extra_configs"] = extra
     print(json.dumps(line), flush=True)
 
 

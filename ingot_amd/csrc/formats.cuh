@@ -135,6 +135,38 @@ struct Fmt<12> {
 
 // --------------------------------------------------------- contiguous chunks
 // Formats whose chunk c covers columns 32c..32c+31 in order.
+// Codebooks in LDS. A lookup with a per-lane index into __constant__ memory
+// is a vector memory access chained after the weight load that supplies the
+// index, so every kernel that decodes IQ2_XS, IQ3_XXS or IQ4_NL copies the
+// codebook into LDS first: stage_codebooks<KIND>() at kernel start, followed
+// by a barrier before the first decode.
+__device__ inline uint64_t* lds_iq2xs_grid() {
+    __shared__ uint64_t g[512];
+    return g;
+}
+__device__ inline uint32_t* lds_iq3xxs_grid() {
+    __shared__ uint32_t g[256];
+    return g;
+}
+__device__ inline float* lds_iq4nl_values() {
+    __shared__ float v[16];
+    return v;
+}
+template <int KIND>
+__device__ inline void stage_codebooks() {
+    if constexpr (KIND == 17) {
+        for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq2xs_grid()[i] = ingot_iq2xs_grid[i];
+    } else if constexpr (KIND == 18) {
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_iq3xxs_grid()[i] = ingot_iq3xxs_grid[i];
+    } else if constexpr (KIND == 20) {
+        if (threadIdx.x < 16u) lds_iq4nl_values()[threadIdx.x] = (float)ingot_kvalues_iq4nl[threadIdx.x];
+    }
+}
+template <int KIND>
+constexpr bool has_codebook() {
+    return KIND == 17 || KIND == 18 || KIND == 20;
+}
+
 struct Contig {
     __device__ static uint32_t col(uint32_t c, uint32_t i) { return 32u * c + i; }
     __device__ static void load_x(const float* x, uint32_t c, float* xv) {
@@ -227,7 +259,7 @@ struct Nibble32 : Contig {
         uint32_t q[4];
     };
     __device__ static float value(uint32_t nib) {
-        if constexpr (NL) return (float)ingot_kvalues_iq4nl[nib];
+        if constexpr (NL) return lds_iq4nl_values()[nib];
         else return (float)((int)nib - 8);
     }
     __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
@@ -296,7 +328,7 @@ struct Fmt<17> : Contig {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             float db = d * (0.5f + (float)((r.scale >> (4 * (l / 2))) & 15u)) * 0.25f;
-            uint64_t grid = ingot_iq2xs_grid[r.code[l] & 511u];
+            uint64_t grid = lds_iq2xs_grid()[r.code[l] & 511u];
             uint32_t sg = ingot_ksign(r.code[l] >> 9);
 #pragma unroll
             for (int v = 0; v < 8; ++v)
@@ -310,7 +342,7 @@ struct Fmt<17> : Contig {
         float s = 0.f;
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            uint64_t grid = ingot_iq2xs_grid[r.code[l] & 511u];
+            uint64_t grid = lds_iq2xs_grid()[r.code[l] & 511u];
             uint32_t sg = ingot_ksign(r.code[l] >> 9);
             float t = 0.f;
 #pragma unroll
@@ -348,7 +380,7 @@ struct Fmt<18> : Contig {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             uint32_t sg = ingot_ksign((r.aux >> (7 * l)) & 127u);
-            uint32_t lo = ingot_iq3xxs_grid[r.gb[l] & 255u], hi = ingot_iq3xxs_grid[r.gb[l] >> 8];
+            uint32_t lo = lds_iq3xxs_grid()[r.gb[l] & 255u], hi = lds_iq3xxs_grid()[r.gb[l] >> 8];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 w[8 * l + v] = flip_sign(db * ubyte_f(lo, v), (sg >> v) & 1u);
@@ -364,7 +396,7 @@ struct Fmt<18> : Contig {
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
             uint32_t sg = ingot_ksign((r.aux >> (7 * l)) & 127u);
-            uint32_t lo = ingot_iq3xxs_grid[r.gb[l] & 255u], hi = ingot_iq3xxs_grid[r.gb[l] >> 8];
+            uint32_t lo = lds_iq3xxs_grid()[r.gb[l] & 255u], hi = lds_iq3xxs_grid()[r.gb[l] >> 8];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 s = __builtin_fmaf(ubyte_f(lo, v), flip_sign(xv[8 * l + v], (sg >> v) & 1u), s);

@@ -144,7 +144,9 @@ int upload(ingot_ctx* ctx, const T* h, uint64_t n, T** d) {
 bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_sg, const float* x, const float* W,
                    const float* sgvec, const float* gain, float eps, float* logits, float* sgl, float* xn) {
     const uint32_t rows = E + (has_sg ? 1u : 0u);
-    const bool decode = T <= 4;
+    // Below 64 tokens one token and one router row per wave keeps the grid
+    // wide (T x E / 4 blocks); from 64 tokens the 64-output transposed kernel.
+    const bool decode = T < 64;
     if (!decode && E % 32u == 0 && (HB == 4 || HB == 8)) {
         const dim3 grid((T + 7) / 8, E / 32);
         if (HB == 8)
@@ -295,7 +297,7 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 
 // Decode gate/up after router routing (k_dec_gate_up2): 2 rows x every pair per 8-wave block.
 constexpr int GU_RPW = 2;
-constexpr int DEC_RPW = 1;  // down rows per wave
+constexpr int DEC_RPW = 2;  // down rows per wave
 
 template <int KIND>
 static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, dim3 grid, const uint8_t* g, const uint8_t* u,

@@ -512,6 +512,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)t * H);
         for (uint32_t i = threadIdx.x; i < H / 4u; i += 512u) reinterpret_cast<float4*>(s_x)[i] = x4[i];
     }
+    stage_codebooks<KIND>();  // decoded only after block_route's barriers
     block_route(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, scale, RouteLds{s_keys, s_vals, s_rank, s_id, s_v, s_w},
                 blockIdx.x == 0 ? flags : nullptr);
     if (blockIdx.x == 0 && threadIdx.x < K) {
@@ -592,6 +593,9 @@ __global__ __launch_bounds__(256) void k_dec_down(const uint8_t* __restrict__ do
     using Fd = Fmt<KD>;
     using Fs = Fmt<(KS < 0 ? KD : KS)>;
     __shared__ float s_act[DOWN_LDS_FLOATS];
+    // Codebooks: decoded only after the barrier that follows the activation staging.
+    stage_codebooks<KD>();
+    if constexpr (KS >= 0) stage_codebooks<(KS < 0 ? KD : KS)>();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const uint32_t t = blockIdx.y;
     const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
@@ -694,6 +698,10 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(const uint8_t* __restrict_
                                                       const float* __restrict__ x, const uint32_t* __restrict__ ids,
                                                       uint32_t K, float limit, float* __restrict__ act) {
     using Fm = Fmt<KIND>;
+    if constexpr (has_codebook<KIND>()) {
+        stage_codebooks<KIND>();
+        __syncthreads();
+    }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t p = blockIdx.y;
     const uint32_t e = ids ? ids[p] : 0u, t = ids ? p / K : p;
@@ -746,6 +754,10 @@ __global__ __launch_bounds__(256) void k_gemv_shared_down_add(const uint8_t* __r
                                                               uint32_t H, uint32_t SF, const float* __restrict__ sact,
                                                               const float* __restrict__ sgl, float* __restrict__ out) {
     using Fs = Fmt<KS>;
+    if constexpr (has_codebook<KS>()) {
+        stage_codebooks<KS>();
+        __syncthreads();
+    }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y, r = blockIdx.x * 4u + wave;
     if (r >= H) return;
@@ -924,6 +936,10 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
     const uint32_t* tile = tiles + 4u * blockIdx.y;
     const uint32_t n = tile[2];
     if (n == 0) return;
+    if constexpr (has_codebook<KIND>()) {
+        stage_codebooks<KIND>();
+        __syncthreads();
+    }
     const uint32_t e = tile[0], q0 = tile[1];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     // Output rows of this block: GATEUP 64 (gate and up), else 128.
@@ -954,86 +970,96 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
         bptr = w0 + ((uint64_t)e * rows_per_expert + row0 + brow) * stride0;
     }
 
-    floatx4 acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Only the first ceil(n / 16) 16-row blocks of the tile issue MFMAs.
+    auto run = [&](auto mbe_tag) {
+        constexpr int MBE = decltype(mbe_tag)::value;
+        floatx4 acc[MBE][2];
+    #pragma unroll
+        for (int i = 0; i < MBE; ++i)
+    #pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    float4 ar[4];
-    typename Fm::Raw br;
-    auto load = [&](uint32_t s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            ar[i] = arow[i] ? *reinterpret_cast<const float4*>(arow[i] + 64u * s + acol) : make_float4(0.f, 0.f, 0.f, 0.f);
-        br = Fm::load_raw(bptr, 2u * s + bh);
-    };
-    const uint32_t slabs = kdim / 64u;
-    load(0);
-    for (uint32_t s = 0; s < slabs; ++s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t m = (tid + 256u * i) >> 4;
-            *reinterpret_cast<float4*>(&As[m * LDS_STRIDE + acol]) = ar[i];
-        }
-        {
-            float wv[32];
-            Fm::dequant_raw(br, 2u * s + bh, wv);
-            float* dst = &Bs[brow * LDS_STRIDE];
-            // Chunk value i -> slab column: Fm::col(chunk, i) - 64 s.
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                uint32_t cl = Fm::col(2u * s + bh, i) - 64u * s;
-                *reinterpret_cast<float4*>(dst + cl) = make_float4(wv[i], wv[i + 1], wv[i + 2], wv[i + 3]);
+        float4 ar[4];
+        typename Fm::Raw br;
+        auto load = [&](uint32_t s) {
+    #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                ar[i] = arow[i] ? *reinterpret_cast<const float4*>(arow[i] + 64u * s + acol) : make_float4(0.f, 0.f, 0.f, 0.f);
+            br = Fm::load_raw(bptr, 2u * s + bh);
+        };
+        const uint32_t slabs = kdim / 64u;
+        load(0);
+        for (uint32_t s = 0; s < slabs; ++s) {
+    #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t m = (tid + 256u * i) >> 4;
+                *reinterpret_cast<float4*>(&As[m * LDS_STRIDE + acol]) = ar[i];
             }
-        }
-        __syncthreads();
-        if (s + 1 < slabs) load(s + 1);
-#pragma unroll
-        for (uint32_t kk = 0; kk < 4; ++kk) {
-            const uint32_t kc = kk * 16u + 4u * (lane >> 4);
-            float4 a[4], b[2];
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-                a[mb] = *reinterpret_cast<const float4*>(&As[(mb * 16u + (lane & 15u)) * LDS_STRIDE + kc]);
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                // GATEUP: nb 0 = gate rows 16w.., nb 1 = up rows 64+16w..; else rows 32w + 16nb..
-                uint32_t br_ = GATEUP ? (nb * 64u + 16u * wave) : (32u * wave + 16u * nb);
-                b[nb] = *reinterpret_cast<const float4*>(&Bs[(br_ + (lane & 15u)) * LDS_STRIDE + kc]);
-            }
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb) {
-                        float av = ks == 0 ? a[mb].x : ks == 1 ? a[mb].y : ks == 2 ? a[mb].z : a[mb].w;
-                        float bv = ks == 0 ? b[nb].x : ks == 1 ? b[nb].y : ks == 2 ? b[nb].z : b[nb].w;
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[mb][nb], 0, 0, 0);
-                    }
-        }
-        __syncthreads();
-    }
-    // Epilogue: lane holds D[m = 4*(lane/16) + j][n = lane%16] of each tile.
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t m = mb * 16u + 4u * (lane >> 4) + j;
-            if (m >= n) continue;
-            uint64_t q = q0 + m;
-            if (GATEUP) {
-                uint32_t r = row0 + 16u * wave + (lane & 15u);
-                out[q * ldo + r] = swiglu(acc[mb][0][j], acc[mb][1][j], limit);
-            } else {
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    uint32_t r = row0 + 32u * wave + 16u * nb + (lane & 15u);
-                    out[q * ldo + r] = acc[mb][nb][j];
+            {
+                float wv[32];
+                Fm::dequant_raw(br, 2u * s + bh, wv);
+                float* dst = &Bs[brow * LDS_STRIDE];
+                // Chunk value i -> slab column: Fm::col(chunk, i) - 64 s.
+    #pragma unroll
+                for (int i = 0; i < 32; i += 4) {
+                    uint32_t cl = Fm::col(2u * s + bh, i) - 64u * s;
+                    *reinterpret_cast<float4*>(dst + cl) = make_float4(wv[i], wv[i + 1], wv[i + 2], wv[i + 3]);
                 }
             }
+            __syncthreads();
+            if (s + 1 < slabs) load(s + 1);
+    #pragma unroll
+            for (uint32_t kk = 0; kk < 4; ++kk) {
+                const uint32_t kc = kk * 16u + 4u * (lane >> 4);
+                float4 a[MBE], b[2];
+    #pragma unroll
+                for (int mb = 0; mb < MBE; ++mb)
+                    a[mb] = *reinterpret_cast<const float4*>(&As[(mb * 16u + (lane & 15u)) * LDS_STRIDE + kc]);
+    #pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    // GATEUP: nb 0 = gate rows 16w.., nb 1 = up rows 64+16w..; else rows 32w + 16nb..
+                    uint32_t br_ = GATEUP ? (nb * 64u + 16u * wave) : (32u * wave + 16u * nb);
+                    b[nb] = *reinterpret_cast<const float4*>(&Bs[(br_ + (lane & 15u)) * LDS_STRIDE + kc]);
+                }
+    #pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+    #pragma unroll
+                    for (int mb = 0; mb < MBE; ++mb)
+    #pragma unroll
+                        for (int nb = 0; nb < 2; ++nb) {
+                            float av = ks == 0 ? a[mb].x : ks == 1 ? a[mb].y : ks == 2 ? a[mb].z : a[mb].w;
+                            float bv = ks == 0 ? b[nb].x : ks == 1 ? b[nb].y : ks == 2 ? b[nb].z : b[nb].w;
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[mb][nb], 0, 0, 0);
+                        }
+            }
+            __syncthreads();
         }
+        // Epilogue: lane holds D[m = 4*(lane/16) + j][n = lane%16] of each tile.
+    #pragma unroll
+        for (int mb = 0; mb < MBE; ++mb)
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t m = mb * 16u + 4u * (lane >> 4) + j;
+                if (m >= n) continue;
+                uint64_t q = q0 + m;
+                if (GATEUP) {
+                    uint32_t r = row0 + 16u * wave + (lane & 15u);
+                    out[q * ldo + r] = swiglu(acc[mb][0][j], acc[mb][1][j], limit);
+                } else {
+    #pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        uint32_t r = row0 + 32u * wave + 16u * nb + (lane & 15u);
+                        out[q * ldo + r] = acc[mb][nb][j];
+                    }
+                }
+            }
+    };
+    switch ((n + 15u) >> 4) {
+        case 1: run(std::integral_constant<int, 1>{}); break;
+        case 2: run(std::integral_constant<int, 2>{}); break;
+        case 3: run(std::integral_constant<int, 3>{}); break;
+        default: run(std::integral_constant<int, 4>{}); break;
+    }
 }
 
 // -------------------------------- prefill: Q4_K grouped GEMM on f16 MFMA
