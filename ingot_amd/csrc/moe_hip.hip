@@ -967,7 +967,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
             if (f16) {
                 hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(8 * (F / 64) * ((cap + 7) / 8)), dim3(128), 0, ss,
                                    gate.d, up.d, gate.stride, up.stride, F, H, xh, xl, xs, pairs, K, tiles, F, limit,
-                                   nullptr, acth, actl, acts, F / 64);
+                                   nullptr, acth, actl, acts, F / 64, T);
             } else {
                 launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
                                   pairs, K, tiles, F, limit, act);
@@ -981,7 +981,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
             if (f16)
                 hipLaunchKernelGGL((k_gemm_q4k_f16<false>), dim3(8 * (H / 128) * ((cap + 7) / 8)), dim3(128), 0, ss,
                                    down.d, nullptr, down.stride, 0ull, H, F, acth, actl, acts, nullptr, K, tiles, H,
-                                   0.f, Y, nullptr, nullptr, nullptr, H / 128);
+                                   0.f, Y, nullptr, nullptr, nullptr, H / 128, P);
             else
                 launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act,
                                    nullptr, K, tiles, H, 0.f, Y);

@@ -1129,13 +1129,27 @@ __device__ __forceinline__ half8 q4_operand(uint32_t b0, uint32_t b1, uint32_t s
 
 constexpr uint32_t TM16 = 64;  // tokens per tile of the f16 GEMM
 
+// Raw buffer access: base and size in a buffer resource (scalar registers),
+// per-lane byte offset in a vector register, uniform byte offset in a scalar
+// register; reads past `bytes` return zero. Word 3 is the gfx9 raw-buffer
+// configuration (no format conversion).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
+}
+
 template <bool GATEUP>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_q4k_f16(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, uint64_t stride0, uint64_t stride1,
     uint32_t rows_per_expert, uint32_t kdim, const _Float16* __restrict__ ah, const _Float16* __restrict__ al,
     const float* __restrict__ gs, const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles,
     uint32_t ldo, float limit, float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l,
-    float* __restrict__ out_gs, uint32_t nblk) {
+    float* __restrict__ out_gs, uint32_t nblk, uint32_t a_rows) {
     constexpr int NB = 4;
     // A tiles, double-buffered by slab parity: 64 halves (128 B) per row,
     // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7) so that the
@@ -1157,35 +1171,51 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t n = tile[2];
     if (n == 0) return;
     const uint32_t e = tile[0], q0 = tile[1];
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, kq = lane >> 4, ln = lane & 15u;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, kq = lane >> 4, ln = lane & 15u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t row0 = (slot - ti * nblk) * (GATEUP ? 64u : 128u);
     const uint32_t ngroups = kdim / 32u;
 
+    // Every global load below is a wave-uniform base (scalar registers) plus a
+    // loop-invariant 32-bit lane offset, so addressing costs no vector ALU.
     const uint32_t ac = tid & 7u, ar0 = tid >> 3;
-    uint32_t aoff[4];
+    uint32_t aoff[4];  // byte offset of row ar0 + 16 j, chunk ac, in ah / al
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t m = ar0 + 16u * j;
         const uint32_t q = q0 + (m < n ? m : 0u);
         const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
-        aoff[j] = r * kdim + 8u * ac;
+        aoff[j] = 2u * (r * kdim + 8u * ac);
     }
     const uint32_t am = tid >> 1, ahalf = tid & 1u;
-    const float* srow;
+    uint32_t soff;  // byte offset of this thread's group sums in gs
     {
         const uint32_t q = q0 + (am < n ? am : 0u);
-        const uint64_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
-        srow = gs + r * ngroups + 4u * ahalf;
+        const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
+        soff = 4u * (r * ngroups + 4u * ahalf);
     }
-    const uint8_t* brow[NB];
+    // Buffer resources: A halves and group sums over their whole arrays, the
+    // weights over this expert's slab (rows_per_expert rows); the slab and
+    // row-block parts of an offset go in the scalar offset.
+    const __amdgpu_buffer_rsrc_t ra_h = make_rsrc(ah, (uint32_t)(kdim * 2u) * a_rows);
+    const __amdgpu_buffer_rsrc_t ra_l = make_rsrc(al, (uint32_t)(kdim * 2u) * a_rows);
+    const __amdgpu_buffer_rsrc_t rgs = make_rsrc(gs, ngroups * 4u * a_rows);
+    const __amdgpu_buffer_rsrc_t rw0 = make_rsrc(w0 + (uint64_t)e * rows_per_expert * stride0,
+                                                 (uint32_t)(rows_per_expert * stride0));
+    const __amdgpu_buffer_rsrc_t rw1 = GATEUP ? make_rsrc(w1 + (uint64_t)e * rows_per_expert * stride1,
+                                                          (uint32_t)(rows_per_expert * stride1))
+                                              : rw0;
+    uint32_t bsoff[NB];  // wave-uniform byte offset of row 0 of n-block nb in its expert slab
+    uint32_t boff[NB];   // lane: its row within the n-block
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         if (GATEUP) {
-            const uint32_t r = row0 + 32u * wave + 16u * (nb & 1) + ln;
-            brow[nb] = (nb < 2 ? w0 : w1) + ((uint64_t)e * rows_per_expert + r) * (nb < 2 ? stride0 : stride1);
+            const uint32_t st = (uint32_t)(nb < 2 ? stride0 : stride1);
+            bsoff[nb] = (row0 + 32u * wave + 16u * (nb & 1)) * st;
+            boff[nb] = ln * st;
         } else {
-            const uint32_t r = row0 + 64u * wave + 16u * nb + ln;
-            brow[nb] = w0 + ((uint64_t)e * rows_per_expert + r) * stride0;
+            bsoff[nb] = (row0 + 64u * wave + 16u * nb) * (uint32_t)stride0;
+            boff[nb] = ln * (uint32_t)stride0;
         }
     }
 
@@ -1195,22 +1225,23 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // branch-free, never used).
     uint4 pa_h0, pa_h1, pa_h2, pa_h3, pa_l0, pa_l1, pa_l2, pa_l3;
     const uint32_t aoff0 = aoff[0], aoff1 = aoff[1], aoff2 = aoff[2], aoff3 = aoff[3];
-#define INGOT_LOAD_A1(J, S_) pa_h##J = *reinterpret_cast<const uint4*>(ah + aoff##J + 64u * (S_)); pa_l##J = *reinterpret_cast<const uint4*>(al + aoff##J + 64u * (S_))
+#define INGOT_LOAD_A1(J, S_) pa_h##J = buf_load16(ra_h, aoff##J, 128u * (S_)); pa_l##J = buf_load16(ra_l, aoff##J, 128u * (S_))
 #define INGOT_LOAD_A(S) do { const uint32_t s_ = (S) < slabs ? (S) : slabs - 1u; INGOT_LOAD_A1(0, s_); INGOT_LOAD_A1(1, s_); INGOT_LOAD_A1(2, s_); INGOT_LOAD_A1(3, s_); } while (0)
     float4 ps;
-#define INGOT_LOAD_S(SB) ps = *reinterpret_cast<const float4*>(srow + 8u * ((SB) < sbs ? (SB) : sbs - 1u))
+#define INGOT_LOAD_S(SB) ps = __builtin_bit_cast(float4, buf_load16(rgs, soff, 32u * ((SB) < sbs ? (SB) : sbs - 1u)))
     uint4 hdr[NB], nhdr[NB];
     auto load_hdr = [&](uint32_t sb) {
         sb = sb < sbs ? sb : sbs - 1u;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) nhdr[nb] = *reinterpret_cast<const uint4*>(brow[nb] + sb * 144u);
+        for (int nb = 0; nb < NB; ++nb) nhdr[nb] = buf_load16(GATEUP && nb >= 2 ? rw1 : rw0, boff[nb], bsoff[nb] + sb * 144u);
     };
     uint2 nqs[2][NB];  // B nibbles of slabs s + 1 and s + 2 (ring by slab parity)
     auto load_qs = [&](uint2* dst, uint32_t s) {
         s = s < slabs ? s : slabs - 1u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-            dst[nb] = *reinterpret_cast<const uint2*>(brow[nb] + (s >> 2) * 144u + 16u + 32u * (s & 3u) + 8u * kq);
+            dst[nb] = buf_load8(GATEUP && nb >= 2 ? rw1 : rw0, boff[nb] + 8u * kq,
+                                bsoff[nb] + (s >> 2) * 144u + 16u + 32u * (s & 3u));
     };
     // Superblock scale D = d 2^24 (1 and B zeroed when d == 0), Dmin = dmin 2^24.
     auto dscale = [](uint4 h) {
