@@ -953,8 +953,8 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         // Dispatch stage: expert grouping, and for the f16 GEMM the split of x
         // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
-            hipLaunchKernelGGL(k_dispatch_count, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, cap, counts, first, tiles);
-            hipLaunchKernelGGL(k_dispatch_place, dim3(E), dim3(256), 0, ss, ids, P, counts, first, pairs, inverse);
+            hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, cap, counts, first, tiles, pairs,
+                               inverse);
             if (hs) hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
             if (f16) {
                 const uint64_t n = (uint64_t)T * H;
@@ -962,7 +962,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
                                    xs);
             }
         };
-        L->stage_name[ST_DISPATCH] = "k_dispatch_count";
+        L->stage_name[ST_DISPATCH] = "k_dispatch";
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             if (f16) {
                 hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(8 * (F / 64) * ((cap + 7) / 8)), dim3(128), 0, ss,
@@ -991,8 +991,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         };
         L->stage_name[ST_DOWN] = f16 ? "k_gemm_q4k_f16<down>" : "k_gemm<down>";
         L->stage[ST_COMBINE] = [=](hipStream_t ss) {
-            uint64_t n4 = (uint64_t)T * H / 4;
-            hipLaunchKernelGGL(k_combine, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, ss, Y, hs ? Ys : nullptr,
+            hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, ss, Y, hs ? Ys : nullptr,
                                inverse, wts, sgl, res, T, H, K, d_out);
         };
         L->stage_name[ST_COMBINE] = "k_combine";

@@ -9,7 +9,7 @@
 //                            act[p] = SwiGLU(G_e x_t, U_e x_t), one wave per pair
 //            k_gemv_gate_up  the same for the shared expert (no routing)
 //            k_dec_down      out[t] = sum_k w_k D_e act[p] (+ shared, + residual)
-//   prefill  k_dispatch_count / k_dispatch_place   stable expert grouping
+//   prefill  k_dispatch      stable expert grouping, tile list (one block)
 //            k_gemm<GATEUP>  MFMA f32 grouped GEMM, dequantised weights in LDS
 //            k_combine       out[t] = sum_k w_k Y[inverse[p]] (+ shared, + residual)
 #pragma once
@@ -809,37 +809,62 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
     return inc - v + wsum[16 + wave];
 }
 
-// One block of 1024 threads, E <= 1024. Counts pairs per expert, writes
-// counts[E], first[E] (exclusive scan: experts ascending) and the tile list of
-// TM-pair tiles {expert, first pair of the tile, n in tile, number of
-// non-empty tiles} (the layout of kernels/prefill.metal:7-23), padded with
-// zero tiles to cap. Order: every expert's full tiles (experts ascending),
-// then the partial last tiles by decreasing n, so that work scheduled last is
-// the cheapest. Results do not depend on the order: each tile's rows are
+// One block of 1024 threads (16 waves), E <= 1024: the whole prefill
+// dispatch (kernels/prefill.metal:7-38). Writes counts[E], first[E]
+// (exclusive scan, experts ascending), the stable pair order pairs[] (experts
+// ascending, pair index ascending within an expert), inverse[p] (packed
+// position of pair p) and the tile list of TM-pair tiles {expert, first pair
+// of the tile, n in tile, number of non-empty tiles}, padded with zero tiles
+// to cap. Tile order: every expert's full tiles (experts ascending), then the
+// partial last tiles by decreasing n, so that work scheduled last is the
+// cheapest; results do not depend on the order, each tile's rows being
 // computed independently.
-__global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
-                                                         uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
-                                                         uint32_t* __restrict__ first, uint32_t* __restrict__ tiles) {
-    __shared__ uint32_t cnt[1024];
+//   Stable placement: wave w owns the contiguous pair segment
+//   [w seg, (w + 1) seg); a histogram per wave gives each wave's start inside
+//   every expert's range; the wave then walks its segment 64 pairs at a time,
+//   and a pair's rank among earlier lanes with the same expert comes from
+//   ballots over the bits of the expert id.
+__global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
+                                                   uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
+                                                   uint32_t* __restrict__ first, uint32_t* __restrict__ tiles,
+                                                   uint32_t* __restrict__ pairs, uint32_t* __restrict__ inverse) {
+    __shared__ uint32_t hist[16][1024];  // per wave, per expert; then each wave's running position
     __shared__ uint32_t wsum[32];
     __shared__ uint32_t tot[3];
     __shared__ uint32_t rbin[1024];  // partial tiles per remainder, then their start positions
-    const uint32_t tid = threadIdx.x;
-    cnt[tid] = 0;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) hist[w][tid] = 0;
     rbin[tid] = 0;
     __syncthreads();
-    for (uint32_t p = tid; p < P; p += 1024u) atomicAdd(&cnt[ids[p]], 1u);
+    const uint32_t seg = (P + 15u) / 16u, s0 = min(P, wave * seg), s1 = min(P, s0 + seg);
+    for (uint32_t p = s0 + lane; p < s1; p += 64u) atomicAdd(&hist[wave][ids[p]], 1u);
     __syncthreads();
-    const uint32_t n = tid < E ? cnt[tid] : 0u;
+    // Expert tid: its count, and each wave's offset within the expert.
+    uint32_t n = 0;
+    if (tid < E) {
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            const uint32_t h = hist[w][tid];
+            hist[w][tid] = n;
+            n += h;
+        }
+    }
     const uint32_t nfull = n / TM, rem = n - nfull * TM;
     const uint32_t f = block_exclusive_scan_1024(n, wsum, &tot[0]);
     __syncthreads();
     const uint32_t t0 = block_exclusive_scan_1024(nfull, wsum, &tot[1]);  // full tiles
+    if (tid < E) {
+        counts[tid] = n;
+        first[tid] = f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) hist[w][tid] += f;
+    }
     if (rem) atomicAdd(&rbin[rem], 1u);
     __syncthreads();
     // Start of each remainder's run among the partial tiles (larger remainders
     // first): exclusive scan over remainders TM-1 .. 1.
-    const uint32_t rr = tid < TM ? TM - 1u - tid : 0u;  // thread tid handles remainder rr
+    const uint32_t rr = tid < TM ? TM - 1u - tid : 0u;
     const uint32_t c = (tid < TM && rr > 0) ? rbin[rr] : 0u;
     const uint32_t before = block_exclusive_scan_1024(c, wsum, &tot[2]);
     const uint32_t nt_all = tot[2];
@@ -848,8 +873,6 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restr
     __syncthreads();
     const uint32_t ntiles = min(tot[1] + nt_all, cap);
     if (tid < E) {
-        counts[tid] = n;
-        first[tid] = f;
         for (uint32_t k = 0; k < nfull && t0 + k < cap; ++k) {
             uint32_t* tl = tiles + 4u * (t0 + k);
             tl[0] = tid;
@@ -873,37 +896,30 @@ __global__ __launch_bounds__(1024) void k_dispatch_count(const uint32_t* __restr
         tl[0] = tl[1] = tl[2] = 0;
         tl[3] = ntiles;
     }
-}
-
-// One block (256 threads) per expert: pair indices of the expert in ascending
-// order at pairs[first[e]...], and each pair's packed position in inverse[p]
-// (kernels/prefill.metal:25-38).
-__global__ __launch_bounds__(256) void k_dispatch_place(const uint32_t* __restrict__ ids, uint32_t P,
-                                                        const uint32_t* __restrict__ counts,
-                                                        const uint32_t* __restrict__ first, uint32_t* __restrict__ pairs,
-                                                        uint32_t* __restrict__ inverse) {
-    const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    if (counts[e] == 0) return;
-    __shared__ uint32_t ws[4];
-    const uint32_t chunk = (P + 255u) / 256u, s = min(P, tid * chunk), end = min(P, s + chunk);
-    uint32_t mine = 0;
-    for (uint32_t i = s; i < end; ++i) mine += ids[i] == e;
-    uint32_t inc = mine;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        uint32_t o = __shfl_up(inc, d);
-        if (lane >= (uint32_t)d) inc += o;
-    }
-    if (lane == 63) ws[wave] = inc;
-    __syncthreads();
-    uint32_t before = inc - mine;
-    for (uint32_t w = 0; w < wave; ++w) before += ws[w];
-    uint32_t at = first[e] + before;
-    for (uint32_t i = s; i < end; ++i)
-        if (ids[i] == e) {
-            inverse[i] = at;
-            pairs[at++] = i;
+    // Stable placement, wave by wave over its own segment (no barrier needed:
+    // each wave only touches its own row of hist).
+    uint32_t nbits = 1;
+    while ((1u << nbits) < E) ++nbits;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (uint32_t base = s0; base < s1; base += 64u) {
+        const uint32_t p = base + lane;
+        const bool live = p < s1;
+        const uint32_t x = live ? ids[p] : 0u;
+        uint64_t same = __ballot(live);
+        for (uint32_t b = 0; b < nbits; ++b) {
+            const uint64_t one = __ballot(live && ((x >> b) & 1u));
+            same &= ((x >> b) & 1u) ? one : ~one;
         }
+        if (live) {
+            const uint32_t pos = hist[wave][x] + (uint32_t)__popcll(same & lt);
+            pairs[pos] = p;
+            inverse[p] = pos;
+        }
+        // every lane has read the running positions before the leaders advance them
+        __builtin_amdgcn_wave_barrier();
+        if (live && (same & lt) == 0) hist[wave][x] += (uint32_t)__popcll(same);
+        __builtin_amdgcn_wave_barrier();
+    }
 }
 
 // ---------------------------------------------------- prefill: grouped GEMM
@@ -1452,24 +1468,24 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
                                                  const uint32_t* __restrict__ inverse, const float* __restrict__ wts,
                                                  const float* __restrict__ sgl, const float* __restrict__ res,
                                                  uint32_t T, uint32_t H, uint32_t K, float* __restrict__ out) {
-    const uint64_t i4 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t per = H / 4u;
-    if (i4 >= (uint64_t)T * per) return;
-    const uint32_t t = (uint32_t)(i4 / per), c = (uint32_t)(i4 % per) * 4u;
+    // grid (ceil(H / 1024), T): the token is uniform in the block, so its
+    // packed positions and weights are scalar loads.
+    const uint32_t t = blockIdx.y, c = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (c >= H) return;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t k = 0; k < K; ++k) {
-        uint32_t p = t * K + k;
-        float w = wts[p];
-        float4 y = *reinterpret_cast<const float4*>(Y + (uint64_t)inverse[p] * H + c);
+        const uint32_t p = t * K + k;
+        const float w = wts[p];
+        const float4 y = *reinterpret_cast<const float4*>(Y + (uint64_t)inverse[p] * H + c);
         s.x += w * y.x; s.y += w * y.y; s.z += w * y.z; s.w += w * y.w;
     }
     if (Ys) {
-        float w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
-        float4 y = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
+        const float w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
+        const float4 y = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
         s.x += y.x * w; s.y += y.y * w; s.z += y.z * w; s.w += y.w * w;
     }
     if (res) {
-        float4 r = *reinterpret_cast<const float4*>(res + (uint64_t)t * H + c);
+        const float4 r = *reinterpret_cast<const float4*>(res + (uint64_t)t * H + c);
         s.x += r.x; s.y += r.y; s.z += r.z; s.w += r.w;
     }
     *reinterpret_cast<float4*>(out + (uint64_t)t * H + c) = s;
