@@ -198,15 +198,20 @@ def extra_configs(gpu, args):
     from ingot_amd.moe import MoeLayer
     out = {}
 
-    def record(name, spec, ids, T, ms, copies, bound):
+    def record(name, spec, ids, T, ms, copies, bound, stages=None):
         nbytes, flops, touched = layer_work(spec, ids, T)
         r = {"tokens": T, "us_per_step": ms * 1e3, "tokens_per_s": T / (ms * 1e-3), "experts_touched": touched,
              "weight_copies": copies, "bytes": nbytes, "hbm_frac": nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9),
              "flops": flops, "frac_vs_fp32_mfma_peak": flops / (ms * 1e-3) / (MFMA_F32_PEAK_TFLOPS * 1e12),
              "bound": bound}
+        if stages:
+            r["stages_us"] = {k: round(v["us"], 2) for k, v in stages.items()}
+            r["stage_kernels"] = {k: v["kernel"] for k, v in stages.items()}
         out[name] = r
         log(f"{name}: {ms * 1e3:.1f} us/step, {r['tokens_per_s']:.0f} tok/s, HBM {100 * r['hbm_frac']:.1f} %, "
             f"fp32 MFMA {100 * r['frac_vs_fp32_mfma_peak']:.1f} %")
+        if stages:
+            log(f"  stages (us): " + ", ".join(f"{k} {v['us']:.1f} ({v['kernel']})" for k, v in stages.items()))
 
     def single(name, spec, T, copies, xin, bound):
         base = MoeLayer(gpu, spec)
@@ -225,7 +230,8 @@ def extra_configs(gpu, args):
             layers[i[0] % copies].forward(dx, T, dout)
             i[0] += 1
         ms = time_steps(gpu, step, args.extra_steps, 10)
-        record(name, spec, ids, T, ms, copies, bound)
+        stages = time_stages(layers, dx, T, dout, 20)
+        record(name, spec, ids, T, ms, copies, bound, stages)
         for l in layers:
             l.destroy()
 

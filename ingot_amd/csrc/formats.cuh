@@ -167,6 +167,39 @@ constexpr bool has_codebook() {
     return KIND == 17 || KIND == 18 || KIND == 20;
 }
 
+// Tables of the f16 grouped GEMM, whose B operands are integers held as f16
+// bit patterns (an f16 with bits b <= 2047 has the value b * 2^-24 exactly).
+//   iq3 sign masks: entry i spreads the 8 signs of ingot_ksign(i) over four
+//     f16 pairs, sign of value 2j in bit 15 and of 2j + 1 in bit 31 of word j.
+//   iq4_nl pairs: entry b holds the two codebook values of the nibbles of b
+//     (low nibble in the low half) as sign-magnitude f16 bit patterns.
+__device__ inline uint4* lds_iq3_signmask() {
+    __shared__ uint4 m[128];
+    return m;
+}
+__device__ inline uint32_t* lds_iq4nl_pairs() {
+    __shared__ uint32_t p[256];
+    return p;
+}
+__device__ inline uint32_t iq4nl_f16_bits(int v) { return v < 0 ? 0x8000u | (uint32_t)(-v) : (uint32_t)v; }
+template <int KIND>
+__device__ inline void stage_f16_tables() {
+    if constexpr (KIND == 18) {
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_iq3xxs_grid()[i] = ingot_iq3xxs_grid[i];
+        for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
+            const uint32_t s = ingot_ksign(i);
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = (((s >> (2 * j)) & 1u) << 15) | (((s >> (2 * j + 1)) & 1u) << 31);
+            lds_iq3_signmask()[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    } else if constexpr (KIND == 20) {
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x)
+            lds_iq4nl_pairs()[i] =
+                iq4nl_f16_bits(ingot_kvalues_iq4nl[i & 15u]) | (iq4nl_f16_bits(ingot_kvalues_iq4nl[i >> 4]) << 16);
+    }
+}
+
 struct Contig {
     __device__ static uint32_t col(uint32_t c, uint32_t i) { return 32u * c + i; }
     __device__ static void load_x(const float* x, uint32_t c, float* xv) {

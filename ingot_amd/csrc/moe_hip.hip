@@ -293,6 +293,51 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 #undef GEMM
 }
 
+// Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K;
+// IQ3_XXS when its rows are a whole number of dwords (kdim % 512 == 0; its
+// loads assume 4-byte aligned rows); IQ4_NL as the down projection only (its A
+// is act, which the gate/up kernel stores permuted for it).
+bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
+    switch (kind) {
+        case 12: return kdim % 256 == 0;
+        case 18: return kdim % 512 == 0;
+        case 20: return !gateup && kdim % 64 == 0;
+        default: return false;
+    }
+}
+
+// Column order of A that an f16 GEMM over weights of `kind` reads.
+int a_order(uint32_t kind) { return kind == 20 ? A_IQ4NL : kind == 18 ? A_IQ3XXS : A_NATURAL; }
+
+// gate/up: `kind` its weights, `aord` the order it writes act in (the down
+// projection's a_order).
+template <bool GATEUP, typename... Args>
+bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... args) {
+#define F16(KV, AO) hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO>), grid, dim3(128), 0, s, args...)
+#define F16_GU(KV)                                          \
+    switch (aord) {                                         \
+        case A_IQ4NL: F16(KV, A_IQ4NL); return true;        \
+        case A_IQ3XXS: F16(KV, A_IQ3XXS); return true;      \
+        default: F16(KV, A_NATURAL); return true;           \
+    }
+    if constexpr (GATEUP) {
+        switch (kind) {
+            case 12: F16_GU(12)
+            case 18: F16_GU(18)
+            default: return false;
+        }
+    } else {
+        switch (kind) {
+            case 12: F16(12, A_NATURAL); return true;
+            case 18: F16(18, A_NATURAL); return true;
+            case 20: F16(20, A_NATURAL); return true;
+            default: return false;
+        }
+    }
+#undef F16_GU
+#undef F16
+}
+
 }  // namespace
 
 // Decode gate/up after router routing (k_dec_gate_up2): 2 rows x every pair per 8-wave block.
@@ -388,7 +433,7 @@ struct ingot_layer {
     uint32_t cap_T = 0;
     void* ws = nullptr;
     float *xn = nullptr, *logits = nullptr, *sgl = nullptr, *wts = nullptr, *act = nullptr, *sact = nullptr,
-          *Y = nullptr, *Ys = nullptr;
+          *Y = nullptr;
     uint32_t *ids = nullptr, *counts = nullptr, *first = nullptr, *tiles = nullptr, *pairs = nullptr,
              *inverse = nullptr, *stiles = nullptr;
     _Float16 *xh = nullptr, *xl = nullptr, *acth = nullptr, *actl = nullptr;
@@ -410,8 +455,11 @@ static int reserve(ingot_layer* L, uint32_t T) {
     ingot_ctx* ctx = L->ctx;
     if (T <= L->cap_T) return INGOT_OK;
     const uint64_t P = (uint64_t)T * L->K;
-    const uint32_t tile_cap = (uint32_t)((P + TM - 1) / TM + L->E);
+    // With a shared expert, rows P..P+T-1 of the packed buffers (pairs, act,
+    // Y) belong to it, and the tile list has room for its tiles.
+    const uint64_t PS = P + (L->SF ? T : 0);
     const uint32_t stile_cap = (T + TM - 1) / TM;
+    const uint32_t tile_cap = (uint32_t)((P + TM - 1) / TM + L->E + (L->SF ? stile_cap : 0));
     struct Part {
         void** p;
         uint64_t bytes;
@@ -421,13 +469,13 @@ static int reserve(ingot_layer* L, uint32_t T) {
         {(void**)&L->sgl, 4ull * T},             {(void**)&L->ids, 4ull * P},
         {(void**)&L->wts, 4ull * P},             {(void**)&L->act, 4ull * P * L->F},
         {(void**)&L->sact, 4ull * T * (L->SF ? L->SF : 1)},
-        {(void**)&L->Y, 4ull * P * L->H},        {(void**)&L->Ys, 4ull * T * L->H},
+        {(void**)&L->Y, 4ull * PS * L->H},
         {(void**)&L->counts, 4ull * L->E},       {(void**)&L->first, 4ull * L->E},
-        {(void**)&L->tiles, 16ull * tile_cap},   {(void**)&L->pairs, 4ull * P},
+        {(void**)&L->tiles, 16ull * tile_cap},   {(void**)&L->pairs, 4ull * PS},
         {(void**)&L->inverse, 4ull * P},         {(void**)&L->stiles, 16ull * stile_cap},
         {(void**)&L->xh, 2ull * T * L->H},      {(void**)&L->xl, 2ull * T * L->H},
-        {(void**)&L->acth, 2ull * P * L->F},     {(void**)&L->actl, 2ull * P * L->F},
-        {(void**)&L->xs, 4ull * T * (L->H / 32)}, {(void**)&L->acts, 4ull * P * (L->F / 32)},
+        {(void**)&L->acth, 2ull * PS * L->F},    {(void**)&L->actl, 2ull * PS * L->F},
+        {(void**)&L->xs, 4ull * T * (L->H / 32)}, {(void**)&L->acts, 4ull * PS * (L->F / 32)},
     };
     uint64_t total = 0;
     for (auto& p : parts) total += (p.bytes + 255) & ~255ull;
@@ -943,53 +991,71 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         uint32_t *counts = L->counts, *first = L->first, *tiles = L->tiles, *pairs = L->pairs, *inverse = L->inverse,
                  *stiles = L->stiles;
         const uint32_t cap = (P + TM - 1) / TM + E, scap = (T + TM - 1) / TM;
-        float *act = L->act, *sact = L->sact, *Y = L->Y, *Ys = L->Ys, limit = L->limit;
+        // Shared-expert rows of Y follow this call's P routed rows.
+        float *act = L->act, *sact = L->sact, *Y = L->Y, *Ys = L->Y + (uint64_t)P * H, limit = L->limit;
         const float* wts = L->wts;
         bool hs = L->has_shared;
-        const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && gate.kind == 12 && down.kind == 12;
+        // The f16 GEMM runs when both projections' formats allow it; the shared
+        // expert then joins the same launches (as tile expert E over rows
+        // P..P+T-1) when it has the routed experts' formats and width, and
+        // otherwise runs on the fp32 GEMM beside them.
+        const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(gate.kind, H, true) &&
+                         f16_gemm_kind(down.kind, F, false);
+        const bool merge = f16 && hs && SF == F && sgate.kind == gate.kind && sup.kind == up.kind &&
+                           sdown.kind == down.kind && sgate.stride == gate.stride && sup.stride == up.stride &&
+                           sdown.stride == down.stride;
+        const int aord = a_order(down.kind), xord = a_order(gate.kind);
+        const bool mins = down.kind == 12;
         const uint32_t tm = f16 ? TM16 : TM;
+        const uint32_t S = merge ? T : 0u, capf = cap + (merge ? scap : 0u), e_sh = merge ? E : 0xffffffffu;
         _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
         float *xs = L->xs, *acts = L->acts;
         // Dispatch stage: expert grouping, and for the f16 GEMM the split of x
         // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
-            hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, cap, counts, first, tiles, pairs,
-                               inverse);
-            if (hs) hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
+            hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, capf, counts, first, tiles, pairs,
+                               inverse, S, K);
+            if (hs && !merge)
+                hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
             if (f16) {
                 const uint64_t n = (uint64_t)T * H;
                 hipLaunchKernelGGL(k_split_f16, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256), 0, ss, xin, n, xh, xl,
-                                   xs);
+                                   xs, (uint32_t)xord);
             }
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch";
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             if (f16) {
-                hipLaunchKernelGGL((k_gemm_q4k_f16<true>), dim3(8 * (F / 64) * ((cap + 7) / 8)), dim3(128), 0, ss,
-                                   gate.d, up.d, gate.stride, up.stride, F, H, xh, xl, xs, pairs, K, tiles, F, limit,
-                                   nullptr, acth, actl, acts, F / 64, T);
+                launch_gemm_f16<true>(ss, gate.kind, aord, dim3(8 * (F / 64) * ((capf + 7) / 8)), gate.d, up.d,
+                                      merge ? sgate.d : nullptr, merge ? sup.d : nullptr, e_sh, gate.stride, up.stride,
+                                      F, H, (const _Float16*)xh, (const _Float16*)xl, (const float*)xs,
+                                      (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit, (float*)nullptr,
+                                      acth, actl, mins ? acts : nullptr, F / 64, T);
             } else {
                 launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
                                   pairs, K, tiles, F, limit, act);
             }
-            if (hs)
+            if (hs && !merge)
                 launch_gemm<true>(ss, sgate.kind, dim3(SF / 64, scap), sgate.d, sup.d, sgate.stride, sup.stride, SF, H,
                                   xin, nullptr, 1, stiles, SF, limit, sact);
         };
-        L->stage_name[ST_GATEUP] = f16 ? "k_gemm_q4k_f16<gate_up>" : "k_gemm<gate_up>";
+        L->stage_name[ST_GATEUP] = f16 ? "k_gemm_f16<gate_up>" : "k_gemm<gate_up>";
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
             if (f16)
-                hipLaunchKernelGGL((k_gemm_q4k_f16<false>), dim3(8 * (H / 128) * ((cap + 7) / 8)), dim3(128), 0, ss,
-                                   down.d, nullptr, down.stride, 0ull, H, F, acth, actl, acts, nullptr, K, tiles, H,
-                                   0.f, Y, nullptr, nullptr, nullptr, H / 128, P);
+                launch_gemm_f16<false>(ss, down.kind, A_NATURAL, dim3(8 * (H / 128) * ((capf + 7) / 8)), down.d,
+                                       (const uint8_t*)nullptr, merge ? sdown.d : nullptr, (const uint8_t*)nullptr, e_sh,
+                                       down.stride, 0ull, H, F, (const _Float16*)acth, (const _Float16*)actl,
+                                       (const float*)acts, (const uint32_t*)nullptr, K, (const uint32_t*)tiles, H, 0.f,
+                                       Y, (_Float16*)nullptr, (_Float16*)nullptr, (float*)nullptr, H / 128,
+                                       (uint32_t)(P + S));
             else
                 launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act,
                                    nullptr, K, tiles, H, 0.f, Y);
-            if (hs)
+            if (hs && !merge)
                 launch_gemm<false>(ss, sdown.kind, dim3(H / 128, scap), sdown.d, nullptr, sdown.stride, 0, H, SF, sact,
                                    nullptr, 1, stiles, H, 0.f, Ys);
         };
-        L->stage_name[ST_DOWN] = f16 ? "k_gemm_q4k_f16<down>" : "k_gemm<down>";
+        L->stage_name[ST_DOWN] = f16 ? "k_gemm_f16<down>" : "k_gemm<down>";
         L->stage[ST_COMBINE] = [=](hipStream_t ss) {
             hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, ss, Y, hs ? Ys : nullptr,
                                inverse, wts, sgl, res, T, H, K, d_out);

@@ -10,7 +10,10 @@
 //            k_gemv_gate_up  the same for the shared expert (no routing)
 //            k_dec_down      out[t] = sum_k w_k D_e act[p] (+ shared, + residual)
 //   prefill  k_dispatch      stable expert grouping, tile list (one block)
+//            k_gemm_f16      f16-MFMA grouped GEMM on integer weight operands
+//                            (Q4_K, IQ3_XXS, IQ4_NL), A split into f16 hi + lo
 //            k_gemm<GATEUP>  MFMA f32 grouped GEMM, dequantised weights in LDS
+//                            (every other format)
 //            k_combine       out[t] = sum_k w_k Y[inverse[p]] (+ shared, + residual)
 #pragma once
 #include <hip/hip_runtime.h>
@@ -815,10 +818,11 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
 // ascending, pair index ascending within an expert), inverse[p] (packed
 // position of pair p) and the tile list of TM-pair tiles {expert, first pair
 // of the tile, n in tile, number of non-empty tiles}, padded with zero tiles
-// to cap. Tile order: every expert's full tiles (experts ascending), then the
-// partial last tiles by decreasing n, so that work scheduled last is the
-// cheapest; results do not depend on the order, each tile's rows being
-// computed independently.
+// to cap. Tile order: the shared expert's tiles when S > 0 (expert id E,
+// positions P..P+S-1, pairs[P + t] = t K so that pairs[q] / K is the token),
+// every expert's full tiles (experts ascending), then the partial last tiles
+// by decreasing n, so that work scheduled last is the cheapest; results do
+// not depend on the order, each tile's rows being computed independently.
 //   Stable placement: wave w owns the contiguous pair segment
 //   [w seg, (w + 1) seg); a histogram per wave gives each wave's start inside
 //   every expert's range; the wave then walks its segment 64 pairs at a time,
@@ -827,7 +831,8 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
 __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
                                                    uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
                                                    uint32_t* __restrict__ first, uint32_t* __restrict__ tiles,
-                                                   uint32_t* __restrict__ pairs, uint32_t* __restrict__ inverse) {
+                                                   uint32_t* __restrict__ pairs, uint32_t* __restrict__ inverse,
+                                                   uint32_t S, uint32_t K) {
     __shared__ uint32_t hist[16][1024];  // per wave, per expert; then each wave's running position
     __shared__ uint32_t wsum[32];
     __shared__ uint32_t tot[3];
@@ -869,12 +874,23 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
     const uint32_t before = block_exclusive_scan_1024(c, wsum, &tot[2]);
     const uint32_t nt_all = tot[2];
     __syncthreads();
-    if (tid < TM && rr > 0) rbin[rr] = tot[1] + before;
+    // The shared expert's S rows (S = 0: none) come first, as expert E over
+    // positions P..P+S-1, whose pairs entry t K names token t.
+    const uint32_t nsh = (S + TM - 1u) / TM;
+    if (tid < TM && rr > 0) rbin[rr] = nsh + tot[1] + before;
     __syncthreads();
-    const uint32_t ntiles = min(tot[1] + nt_all, cap);
+    const uint32_t ntiles = min(nsh + tot[1] + nt_all, cap);
+    for (uint32_t j = tid; j < nsh && j < cap; j += 1024u) {
+        uint32_t* tl = tiles + 4u * j;
+        tl[0] = E;
+        tl[1] = P + j * TM;
+        tl[2] = min(TM, S - j * TM);
+        tl[3] = ntiles;
+    }
+    for (uint32_t t = tid; t < S; t += 1024u) pairs[P + t] = t * K;
     if (tid < E) {
-        for (uint32_t k = 0; k < nfull && t0 + k < cap; ++k) {
-            uint32_t* tl = tiles + 4u * (t0 + k);
+        for (uint32_t k = 0; k < nfull && nsh + t0 + k < cap; ++k) {
+            uint32_t* tl = tiles + 4u * (nsh + t0 + k);
             tl[0] = tid;
             tl[1] = f + k * TM;
             tl[2] = TM;
@@ -891,7 +907,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
             }
         }
     }
-    for (uint32_t t = tot[1] + nt_all + tid; t < cap; t += 1024u) {
+    for (uint32_t t = nsh + tot[1] + nt_all + tid; t < cap; t += 1024u) {
         uint32_t* tl = tiles + 4u * t;
         tl[0] = tl[1] = tl[2] = 0;
         tl[3] = ntiles;
@@ -1078,36 +1094,78 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
     }
 }
 
-// -------------------------------- prefill: Q4_K grouped GEMM on f16 MFMA
+// ------------------ prefill: grouped GEMM on f16 MFMA (Q4_K, IQ3_XXS, IQ4_NL)
 // Same tile list as k_gemm, computed on v_mfma_f32_16x16x32_f16 with fp32
 // accumulation and no loss against fp32 operands:
 //   * A (inputs or activations, fp32) arrives split in HBM as f16 hi + lo
 //     (ah, al: [rows][kdim], a = hi + lo to 2^-22 |a|) and is staged per
 //     64-column slab in LDS; both halves enter the MFMA.
-//   * B is not dequantised. A Q4_K weight is w = d sc_g q - dmin mn_g (q a
-//     nibble, sc_g and mn_g 6-bit integers of the 32-column group g, d and
-//     dmin f16 per 256-column superblock; ggml get_scale_min_k4,
-//     kernels/iq3_mix.metal:13-23). The MFMA takes the integer q sc_g <= 945
-//     as the raw bits of an f16 subnormal, i.e. the exact value q sc_g 2^-24,
-//     so one superblock accumulates sum_c a_c q_c sc_g(c) 2^-24 exactly up to
-//     fp32 rounding, in units of D = d 2^24.
-//   * The mins term dmin sum_g mn_g S_g, with S_g = sum of a over the group
-//     (precomputed per A row: gs [rows][kdim/32]), is one more MFMA per
+//   * B is not dequantised. Each format's weight is an integer times scales,
+//     and the MFMA takes the integer (at most 2047, sign in bit 15) as the raw
+//     bits of an f16: bits b <= 2047 are the exact value b 2^-24 (subnormal
+//     below 1024, exponent field 1 up to 2047).
+//       Q4_K    w = d sc_g q - dmin mn_g (q a nibble, sc_g and mn_g 6-bit
+//               integers of the 32-column group g, d and dmin f16 per
+//               256-column superblock; ggml get_scale_min_k4,
+//               kernels/iq3_mix.metal:13-23): B = q sc_g <= 945, so a
+//               superblock accumulates in units of D = d 2^24.
+//       IQ3_XXS w = d (0.5 + s_g) 0.5 grid sign (kernels/iq3_mix.metal:31-35):
+//               B = (1 + 2 s_g) grid <= 31 * 62 with the sign, D = d 2^22.
+//       IQ4_NL  w = d_g kv[q] (kernels/moe.metal:76-80): B = kv[q], |kv| <=
+//               127, with the sign. d_g belongs to one 32-column block, so
+//               each block's two MFMAs (A hi, A lo) start from zero and their
+//               sum is added to the accumulator times d_g 2^24.
+//   * The Q4_K mins term dmin sum_g mn_g S_g, with S_g = sum of a over the
+//     group (precomputed per A row: gs [rows][kdim/32]), is one more MFMA per
 //     superblock: A = (S hi, S lo) of the 8 groups, B = mn_g as subnormals.
-//   * Between superblocks the accumulator moves from units D_sb to D_sb+1:
-//     acc = acc D_sb / D_sb+1 - macc Dmin_sb / D_sb+1 (D = 1 for the true units
-//     after the last superblock; a zero d gives D = 1 and zeroes B).
+//   * Between superblocks (Q4_K, IQ3_XXS) the accumulator moves from units
+//     D_sb to D_sb+1: acc = acc D_sb / D_sb+1 (- macc Dmin_sb / D_sb+1 for
+//     Q4_K; D = 1 for the true units after the last superblock; a zero d gives
+//     D = 1 and zeroes B).
 // Block = 2 waves, tile of 64 tokens x 128 rows; wave tile 64 x 64 (4 x 4
-// MFMA tiles). Lane l owns B row (l % 16) of each 16-row block and columns
-// 8 (l / 16) .. + 7 of each 32-column group (the slab's two groups are the low
-// and high nibbles of the same 8 bytes).
+// MFMA tiles). Lane l owns B row (l % 16) of each 16-row block; which 8
+// columns of a slab it feeds to MFMA gi depends on the format's byte order:
+//   Q4_K    columns 32 gi + 8 (l / 16) .. + 7 (the slab's two groups are the
+//           low and high nibbles of the same 8 bytes);
+//   IQ3_XXS superblock columns 64 kq + 16 sq + 8 gi .. + 7 in slab sq
+//           (kq = l / 16; grid bytes 16 kq + 4 sq + 2 gi, + 1), so that a lane
+//           reads its 16 grid bytes and 2 sign/scale words once per superblock;
+//           A is stored in the matching order (A_IQ3XXS) so that slab sq is one
+//           contiguous run of 64 columns;
+//   IQ4_NL  block gi, bytes 4 (l / 16) .. + 3, each holding values j (low
+//           nibble) and j + 16 (high): the lane's 8 values are block columns
+//           4 kq + i + 16 h at position 2 i + h; A is stored in that order
+//           (A_IQ4NL).
+//   The gate/up kernel writes act in the order of the down projection's
+//   format; k_split_f16 writes x in the order of gate/up's.
 //   GATEUP: block b covers act columns 64 b..+63; wave w gate and up rows
 //   64 b + 32 w ..+31 (n-blocks 0,1 gate, 2,3 up). Writes act = SwiGLU split
-//   into out_h/out_l [P][F] and its 32-column sums out_gs [P][F/32].
+//   into out_h/out_l [P][F] and, for a Q4_K down projection, its 32-column
+//   sums out_gs [P][F/32].
 //   !GATEUP: block b covers rows 128 b..+127, wave w rows 128 b + 64 w..+63;
 //   writes fp32 Y [P][ldo].
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef short short2v __attribute__((ext_vector_type(2)));
+
+// Column orders of an A operand (x split, act) in HBM; a_pos maps a column to
+// its stored position.
+//   A_IQ4NL: within each 32-column group, column 4 kq + i + 16 h -> 8 kq + 2 i + h
+//     (kq, i < 4; h < 2): a lane's 4 IQ4_NL bytes hold these 8 values.
+//   A_IQ3XXS: within each 256-column superblock, the 16-column pieces are
+//     transposed, column 64 kq + 16 sq + j -> 64 sq + 16 kq + j (kq, sq < 4):
+//     lane kq reads its grid bytes 16 kq .. +15 once per superblock and uses
+//     4 of them (16 columns) in slab sq, so slab sq's A is one contiguous run.
+enum : int { A_NATURAL = 0, A_IQ4NL = 1, A_IQ3XXS = 2 };
+template <int ORD>
+__device__ __forceinline__ uint32_t a_pos(uint32_t c) {
+    if constexpr (ORD == A_IQ4NL) {
+        const uint32_t k = c & 31u;
+        return (c & ~31u) | (8u * ((k & 15u) >> 2) + 2u * (k & 3u) + (k >> 4));
+    } else if constexpr (ORD == A_IQ3XXS) {
+        return (c & ~255u) | (((c >> 4) & 3u) << 6) | (((c >> 6) & 3u) << 4) | (c & 15u);
+    }
+    return c;
+}
 
 __device__ __forceinline__ void split_f16(float v, _Float16& hi, _Float16& lo) {
     hi = (_Float16)v;
@@ -1134,6 +1192,12 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
 __device__ __forceinline__ uint32_t mul_u16x2(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2v, a) * __builtin_bit_cast(short2v, b));
 }
+// a * b + c per 16-bit half (the products used here stay below 0x8000, so a
+// c of sign bits is an OR).
+__device__ __forceinline__ uint32_t mad_u16x2(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2v, a) * __builtin_bit_cast(short2v, b) +
+                                            __builtin_bit_cast(short2v, c));
+}
 
 // 8 nibbles (already masked to 0x0f0f0f0f in lo4/hi4 bytes) times the
 // replicated scale scl2 = sc | sc << 16 -> half8 of subnormal f16 bits.
@@ -1158,34 +1222,54 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
 __device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
 }
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
 
-template <bool GATEUP>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_q4k_f16(
-    const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, uint64_t stride0, uint64_t stride1,
-    uint32_t rows_per_expert, uint32_t kdim, const _Float16* __restrict__ ah, const _Float16* __restrict__ al,
-    const float* __restrict__ gs, const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles,
-    uint32_t ldo, float limit, float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l,
-    float* __restrict__ out_gs, uint32_t nblk, uint32_t a_rows) {
+// Grouped GEMM on f16 MFMA for Q4_K, IQ3_XXS and IQ4_NL weights (see the
+// block comment above). e_shared names the tile expert id whose weights are
+// ws0/ws1 (the shared expert, run in the same launch); no tile carries it when
+// it is 0xffffffff. AORD (gate/up only) is the column order in which act is
+// stored: the order the down projection's format reads (a_pos).
+template <int KIND, bool GATEUP, int AORD>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
+    const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ ws0,
+    const uint8_t* __restrict__ ws1, uint32_t e_shared, uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
+    uint32_t kdim, const _Float16* __restrict__ ah, const _Float16* __restrict__ al, const float* __restrict__ gs,
+    const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
+    float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
+    uint32_t nblk, uint32_t a_rows) {
+    static_assert(KIND == 12 || KIND == 18 || KIND == 20, "f16 GEMM formats: Q4_K, IQ3_XXS, IQ4_NL");
+    static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
+    static_assert(KIND != 20 || !GATEUP, "IQ4_NL is read with permuted A, which only act provides");
     constexpr int NB = 4;
+    constexpr bool Q4K = KIND == 12, IQ3 = KIND == 18, IQ4 = KIND == 20;
+    // Slabs per step of the main loop: one 256-column superblock (Q4_K,
+    // IQ3_XXS); IQ4_NL steps the same way and stops at the last slab.
+    constexpr uint32_t UNR = 4u;
     // A tiles, double-buffered by slab parity: 64 halves (128 B) per row,
     // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7) so that the
     // stores and the MFMA fragment reads (16 rows at one chunk) touch every
-    // bank once. S tiles double-buffered by superblock parity.
+    // bank once. S tiles (Q4_K) double-buffered by superblock parity.
     __shared__ _Float16 Ash[2][TM16 * 64];
     __shared__ _Float16 Asl[2][TM16 * 64];
     __shared__ _Float16 Ss[2][TM16 * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
     // 1-D grid of 8 * nblk * ceil(cap / 8) blocks. The hardware deals blocks to
     // the 8 XCDs round-robin (block h runs on XCD h % 8); XCD x takes tiles
-    // x, x + 8, x + 16, ... in list order (full tiles first, then partial
-    // tiles by decreasing size) with all nblk row blocks of each tile, so a
-    // tile's A rows are fetched into one XCD's L2 and the blocks each XCD
-    // runs last are its smallest tiles.
+    // x, x + 8, x + 16, ... in list order (shared-expert tiles, full tiles,
+    // then partial tiles by decreasing size) with all nblk row blocks of each
+    // tile, so a tile's A rows are fetched into one XCD's L2 and the blocks
+    // each XCD runs last are its smallest tiles.
     const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk;
     const uint32_t t = ti * 8u + (blockIdx.x & 7u);
     if (t >= nt) return;
     const uint32_t* tile = tiles + 4u * t;
     const uint32_t n = tile[2];
     if (n == 0) return;
+    if constexpr (!Q4K) {
+        stage_f16_tables<KIND>();
+        __syncthreads();
+    }
     const uint32_t e = tile[0], q0 = tile[1];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, kq = lane >> 4, ln = lane & 15u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1204,8 +1288,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         aoff[j] = 2u * (r * kdim + 8u * ac);
     }
     const uint32_t am = tid >> 1, ahalf = tid & 1u;
-    uint32_t soff;  // byte offset of this thread's group sums in gs
-    {
+    uint32_t soff = 0;  // byte offset of this thread's group sums in gs (Q4_K)
+    if constexpr (Q4K) {
         const uint32_t q = q0 + (am < n ? am : 0u);
         const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
         soff = 4u * (r * ngroups + 4u * ahalf);
@@ -1213,14 +1297,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // Buffer resources: A halves and group sums over their whole arrays, the
     // weights over this expert's slab (rows_per_expert rows); the slab and
     // row-block parts of an offset go in the scalar offset.
+    const bool sh_tile = e == e_shared;
+    const uint8_t* const wb0 = sh_tile ? ws0 : w0 + (uint64_t)e * rows_per_expert * stride0;
+    const uint8_t* const wb1 = GATEUP ? (sh_tile ? ws1 : w1 + (uint64_t)e * rows_per_expert * stride1) : wb0;
     const __amdgpu_buffer_rsrc_t ra_h = make_rsrc(ah, (uint32_t)(kdim * 2u) * a_rows);
     const __amdgpu_buffer_rsrc_t ra_l = make_rsrc(al, (uint32_t)(kdim * 2u) * a_rows);
     const __amdgpu_buffer_rsrc_t rgs = make_rsrc(gs, ngroups * 4u * a_rows);
-    const __amdgpu_buffer_rsrc_t rw0 = make_rsrc(w0 + (uint64_t)e * rows_per_expert * stride0,
-                                                 (uint32_t)(rows_per_expert * stride0));
-    const __amdgpu_buffer_rsrc_t rw1 = GATEUP ? make_rsrc(w1 + (uint64_t)e * rows_per_expert * stride1,
-                                                          (uint32_t)(rows_per_expert * stride1))
-                                              : rw0;
+    const __amdgpu_buffer_rsrc_t rw0 = make_rsrc(wb0, (uint32_t)(rows_per_expert * stride0));
+    const __amdgpu_buffer_rsrc_t rw1 = GATEUP ? make_rsrc(wb1, (uint32_t)(rows_per_expert * stride1)) : rw0;
     uint32_t bsoff[NB];  // wave-uniform byte offset of row 0 of n-block nb in its expert slab
     uint32_t boff[NB];   // lane: its row within the n-block
 #pragma unroll
@@ -1235,180 +1319,379 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     }
 
-
     const uint32_t slabs = kdim / 64u, sbs = kdim / 256u;
     // Loads past the last slab or superblock re-read the last one (uniform,
     // branch-free, never used).
-    uint4 pa_h0, pa_h1, pa_h2, pa_h3, pa_l0, pa_l1, pa_l2, pa_l3;
     const uint32_t aoff0 = aoff[0], aoff1 = aoff[1], aoff2 = aoff[2], aoff3 = aoff[3];
-#define INGOT_LOAD_A1(J, S_) pa_h##J = buf_load16(ra_h, aoff##J, 128u * (S_)); pa_l##J = buf_load16(ra_l, aoff##J, 128u * (S_))
-#define INGOT_LOAD_A(S) do { const uint32_t s_ = (S) < slabs ? (S) : slabs - 1u; INGOT_LOAD_A1(0, s_); INGOT_LOAD_A1(1, s_); INGOT_LOAD_A1(2, s_); INGOT_LOAD_A1(3, s_); } while (0)
+    // A rows of active row blocks only (ar0 + 16 j, j < MBE) into register set SET.
+#define INGOT_LOAD_A1(SET, J, S_) pah[SET][J] = buf_load16(ra_h, aoff##J, 128u * (S_)); pal[SET][J] = buf_load16(ra_l, aoff##J, 128u * (S_))
+#define INGOT_LOAD_A(SET, S) do { const uint32_t s_ = (S) < slabs ? (S) : slabs - 1u; INGOT_LOAD_A1(SET, 0, s_); if (MBE > 1) { INGOT_LOAD_A1(SET, 1, s_); } if (MBE > 2) { INGOT_LOAD_A1(SET, 2, s_); } if (MBE > 3) { INGOT_LOAD_A1(SET, 3, s_); } } while (0)
     float4 ps;
 #define INGOT_LOAD_S(SB) ps = __builtin_bit_cast(float4, buf_load16(rgs, soff, 32u * ((SB) < sbs ? (SB) : sbs - 1u)))
+    // Superblock headers, one superblock ahead: Q4_K {d, dmin, scales}; IQ3_XXS
+    // the dword holding d (superblock offset 98 sb is 2 mod 4 for odd sb, d
+    // then in the high half: row strides are multiples of 4).
     uint4 hdr[NB], nhdr[NB];
+    // IQ3_XXS reads each lane's bytes once per superblock, one superblock
+    // ahead: lane kq takes grid bytes 16 kq .. +15 (nhdr, n5: 20-byte window)
+    // and the sign/scale words of groups 2 kq, 2 kq + 1 (n3: 12-byte window);
+    // a window starts 2 (even sb) or 4 (odd sb) bytes before its target and
+    // never passes the next superblock; n_d is the dword holding d.
+    uint32_t n5[NB], n_d[NB];
+    uint3 n3[NB];
     auto load_hdr = [&](uint32_t sb) {
         sb = sb < sbs ? sb : sbs - 1u;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) nhdr[nb] = buf_load16(GATEUP && nb >= 2 ? rw1 : rw0, boff[nb], bsoff[nb] + sb * 144u);
+        for (int nb = 0; nb < NB; ++nb) {
+            const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
+            if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * 144u);
+            if constexpr (IQ3) {
+                const uint32_t u = (bsoff[nb] + sb * 98u) & ~3u;
+                nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);
+                n5[nb] = buf_load4(rw, boff[nb] + 16u * kq, u + 16u);
+                const uint2 a = buf_load8(rw, boff[nb] + 8u * kq, u + 64u);
+                n3[nb] = make_uint3(a.x, a.y, buf_load4(rw, boff[nb] + 8u * kq, u + 72u));
+                n_d[nb] = buf_load4(rw, boff[nb], u);
+            }
+        }
     };
-    uint2 nqs[2][NB];  // B nibbles of slabs s + 1 and s + 2 (ring by slab parity)
-    auto load_qs = [&](uint2* dst, uint32_t s) {
+    // Per-slab B bytes, DEPTH slabs ahead (ring slot s % DEPTH; see run()).
+    //   Q4_K: .xy = the lane's 8 nibble bytes.
+    //   IQ4_NL: .xy = slab bytes 4 kq .. +7 (block 0 quants 4 kq .. +3 at
+    //     offset 2); n1 = block 1 quants 4 kq .. +3; nd = slab dwords 0 and 4
+    //     (d of block 0 in the low half, d of block 1 in the high half).
+    uint4 nq[4][NB];
+    uint32_t n1[4][NB];
+    uint2 nd[4][NB];
+    auto load_slab = [&](uint32_t rs, uint32_t s) {
         s = s < slabs ? s : slabs - 1u;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            dst[nb] = buf_load8(GATEUP && nb >= 2 ? rw1 : rw0, boff[nb] + 8u * kq,
-                                bsoff[nb] + (s >> 2) * 144u + 16u + 32u * (s & 3u));
+        for (int nb = 0; nb < NB; ++nb) {
+            const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
+            if constexpr (Q4K) {
+                const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * 144u + 16u + 32u * (s & 3u));
+                nq[rs][nb].x = v.x;
+                nq[rs][nb].y = v.y;
+            } else if constexpr (IQ4) {
+                const uint32_t u = bsoff[nb] + 36u * s;
+                const uint2 q = buf_load8(rw, boff[nb] + 4u * kq, u);
+                nq[rs][nb].x = q.x;
+                nq[rs][nb].y = q.y;
+                n1[rs][nb] = buf_load4(rw, boff[nb] + 4u * kq, u + 20u);
+                nd[rs][nb] = make_uint2(buf_load4(rw, boff[nb], u), buf_load4(rw, boff[nb], u + 16u));
+            }
+        }
     };
-    // Superblock scale D = d 2^24 (1 and B zeroed when d == 0), Dmin = dmin 2^24.
-    auto dscale = [](uint4 h) {
-        const float d = half_bits_to_float(h.x);
-        return d != 0.f ? d * 16777216.f : 1.f;
+    // Superblock d of n-block nb as loaded for superblock sb (IQ3_XXS: in the
+    // high half of its dword for odd sb), and the unit D = d 2^24 (Q4_K) or
+    // d 2^22 (IQ3_XXS); 1, with B zeroed, when d == 0.
+    auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
+        if constexpr (IQ3) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
+        return nhdr[nb].x;
+    };
+    auto unit = [](uint32_t bits) {
+        const float d = half_bits_to_float(bits);
+        return d != 0.f ? d * (IQ3 ? 4194304.f : 16777216.f) : 1.f;
     };
 
     // Only the first ceil(n / 16) 16-row blocks of the tile issue MFMAs; the
     // main loop is instantiated for 1..4 active row blocks.
+    //   Prefetch: vector-memory loads complete in issue order, so waiting for
+    // slab s + 1's A also waits for every load issued before it. A and B are
+    // therefore loaded together, A DA slabs ahead (register sets s % DA) and B
+    // DEPTH >= DA slabs ahead, with the next superblock's header after them.
+    // Small tiles, bound by load latency, have the registers for DA = 4 (one
+    // row block) or 2 (two).
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
+        constexpr uint32_t DA = MBE == 1 ? 4u : MBE == 2 ? 2u : 1u;
+        constexpr uint32_t DEPTH = DA > 2u ? DA : 2u;
+        uint4 pah[DA][4], pal[DA][4];
         floatx4 acc[MBE][NB];
+        float dlast[NB] = {1.f, 1.f, 1.f, 1.f};  // IQ4_NL: the accumulator's unit
 #pragma unroll
         for (int i = 0; i < MBE; ++i)
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        load_hdr(0);
-        load_qs(nqs[0], 0);
-        load_qs(nqs[1], 1);
-        INGOT_LOAD_A(0u);
-        INGOT_LOAD_S(0u);
-        for (uint32_t sb = 0; sb < sbs; ++sb) {
+        if constexpr (!IQ4) load_hdr(0);
+        if constexpr (Q4K) INGOT_LOAD_S(0u);
+#pragma unroll
+        for (uint32_t d = 0; d < DEPTH; ++d) {
+            if (d < DA) INGOT_LOAD_A(d, d);
+            load_slab(d, d);
+        }
+        for (uint32_t s0 = 0; s0 < slabs; s0 += UNR) {
+            const uint32_t sb = s0 >> 2;
             uint32_t sc[NB][2], mn[NB][2];
+            uint32_t gw[NB][4], aw[NB][2];  // IQ3_XXS: this superblock's grid and sign/scale words
             float dsc[NB], dmn[NB];
-    #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                hdr[nb] = nhdr[nb];
-                q4k_sc_mn(hdr[nb], sc[nb][0], sc[nb][1], mn[nb][0], mn[nb][1]);
-                dsc[nb] = dscale(hdr[nb]);
-                dmn[nb] = half_bits_to_float(hdr[nb].x >> 16) * 16777216.f;
-                if (half_bits_to_float(hdr[nb].x) == 0.f) sc[nb][0] = sc[nb][1] = 0u;
+            if constexpr (!IQ4) {
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t db = dbits(nb, sb);
+                    dsc[nb] = unit(db);
+                    if constexpr (Q4K) {
+                        hdr[nb] = nhdr[nb];
+                        q4k_sc_mn(hdr[nb], sc[nb][0], sc[nb][1], mn[nb][0], mn[nb][1]);
+                        dmn[nb] = half_bits_to_float(hdr[nb].x >> 16) * 16777216.f;
+                        if (half_bits_to_float(hdr[nb].x) == 0.f) sc[nb][0] = sc[nb][1] = 0u;
+                    } else {
+                        // The lane's 4 grid words and 2 sign/scale words, aligned.
+                        const bool odd = (sb & 1u) != 0u;
+                        const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
+                        const uint32_t v[3] = {n3[nb].x, n3[nb].y, n3[nb].z};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) gw[nb][i] = odd ? w[i + 1] : __builtin_amdgcn_alignbit(w[i + 1], w[i], 16u);
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) aw[nb][i] = odd ? v[i + 1] : __builtin_amdgcn_alignbit(v[i + 1], v[i], 16u);
+                        sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;  // B multiplier (0 zeroes B)
+                    }
+                }
             }
-            load_hdr(sb + 1);
             _Float16* const sbuf = Ss[sb & 1u];
-    #pragma unroll
-            for (uint32_t sq = 0; sq < 4; ++sq) {
-                const uint32_t s = 4u * sb + sq;
+#pragma unroll
+            for (uint32_t sq = 0; sq < UNR; ++sq) {
+                const uint32_t s = s0 + sq;
+                if constexpr (IQ4) {
+                    if (s >= slabs) break;  // uniform
+                }
                 _Float16* const bh = Ash[sq & 1u];
                 _Float16* const bl = Asl[sq & 1u];
-                {
-                    const uint4 vh[4] = {pa_h0, pa_h1, pa_h2, pa_h3}, vl[4] = {pa_l0, pa_l1, pa_l2, pa_l3};
-    #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t r_ = ar0 + 16u * j;
-                        const uint32_t off = r_ * 64u + 8u * (ac ^ ((r_ >> 1) & 7u));
-                        *reinterpret_cast<uint4*>(&bh[off]) = vh[j];
-                        *reinterpret_cast<uint4*>(&bl[off]) = vl[j];
+                const uint32_t aset = sq % DA;
+#pragma unroll
+                for (int j = 0; j < MBE; ++j) {
+                    const uint32_t r_ = ar0 + 16u * j;
+                    const uint32_t off = r_ * 64u + 8u * (ac ^ ((r_ >> 1) & 7u));
+                    *reinterpret_cast<uint4*>(&bh[off]) = pah[aset][j];
+                    *reinterpret_cast<uint4*>(&bl[off]) = pal[aset][j];
+                }
+                if constexpr (Q4K) {
+                    if (sq == 0) {
+                        const float v[4] = {ps.x, ps.y, ps.z, ps.w};
+                        _Float16 h[4], l[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
+                        *reinterpret_cast<uint2*>(&sbuf[am * 16u + 4u * ahalf]) =
+                            make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
+                        *reinterpret_cast<uint2*>(&sbuf[am * 16u + 8u + 4u * ahalf]) =
+                            make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
                     }
                 }
-                if (sq == 0) {
-                    const float v[4] = {ps.x, ps.y, ps.z, ps.w};
-                    _Float16 h[4], l[4];
-    #pragma unroll
-                    for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
-                    *reinterpret_cast<uint2*>(&sbuf[am * 16u + 4u * ahalf]) = make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
-                    *reinterpret_cast<uint2*>(&sbuf[am * 16u + 8u + 4u * ahalf]) =
-                        make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
-                    INGOT_LOAD_S(sb + 1u);
-                }
-                INGOT_LOAD_A(s + 1u);
-                // B operands of this slab: group 2 sq (low nibbles) and 2 sq + 1 (high nibbles).
-                uint2 qs[NB];
-    #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) qs[nb] = nqs[sq & 1u][nb];
-                load_qs(nqs[sq & 1u], s + 2);
-                half8 fb[NB][2];
-    #pragma unroll
+                INGOT_LOAD_A(aset, s + DA);
+                uint4 qv[NB];
+                uint2 dv[NB];
+                const uint32_t slot = sq % DEPTH;
+#pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    const uint32_t scw = sc[nb][sq >> 1] >> (16u * (sq & 1u));
-                    const uint32_t s0 = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
-                    const uint32_t s1 = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
-                    fb[nb][0] = q4_operand(qs[nb].x & 0x0f0f0f0fu, qs[nb].y & 0x0f0f0f0fu, s0);
-                    fb[nb][1] = q4_operand((qs[nb].x >> 4) & 0x0f0f0f0fu, (qs[nb].y >> 4) & 0x0f0f0f0fu, s1);
+                    qv[nb] = nq[slot][nb];
+                    if constexpr (IQ4) {
+                        qv[nb].z = n1[slot][nb];
+                        dv[nb] = nd[slot][nb];
+                    }
+                }
+                load_slab(slot, s + DEPTH);
+                if constexpr (!IQ4) {
+                    if (sq == 0) {
+                        load_hdr(sb + 1);
+                        if constexpr (Q4K) INGOT_LOAD_S(sb + 1u);
+                    }
+                }
+                // B operands of this slab, fb[nb][gi] for the lane's 8 values of MFMA gi.
+                half8 fb[NB][2];
+                float dg[NB][2];     // IQ4_NL: unit D of blocks 2 s + gi
+                bool dzero = false;  // IQ4_NL: some block of the lane has d == 0
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    if constexpr (Q4K) {
+                        // groups 2 sq (low nibbles) and 2 sq + 1 (high nibbles)
+                        const uint32_t scw = sc[nb][sq >> 1] >> (16u * (sq & 1u));
+                        const uint32_t s0_ = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
+                        const uint32_t s1_ = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
+                        fb[nb][0] = q4_operand(qv[nb].x & 0x0f0f0f0fu, qv[nb].y & 0x0f0f0f0fu, s0_);
+                        fb[nb][1] = q4_operand((qv[nb].x >> 4) & 0x0f0f0f0fu, (qv[nb].y >> 4) & 0x0f0f0f0fu, s1_);
+                    } else if constexpr (IQ3) {
+                        // Lane kq, slab sq: grid bytes 16 kq + 4 sq .. +3 of the superblock
+                        // (values 64 kq + 16 sq .. +15; MFMA gi takes bytes 2 gi, 2 gi + 1),
+                        // sign/scale word of group 2 kq + sq / 2, sign chunks 2 (sq & 1) + gi.
+                        const uint32_t g = gw[nb][sq];
+                        const uint32_t x = aw[nb][sq >> 1];
+                        const uint32_t f = sc[nb][0] * (2u * (x >> 28) + 1u);
+                        const uint32_t f2 = f | (f << 16);
+#pragma unroll
+                        for (int gi = 0; gi < 2; ++gi) {
+                            const uint4 m = lds_iq3_signmask()[(x >> (14u * (sq & 1u) + 7u * gi)) & 127u];
+                            const uint32_t e0 = lds_iq3xxs_grid()[(g >> (16 * gi)) & 255u];
+                            const uint32_t e1 = lds_iq3xxs_grid()[(g >> (16 * gi + 8)) & 255u];
+                            fb[nb][gi] = __builtin_bit_cast(
+                                half8, make_uint4(mad_u16x2(bytes01(e0), f2, m.x), mad_u16x2(bytes23(e0), f2, m.y),
+                                                  mad_u16x2(bytes01(e1), f2, m.z), mad_u16x2(bytes23(e1), f2, m.w)));
+                        }
+                    } else {
+                        // The codebook lookups wait until the MFMA loop (fewer live
+                        // registers); here the quant words and block units D = d 2^24
+                        // (1 for d == 0, whose B is then zeroed).
+                        qv[nb].x = __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u);
+                        const float d0 = half_bits_to_float(dv[nb].x & 0xffffu);
+                        const float d1 = half_bits_to_float(dv[nb].y >> 16);
+                        dg[nb][0] = d0 != 0.f ? d0 * 16777216.f : 1.f;
+                        dg[nb][1] = d1 != 0.f ? d1 * 16777216.f : 1.f;
+                        dzero |= d0 == 0.f || d1 == 0.f;
+                    }
                 }
                 __syncthreads();
-    #pragma unroll
-                for (int gi = 0; gi < 2; ++gi)
-    #pragma unroll
-                    for (int part = 0; part < 2; ++part)
-    #pragma unroll
-                        for (int mb = 0; mb < MBE; ++mb) {
-                            const uint32_t ar = mb * 16u + ln;
-                            const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
-                            const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
-    #pragma unroll
-                            for (int nb = 0; nb < NB; ++nb)
-                                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                if constexpr (!IQ4) {
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+                        for (int part = 0; part < 2; ++part)
+#pragma unroll
+                            for (int mb = 0; mb < MBE; ++mb) {
+                                const uint32_t ar = mb * 16u + ln;
+                                const uint32_t ch = IQ3 ? 2u * kq + gi : 4u * gi + kq;
+                                const uint32_t off = ar * 64u + 8u * (ch ^ ((ar >> 1) & 7u));
+                                const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
+#pragma unroll
+                                for (int nb = 0; nb < NB; ++nb)
+                                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                            }
+                } else {
+                    // Block gi accumulates in units of its own D: the accumulator
+                    // moves from the previous block's units first.
+                    const bool zany = __builtin_amdgcn_ballot_w64(dzero) != 0u;
+#pragma unroll
+                    for (int gi = 0; gi < 2; ++gi) {
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) {
+                            const uint32_t qq = gi ? qv[nb].z : qv[nb].x;
+                            const uint32_t* const P = lds_iq4nl_pairs();
+                            uint4 b = make_uint4(P[qq & 255u], P[(qq >> 8) & 255u], P[(qq >> 16) & 255u], P[qq >> 24]);
+                            if (zany) {
+                                const bool z = half_bits_to_float(gi ? dv[nb].y >> 16 : dv[nb].x & 0xffffu) == 0.f;
+                                if (z) b = make_uint4(0u, 0u, 0u, 0u);
+                            }
+                            fb[nb][gi] = __builtin_bit_cast(half8, b);
                         }
-                if (sq == 3) {
-                    // Mins of the superblock and the move to the next superblock's units.
-                    half8 fm[NB];
-    #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        const uint4 v = kq < 2 ? make_uint4(bytes01(mn[nb][0]), bytes23(mn[nb][0]), bytes01(mn[nb][1]),
-                                                            bytes23(mn[nb][1]))
-                                               : make_uint4(0, 0, 0, 0);
-                        fm[nb] = __builtin_bit_cast(half8, v);
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) {
+                            const float f1 = dlast[nb] * __builtin_amdgcn_rcpf(dg[nb][gi]);
+                            dlast[nb] = dg[nb][gi];
+#pragma unroll
+                            for (int mb = 0; mb < MBE; ++mb)
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) acc[mb][nb][j] *= f1;
+                        }
+#pragma unroll
+                        for (int part = 0; part < 2; ++part)
+#pragma unroll
+                            for (int mb = 0; mb < MBE; ++mb) {
+                                const uint32_t ar = mb * 16u + ln;
+                                const uint32_t off = ar * 64u + 8u * ((4u * gi + kq) ^ ((ar >> 1) & 7u));
+                                const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
+#pragma unroll
+                                for (int nb = 0; nb < NB; ++nb)
+                                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                            }
                     }
-                    float f1[NB], f2[NB];
-    #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        const float rn = sb + 1 < sbs ? __builtin_amdgcn_rcpf(dscale(nhdr[nb])) : 1.f;
-                        f1[nb] = dsc[nb] * rn;
-                        f2[nb] = -dmn[nb] * rn;
+                }
+                if constexpr (Q4K) {
+                    if (sq == 3) {
+                        // Mins of the superblock and the move to the next superblock's units.
+                        half8 fm[NB];
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) {
+                            const uint4 v = kq < 2 ? make_uint4(bytes01(mn[nb][0]), bytes23(mn[nb][0]),
+                                                                bytes01(mn[nb][1]), bytes23(mn[nb][1]))
+                                                   : make_uint4(0, 0, 0, 0);
+                            fm[nb] = __builtin_bit_cast(half8, v);
+                        }
+                        float f1[NB], f2[NB];
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) {
+                            const float rn = sb + 1 < sbs ? __builtin_amdgcn_rcpf(unit(dbits(nb, sb + 1))) : 1.f;
+                            f1[nb] = dsc[nb] * rn;
+                            f2[nb] = -dmn[nb] * rn;
+                        }
+                        // Four independent MFMAs per row block before their results are
+                        // used, so the updates do not wait on each MFMA in turn.
+#pragma unroll
+                        for (int mb = 0; mb < MBE; ++mb) {
+                            const half8 sa =
+                                *reinterpret_cast<const half8*>(&sbuf[(mb * 16u + ln) * 16u + 8u * (kq & 1u)]);
+                            floatx4 mc[NB];
+#pragma unroll
+                            for (int nb = 0; nb < NB; ++nb)
+                                mc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, fm[nb], floatx4{0.f, 0.f, 0.f, 0.f},
+                                                                                0, 0, 0);
+#pragma unroll
+                            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                                for (int j = 0; j < 4; ++j)
+                                    acc[mb][nb][j] = acc[mb][nb][j] * f1[nb] + mc[nb][j] * f2[nb];
+                        }
                     }
-                    // Four independent MFMAs per row block before their results are
-                    // used, so the updates do not wait on each MFMA in turn.
-    #pragma unroll
-                    for (int mb = 0; mb < MBE; ++mb) {
-                        const half8 sa = *reinterpret_cast<const half8*>(&sbuf[(mb * 16u + ln) * 16u + 8u * (kq & 1u)]);
-                        floatx4 mc[NB];
-    #pragma unroll
-                        for (int nb = 0; nb < NB; ++nb)
-                            mc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, fm[nb], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    #pragma unroll
-                        for (int nb = 0; nb < NB; ++nb)
-    #pragma unroll
-                            for (int j = 0; j < 4; ++j) acc[mb][nb][j] = acc[mb][nb][j] * f1[nb] + mc[nb][j] * f2[nb];
+                } else if constexpr (IQ3) {
+                    if (sq == 3) {
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) {
+                            const float f1 =
+                                dsc[nb] * (sb + 1 < sbs ? __builtin_amdgcn_rcpf(unit(dbits(nb, sb + 1))) : 1.f);
+#pragma unroll
+                            for (int mb = 0; mb < MBE; ++mb)
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) acc[mb][nb][j] *= f1;
+                        }
                     }
                 }
             }
         }
-    #pragma unroll
+        if constexpr (IQ4) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < MBE; ++mb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[mb][nb][j] *= dlast[nb];
+        }
+#pragma unroll
         for (int mb = 0; mb < MBE; ++mb)
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t m = mb * 16u + 4u * kq + j;
                 const uint64_t q = q0 + m;
                 if (GATEUP) {
-                    float gsum = 0.f;
-    #pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const uint32_t r = row0 + 32u * wave + 16u * c + ln;
-                        const float v = swiglu(acc[mb][c][j], acc[mb][2 + c][j], limit);
-                        gsum += v;
-                        _Float16 xh, xl;
-                        split_f16(v, xh, xl);
-                        if (m < n) {
-                            out_h[q * ldo + r] = xh;
-                            out_l[q * ldo + r] = xl;
+                    const float v0 = swiglu(acc[mb][0][j], acc[mb][2][j], limit);
+                    const float v1 = swiglu(acc[mb][1][j], acc[mb][3][j], limit);
+                    _Float16 h0, l0, h1, l1;
+                    split_f16(v0, h0, l0);
+                    split_f16(v1, h1, l1);
+                    if (m < n) {
+                        if (AORD == A_IQ4NL) {
+                            // columns c0 = ln and c1 = 16 + ln of the wave's 32-column group
+                            // go to 8 (ln / 4) + 2 (ln % 4) + {0, 1}: one 4-byte store each.
+                            const uint64_t o = q * ldo + row0 + 32u * wave + 8u * (ln >> 2) + 2u * (ln & 3u);
+                            *reinterpret_cast<uint32_t*>(out_h + o) = pack_h2(h0, h1);
+                            *reinterpret_cast<uint32_t*>(out_l + o) = pack_h2(l0, l1);
+                        } else {
+                            const uint64_t o0 = q * ldo + a_pos<AORD>(row0 + 32u * wave + ln);
+                            const uint64_t o1 = q * ldo + a_pos<AORD>(row0 + 32u * wave + 16u + ln);
+                            out_h[o0] = h0;
+                            out_l[o0] = l0;
+                            out_h[o1] = h1;
+                            out_l[o1] = l1;
                         }
                     }
-                    // 32-column sum of act over this wave's columns (16 lanes x 2).
-                    gsum += dpp_mov<0xb1>(gsum);
-                    gsum += dpp_mov<0x4e>(gsum);
-                    gsum += dpp_mov<0x141>(gsum);
-                    gsum += dpp_mov<0x140>(gsum);
-                    if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
+                    if (out_gs != nullptr) {
+                        // 32-column sum of act over this wave's columns (16 lanes x 2).
+                        float gsum = v0 + v1;
+                        gsum += dpp_mov<0xb1>(gsum);
+                        gsum += dpp_mov<0x4e>(gsum);
+                        gsum += dpp_mov<0x141>(gsum);
+                        gsum += dpp_mov<0x140>(gsum);
+                        if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
+                    }
                 } else {
                     if (m < n) {
-    #pragma unroll
+#pragma unroll
                         for (int nb = 0; nb < NB; ++nb) out[q * ldo + row0 + 64u * wave + 16u * nb + ln] = acc[mb][nb][j];
                     }
                 }
@@ -1421,20 +1704,24 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         default: run(std::integral_constant<int, 4>{}); break;
     }
 #undef INGOT_LOAD_A
+#undef INGOT_LOAD_A1
 #undef INGOT_LOAD_S
 }
 
-// x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)) and
-// the 32-column sums xs [T][H/32] used by the Q4_K mins term.
+// x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)),
+// stored in column order `order` (A_NATURAL or A_IQ3XXS, whose permutation
+// keeps runs of 4 columns together; H % 256 == 0 for the latter), and the
+// natural 32-column sums xs [T][H/32] used by the Q4_K mins term.
 __global__ __launch_bounds__(256) void k_split_f16(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
-                                                   _Float16* __restrict__ xl, float* __restrict__ xs) {
+                                                   _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order) {
     const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4u;
     const bool live = i < n;
     const float4 v = live ? *reinterpret_cast<const float4*>(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float a[4] = {v.x, v.y, v.z, v.w};
     if (live) {
+        const uint64_t o = order == A_IQ3XXS ? (i & ~255ull) | a_pos<A_IQ3XXS>((uint32_t)i & 255u) : i;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) split_f16(a[j], xh[i + j], xl[i + j]);
+        for (int j = 0; j < 4; ++j) split_f16(a[j], xh[o + j], xl[o + j]);
     }
     // 8 consecutive threads cover one 32-column group (n is a multiple of 32).
     float s = (a[0] + a[1]) + (a[2] + a[3]);

@@ -113,6 +113,34 @@ def test_shared_expert_gated_and_ungated(gpu, oracle):
         layer.destroy()
 
 
+BLOCK_BYTES = {Q4_K: 144, IQ3_XXS: 98, IQ4_NL: 18}  # each block starts with its f16 scale d
+
+
+def zero_scales(m, every=7, phase=3):
+    """Sets d = 0 in every `every`-th block of a matrix (ggml writes such blocks for all-zero weights)."""
+    bb = BLOCK_BYTES[m.kind]
+    nblk = m.stride // bb
+    blocks = m.data.copy().reshape(m.rows * m.count, nblk, bb)
+    hit = (np.arange(blocks.shape[0] * nblk).reshape(-1, nblk) % every) == phase
+    blocks[hit, 0:2] = 0
+    m.data = blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("gk,dk,sf", [(Q4_K, IQ4_NL, 512), (IQ3_XXS, Q4_K, 512), (IQ3_XXS, IQ3_XXS, 512),
+                                      (IQ3_XXS, IQ4_NL, 256), (Q4_K, Q4_K, 512)])
+def test_f16_gemm_formats_shared_and_zero_scales(gpu, oracle, gk, dk, sf):
+    """Every format pair the f16 grouped GEMM takes, with a shared expert that joins its launches
+    (same formats and width, sf == 512) or runs on the fp32 GEMM beside them (sf == 256), and
+    blocks whose scale d is zero (unit 1, zeroed operand)."""
+    spec = CF.make_layer(9, 10 * gk + dk, 2048, 16, 4, 512, gk, dk, shared_ffn=sf)
+    for m in (spec.gate, spec.up, spec.down, *spec.shared):
+        zero_scales(m)
+    layer = MoeLayer(gpu, spec)
+    for T in (70, 130):  # 2 and 3 shared-expert tiles, partial last tiles
+        check_layer(layer, spec, CF.inputs(9, T, 2048, seed=T), oracle, f"f16 {gk}/{dk} shared {sf} T={T}")
+    layer.destroy()
+
+
 def test_sigmoid_routing_scale_and_clamp(gpu, oracle):
     spec = small_layer(Q4_K, Q4_K, routing=ROUTE_SIGMOID, route_scale=2.5, bias="uniform")
     spec.swiglu_limit = 10.0
