@@ -96,6 +96,65 @@ struct RouteLds {
     float* w;
 };
 
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), (int)l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Selection for larger E (E <= 2 * blockDim.x, K <= 64, blockDim.x / 64 * K
+// <= 1024), from keys[0..E) (zero above E) and vals in LDS; writes
+// sel_id/sel_v[0..K). Each wave ranks its own keys (lane j holds keys j and
+// j + blockDim.x of its wave's range) against the wave's keys read by lane
+// broadcasts; a wave's keys of rank < K are candidates, and every global top-K
+// key is one (whatever beats it is also in the global top K). The candidates,
+// at most K per wave, are then ranked against each other: a candidate's rank
+// among them is its global rank when that rank is below K.
+__device__ inline void block_route_select_large(uint32_t E, uint32_t K, RouteLds s) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, wave = tid >> 6, slots = (nt >> 6) * K;
+    const uint32_t e0 = tid, e1 = tid + nt;
+    const uint64_t k0 = e0 < E ? s.keys[e0] : 0ull, k1 = e1 < E ? s.keys[e1] : 0ull;
+    const float v0 = e0 < E ? s.vals[e0] : 0.f, v1 = e1 < E ? s.vals[e1] : 0.f;
+    uint32_t r0 = 0, r1 = 0;
+    const bool two = E > nt;
+#pragma unroll 8
+    for (uint32_t src = 0; src < 64u; ++src) {
+        const uint64_t a = readlane_u64(k0, src);
+        r0 += a > k0 ? 1u : 0u;
+        r1 += a > k1 ? 1u : 0u;
+        if (two) {
+            const uint64_t b = readlane_u64(k1, src);
+            r0 += b > k0 ? 1u : 0u;
+            r1 += b > k1 ? 1u : 0u;
+        }
+    }
+    __syncthreads();  // every thread holds its keys: the key array becomes the candidate slots
+    for (uint32_t i = tid; i < slots; i += nt) s.keys[i] = 0;
+    __syncthreads();
+    if (k0 != 0ull && r0 < K) {
+        s.keys[wave * K + r0] = k0;
+        s.vals[wave * K + r0] = v0;
+        s.rank[wave * K + r0] = e0;
+    }
+    if (k1 != 0ull && r1 < K) {
+        s.keys[wave * K + r1] = k1;
+        s.vals[wave * K + r1] = v1;
+        s.rank[wave * K + r1] = e1;
+    }
+    __syncthreads();
+    if (tid < slots) {
+        const uint64_t mine = s.keys[tid];
+        if (mine != 0ull) {
+            uint32_t c = 0;
+            for (uint32_t i = 0; i < slots; ++i) c += s.keys[i] > mine ? 1u : 0u;
+            if (c < K) {
+                s.sel_id[c] = s.rank[tid];
+                s.sel_v[c] = s.vals[tid];
+            }
+        }
+    }
+}
+
 __device__ inline void block_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
                                    uint32_t sigmoid_mode, float scale, RouteLds s, uint32_t* __restrict__ flags) {
     INGOT_NO_CONTRACT
@@ -121,27 +180,31 @@ __device__ inline void block_route(const float* __restrict__ l, const float* __r
     for (uint32_t e = E + tid; e < E16; e += nt) s.keys[e] = 0;  // below every real key
     if (flags && __any(bad) && (tid & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
     __syncthreads();
-    // rank[e] = number of keys above key e (keys are distinct), counted over
-    // (expert, 16-key group) items spread across the block; consecutive
-    // threads share a group, so its keys are LDS broadcasts.
-    const uint32_t G = E16 / 16u;
-    for (uint32_t item = tid; item < E * G; item += nt) {
-        const uint32_t g = item / E, e = item - g * E;
-        const uint64_t mine = s.keys[e];
-        ulonglong2 kv[8];
+    if (E > 128u) {
+        block_route_select_large(E, K, s);
+    } else {
+        // rank[e] = number of keys above key e (keys are distinct), counted over
+        // (expert, 16-key group) items spread across the block; consecutive
+        // threads share a group, so its keys are LDS broadcasts.
+        const uint32_t G = E16 / 16u;
+        for (uint32_t item = tid; item < E * G; item += nt) {
+            const uint32_t g = item / E, e = item - g * E;
+            const uint64_t mine = s.keys[e];
+            ulonglong2 kv[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) kv[q] = *reinterpret_cast<const ulonglong2*>(&s.keys[16u * g + 2 * q]);
-        uint32_t c = 0;
+            for (int q = 0; q < 8; ++q) kv[q] = *reinterpret_cast<const ulonglong2*>(&s.keys[16u * g + 2 * q]);
+            uint32_t c = 0;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) c += (kv[q].x > mine ? 1u : 0u) + (kv[q].y > mine ? 1u : 0u);
-        if (c) atomicAdd(&s.rank[e], c);
-    }
-    __syncthreads();
-    for (uint32_t e = tid; e < E; e += nt) {
-        const uint32_t rank = s.rank[e];
-        if (rank < K) {
-            s.sel_id[rank] = e;
-            s.sel_v[rank] = s.vals[e];
+            for (int q = 0; q < 8; ++q) c += (kv[q].x > mine ? 1u : 0u) + (kv[q].y > mine ? 1u : 0u);
+            if (c) atomicAdd(&s.rank[e], c);
+        }
+        __syncthreads();
+        for (uint32_t e = tid; e < E; e += nt) {
+            const uint32_t rank = s.rank[e];
+            if (rank < K) {
+                s.sel_id[rank] = e;
+                s.sel_v[rank] = s.vals[e];
+            }
         }
     }
     __syncthreads();
@@ -510,11 +573,13 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     const uint32_t t = blockIdx.y;
     const uint32_t nch = H / 32u;
     const uint32_t r0 = blockIdx.x * RPW;
-    // Stage the token's input while the block routes it.
-    {
-        const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)t * H);
-        for (uint32_t i = threadIdx.x; i < H / 4u; i += 512u) reinterpret_cast<float4*>(s_x)[i] = x4[i];
-    }
+    // The token's input (H <= 4096: at most two float4 per thread) is loaded
+    // into registers now and written to LDS after the weight loads are issued,
+    // so its latency overlaps the routing's logit loads.
+    const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)t * H);
+    const uint32_t xi0 = threadIdx.x, xi1 = threadIdx.x + 512u;
+    const float4 xa = xi0 < H / 4u ? x4[xi0] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 xb = xi1 < H / 4u ? x4[xi1] : make_float4(0.f, 0.f, 0.f, 0.f);
     stage_codebooks<KIND>();  // decoded only after block_route's barriers
     block_route(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, scale, RouteLds{s_keys, s_vals, s_rank, s_id, s_v, s_w},
                 blockIdx.x == 0 ? flags : nullptr);
@@ -542,6 +607,9 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
         }
     }
+    if (xi0 < H / 4u) reinterpret_cast<float4*>(s_x)[xi0] = xa;
+    if (xi1 < H / 4u) reinterpret_cast<float4*>(s_x)[xi1] = xb;
+    __syncthreads();
     float xv[CPL][32], xs0[CPL], xs1[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -1006,15 +1074,15 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
         floatx4 acc[MBE][2];
-    #pragma unroll
+#pragma unroll
         for (int i = 0; i < MBE; ++i)
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
         float4 ar[4];
         typename Fm::Raw br;
         auto load = [&](uint32_t s) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < 4; ++i)
                 ar[i] = arow[i] ? *reinterpret_cast<const float4*>(arow[i] + 64u * s + acol) : make_float4(0.f, 0.f, 0.f, 0.f);
             br = Fm::load_raw(bptr, 2u * s + bh);
@@ -1022,7 +1090,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
         const uint32_t slabs = kdim / 64u;
         load(0);
         for (uint32_t s = 0; s < slabs; ++s) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < 4; ++i) {
                 uint32_t m = (tid + 256u * i) >> 4;
                 *reinterpret_cast<float4*>(&As[m * LDS_STRIDE + acol]) = ar[i];
@@ -1032,7 +1100,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
                 Fm::dequant_raw(br, 2u * s + bh, wv);
                 float* dst = &Bs[brow * LDS_STRIDE];
                 // Chunk value i -> slab column: Fm::col(chunk, i) - 64 s.
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < 32; i += 4) {
                     uint32_t cl = Fm::col(2u * s + bh, i) - 64u * s;
                     *reinterpret_cast<float4*>(dst + cl) = make_float4(wv[i], wv[i + 1], wv[i + 2], wv[i + 3]);
@@ -1040,24 +1108,24 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
             }
             __syncthreads();
             if (s + 1 < slabs) load(s + 1);
-    #pragma unroll
+#pragma unroll
             for (uint32_t kk = 0; kk < 4; ++kk) {
                 const uint32_t kc = kk * 16u + 4u * (lane >> 4);
                 float4 a[MBE], b[2];
-    #pragma unroll
+#pragma unroll
                 for (int mb = 0; mb < MBE; ++mb)
                     a[mb] = *reinterpret_cast<const float4*>(&As[(mb * 16u + (lane & 15u)) * LDS_STRIDE + kc]);
-    #pragma unroll
+#pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
                     // GATEUP: nb 0 = gate rows 16w.., nb 1 = up rows 64+16w..; else rows 32w + 16nb..
                     uint32_t br_ = GATEUP ? (nb * 64u + 16u * wave) : (32u * wave + 16u * nb);
                     b[nb] = *reinterpret_cast<const float4*>(&Bs[(br_ + (lane & 15u)) * LDS_STRIDE + kc]);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-    #pragma unroll
+#pragma unroll
                     for (int mb = 0; mb < MBE; ++mb)
-    #pragma unroll
+#pragma unroll
                         for (int nb = 0; nb < 2; ++nb) {
                             float av = ks == 0 ? a[mb].x : ks == 1 ? a[mb].y : ks == 2 ? a[mb].z : a[mb].w;
                             float bv = ks == 0 ? b[nb].x : ks == 1 ? b[nb].y : ks == 2 ? b[nb].z : b[nb].w;
@@ -1067,9 +1135,9 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
             __syncthreads();
         }
         // Epilogue: lane holds D[m = 4*(lane/16) + j][n = lane%16] of each tile.
-    #pragma unroll
+#pragma unroll
         for (int mb = 0; mb < MBE; ++mb)
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < 4; ++j) {
                 uint32_t m = mb * 16u + 4u * (lane >> 4) + j;
                 if (m >= n) continue;
@@ -1078,7 +1146,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
                     uint32_t r = row0 + 16u * wave + (lane & 15u);
                     out[q * ldo + r] = swiglu(acc[mb][0][j], acc[mb][1][j], limit);
                 } else {
-    #pragma unroll
+#pragma unroll
                     for (int nb = 0; nb < 2; ++nb) {
                         uint32_t r = row0 + 32u * wave + 16u * nb + (lane & 15u);
                         out[q * ldo + r] = acc[mb][nb][j];

@@ -206,6 +206,24 @@ def test_route_ties_across_lanes_top8(gpu, oracle):
     layer.destroy()
 
 
+@pytest.mark.parametrize("E,K", [(256, 10), (1024, 16)])
+def test_decode_route_many_experts_ties(gpu, oracle, E, K):
+    """Decode routing above 128 experts (each wave ranks its own keys; the waves' best K are then
+    ranked against each other), with ties inside a wave, across waves and between the two keys a
+    lane holds when E > 512: ids bit-exact, lower id first."""
+    H = 1024
+    spec = identity_router_layer(E, K, H, F=64, kind=Q8_0)
+    x = CF.inputs(14, 4, H) * 0.05
+    x[0, :E] = 1.0                                          # all tied: ids 0..K-1
+    x[1, :E] = ((np.arange(E) * 17) % 23) - 11.0            # ties spread over every wave
+    x[2, :E] = np.where(np.arange(E) % 64 == 9, 3.0, 0.0)   # ties at one lane of every wave
+    x[3, :E] = np.where(np.arange(E) % 512 == 7, 2.0, 0.0)  # ties between a lane's two keys
+    layer = MoeLayer(gpu, spec)
+    out, ids, w = check_layer(layer, spec, x, oracle, f"route E={E} K={K}")
+    assert list(ids[0]) == list(range(K))
+    layer.destroy()
+
+
 # ----------------------------------------------------------- errors, graphs
 def test_nonfinite_input_rejected(gpu):
     spec = small_layer(Q4_K, Q4_K)
