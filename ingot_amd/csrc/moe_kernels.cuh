@@ -1294,11 +1294,29 @@ __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
 
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt fields at their maxima).
+template <uint32_t N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N < 64, "vmcnt has 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15u) | ((N >> 4) << 14));
+}
+
 // Grouped GEMM on f16 MFMA for Q4_K, IQ3_XXS and IQ4_NL weights (see the
 // block comment above). e_shared names the tile expert id whose weights are
 // ws0/ws1 (the shared expert, run in the same launch); no tile carries it when
 // it is 0xffffffff. AORD (gate/up only) is the column order in which act is
 // stored: the order the down projection's format reads (a_pos).
+//   Pipeline. A slabs go straight from L2 to LDS (buffer_load ... lds; lane i
+// of a load writes 16 bytes at M0 + 16 i), two buffers by slab parity, so A
+// takes no registers. Per slab s: barrier; A(s + 1) into the other buffer, the
+// B ring's loads, at a superblock's first slab the next header (these loads
+// kept together and in this order); MFMAs of slab s with the operands decoded
+// one slab earlier, and the decode of slab s + 1 (into a second operand set,
+// interleaved with the MFMAs, when the tile has at most two row blocks; after
+// them otherwise); at a superblock's end the mins and the unit change; then a
+// wait for this wave's A(s + 1) only (vector-memory loads complete in issue
+// order, so vmcnt counts the B loads issued after it), which the next barrier
+// publishes. Every A DMA has landed before the block exits.
 template <int KIND, bool GATEUP, int AORD>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ ws0,
@@ -1312,22 +1330,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     static_assert(KIND != 20 || !GATEUP, "IQ4_NL is read with permuted A, which only act provides");
     constexpr int NB = 4;
     constexpr bool Q4K = KIND == 12, IQ3 = KIND == 18, IQ4 = KIND == 20;
-    // Slabs per step of the main loop: one 256-column superblock (Q4_K,
-    // IQ3_XXS); IQ4_NL steps the same way and stops at the last slab.
     constexpr uint32_t UNR = 4u;
-    // A tiles, double-buffered by slab parity: 64 halves (128 B) per row,
-    // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7) so that the
-    // stores and the MFMA fragment reads (16 rows at one chunk) touch every
-    // bank once. S tiles (Q4_K) double-buffered by superblock parity.
-    __shared__ _Float16 Ash[2][TM16 * 64];
-    __shared__ _Float16 Asl[2][TM16 * 64];
+    // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
+    // 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7), so that the fragment
+    // reads (16 rows at one chunk) touch every bank once. Separate objects, so
+    // that the compiler sees that a DMA into one never aliases reads of the
+    // other. S tiles (Q4_K group sums) by superblock parity.
+    __shared__ _Float16 Ah0[TM16 * 64], Ah1[TM16 * 64], Al0[TM16 * 64], Al1[TM16 * 64];
     __shared__ _Float16 Ss[2][TM16 * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
-    // 1-D grid of 8 * nblk * ceil(cap / 8) blocks. The hardware deals blocks to
-    // the 8 XCDs round-robin (block h runs on XCD h % 8); XCD x takes tiles
-    // x, x + 8, x + 16, ... in list order (shared-expert tiles, full tiles,
-    // then partial tiles by decreasing size) with all nblk row blocks of each
-    // tile, so a tile's A rows are fetched into one XCD's L2 and the blocks
-    // each XCD runs last are its smallest tiles.
     const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk;
     const uint32_t t = ti * 8u + (blockIdx.x & 7u);
     if (t >= nt) return;
@@ -1344,27 +1354,24 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t row0 = (slot - ti * nblk) * (GATEUP ? 64u : 128u);
     const uint32_t ngroups = kdim / 32u;
 
-    // Every global load below is a wave-uniform base (scalar registers) plus a
-    // loop-invariant 32-bit lane offset, so addressing costs no vector ALU.
-    const uint32_t ac = tid & 7u, ar0 = tid >> 3;
-    uint32_t aoff[4];  // byte offset of row ar0 + 16 j, chunk ac, in ah / al
+    // A DMA: instruction i of wave w fills tile rows 8 (2 i + w) .. + 7; lane l
+    // writes row r = 8 (2 i + w) + l / 8 at LDS slot l % 8, which holds chunk
+    // (l % 8) ^ ((r >> 1) & 7) of the row (the swizzle of the fragment reads).
+    uint32_t avo[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t m = ar0 + 16u * j;
-        const uint32_t q = q0 + (m < n ? m : 0u);
-        const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
-        aoff[j] = 2u * (r * kdim + 8u * ac);
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = 8u * (2u * i + wave) + (lane >> 3);
+        const uint32_t q = q0 + (r < n ? r : 0u);
+        const uint32_t arow = GATEUP ? (pairs ? pairs[q] / K : q) : q;
+        avo[i] = 2u * (arow * kdim + 8u * ((lane & 7u) ^ ((r >> 1) & 7u)));
     }
     const uint32_t am = tid >> 1, ahalf = tid & 1u;
-    uint32_t soff = 0;  // byte offset of this thread's group sums in gs (Q4_K)
+    uint32_t soff = 0;
     if constexpr (Q4K) {
         const uint32_t q = q0 + (am < n ? am : 0u);
         const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
         soff = 4u * (r * ngroups + 4u * ahalf);
     }
-    // Buffer resources: A halves and group sums over their whole arrays, the
-    // weights over this expert's slab (rows_per_expert rows); the slab and
-    // row-block parts of an offset go in the scalar offset.
     const bool sh_tile = e == e_shared;
     const uint8_t* const wb0 = sh_tile ? ws0 : w0 + (uint64_t)e * rows_per_expert * stride0;
     const uint8_t* const wb1 = GATEUP ? (sh_tile ? ws1 : w1 + (uint64_t)e * rows_per_expert * stride1) : wb0;
@@ -1373,8 +1380,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const __amdgpu_buffer_rsrc_t rgs = make_rsrc(gs, ngroups * 4u * a_rows);
     const __amdgpu_buffer_rsrc_t rw0 = make_rsrc(wb0, (uint32_t)(rows_per_expert * stride0));
     const __amdgpu_buffer_rsrc_t rw1 = GATEUP ? make_rsrc(wb1, (uint32_t)(rows_per_expert * stride1)) : rw0;
-    uint32_t bsoff[NB];  // wave-uniform byte offset of row 0 of n-block nb in its expert slab
-    uint32_t boff[NB];   // lane: its row within the n-block
+    uint32_t bsoff[NB], boff[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         if (GATEUP) {
@@ -1386,25 +1392,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             boff[nb] = ln * (uint32_t)stride0;
         }
     }
-
     const uint32_t slabs = kdim / 64u, sbs = kdim / 256u;
-    // Loads past the last slab or superblock re-read the last one (uniform,
-    // branch-free, never used).
-    const uint32_t aoff0 = aoff[0], aoff1 = aoff[1], aoff2 = aoff[2], aoff3 = aoff[3];
-    // A rows of active row blocks only (ar0 + 16 j, j < MBE) into register set SET.
-#define INGOT_LOAD_A1(SET, J, S_) pah[SET][J] = buf_load16(ra_h, aoff##J, 128u * (S_)); pal[SET][J] = buf_load16(ra_l, aoff##J, 128u * (S_))
-#define INGOT_LOAD_A(SET, S) do { const uint32_t s_ = (S) < slabs ? (S) : slabs - 1u; INGOT_LOAD_A1(SET, 0, s_); if (MBE > 1) { INGOT_LOAD_A1(SET, 1, s_); } if (MBE > 2) { INGOT_LOAD_A1(SET, 2, s_); } if (MBE > 3) { INGOT_LOAD_A1(SET, 3, s_); } } while (0)
+
     float4 ps;
 #define INGOT_LOAD_S(SB) ps = __builtin_bit_cast(float4, buf_load16(rgs, soff, 32u * ((SB) < sbs ? (SB) : sbs - 1u)))
-    // Superblock headers, one superblock ahead: Q4_K {d, dmin, scales}; IQ3_XXS
-    // the dword holding d (superblock offset 98 sb is 2 mod 4 for odd sb, d
-    // then in the high half: row strides are multiples of 4).
-    uint4 hdr[NB], nhdr[NB];
-    // IQ3_XXS reads each lane's bytes once per superblock, one superblock
-    // ahead: lane kq takes grid bytes 16 kq .. +15 (nhdr, n5: 20-byte window)
-    // and the sign/scale words of groups 2 kq, 2 kq + 1 (n3: 12-byte window);
-    // a window starts 2 (even sb) or 4 (odd sb) bytes before its target and
-    // never passes the next superblock; n_d is the dword holding d.
+    uint4 nhdr[NB];
     uint32_t n5[NB], n_d[NB];
     uint3 n3[NB];
     auto load_hdr = [&](uint32_t sb) {
@@ -1423,11 +1415,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
     };
-    // Per-slab B bytes, DEPTH slabs ahead (ring slot s % DEPTH; see run()).
-    //   Q4_K: .xy = the lane's 8 nibble bytes.
-    //   IQ4_NL: .xy = slab bytes 4 kq .. +7 (block 0 quants 4 kq .. +3 at
-    //     offset 2); n1 = block 1 quants 4 kq .. +3; nd = slab dwords 0 and 4
-    //     (d of block 0 in the low half, d of block 1 in the high half).
     uint4 nq[4][NB];
     uint32_t n1[4][NB];
     uint2 nd[4][NB];
@@ -1450,9 +1437,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
     };
-    // Superblock d of n-block nb as loaded for superblock sb (IQ3_XXS: in the
-    // high half of its dword for odd sb), and the unit D = d 2^24 (Q4_K) or
-    // d 2^22 (IQ3_XXS); 1, with B zeroed, when d == 0.
     auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
         if constexpr (IQ3) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
         return nhdr[nb].x;
@@ -1461,61 +1445,142 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         const float d = half_bits_to_float(bits);
         return d != 0.f ? d * (IQ3 ? 4194304.f : 16777216.f) : 1.f;
     };
+    // Superblock state for the decode (and, at the superblock's end, the mins
+    // and the unit change).
+    struct SbState {
+        uint32_t sc[NB][2], mn[NB][2];
+        uint32_t gw[NB][4], aw[NB][2];
+        float dsc[NB], dmn[NB];
+    };
+    auto take_hdr = [&](SbState& st, uint32_t sb) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const uint32_t db = dbits(nb, sb);
+            st.dsc[nb] = unit(db);
+            if constexpr (Q4K) {
+                q4k_sc_mn(nhdr[nb], st.sc[nb][0], st.sc[nb][1], st.mn[nb][0], st.mn[nb][1]);
+                st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 16777216.f;
+                if (half_bits_to_float(nhdr[nb].x) == 0.f) st.sc[nb][0] = st.sc[nb][1] = 0u;
+            } else if constexpr (IQ3) {
+                const bool odd = (sb & 1u) != 0u;
+                const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
+                const uint32_t v[3] = {n3[nb].x, n3[nb].y, n3[nb].z};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) st.gw[nb][i] = odd ? w[i + 1] : __builtin_amdgcn_alignbit(w[i + 1], w[i], 16u);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) st.aw[nb][i] = odd ? v[i + 1] : __builtin_amdgcn_alignbit(v[i + 1], v[i], 16u);
+                st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
+            }
+        }
+    };
+    // Decode of slab position sq (within its superblock) into fb; IQ4_NL also
+    // yields the units of its two blocks and whether a d is zero.
+    auto decode = [&](const SbState& st, uint32_t sq, const uint4* qv, const uint2* dv, half8 (*fb)[2],
+                      float (*dg)[2]) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            if constexpr (Q4K) {
+                const uint32_t scw = st.sc[nb][sq >> 1] >> (16u * (sq & 1u));
+                const uint32_t s0_ = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
+                const uint32_t s1_ = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
+                fb[nb][0] = q4_operand(qv[nb].x & 0x0f0f0f0fu, qv[nb].y & 0x0f0f0f0fu, s0_);
+                fb[nb][1] = q4_operand((qv[nb].x >> 4) & 0x0f0f0f0fu, (qv[nb].y >> 4) & 0x0f0f0f0fu, s1_);
+            } else if constexpr (IQ3) {
+                const uint32_t g = st.gw[nb][sq];
+                const uint32_t x = st.aw[nb][sq >> 1];
+                const uint32_t f = st.sc[nb][0] * (2u * (x >> 28) + 1u);
+                const uint32_t f2 = f | (f << 16);
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    const uint4 m = lds_iq3_signmask()[(x >> (14u * (sq & 1u) + 7u * gi)) & 127u];
+                    const uint32_t e0 = lds_iq3xxs_grid()[(g >> (16 * gi)) & 255u];
+                    const uint32_t e1 = lds_iq3xxs_grid()[(g >> (16 * gi + 8)) & 255u];
+                    fb[nb][gi] = __builtin_bit_cast(
+                        half8, make_uint4(mad_u16x2(bytes01(e0), f2, m.x), mad_u16x2(bytes23(e0), f2, m.y),
+                                          mad_u16x2(bytes01(e1), f2, m.z), mad_u16x2(bytes23(e1), f2, m.w)));
+                }
+            } else {
+                const uint32_t qa = __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u), qb = qv[nb].z;
+                const uint32_t* const P = lds_iq4nl_pairs();
+                const float d0 = half_bits_to_float(dv[nb].x & 0xffffu), d1 = half_bits_to_float(dv[nb].y >> 16);
+                uint4 b0 = make_uint4(P[qa & 255u], P[(qa >> 8) & 255u], P[(qa >> 16) & 255u], P[qa >> 24]);
+                uint4 b1 = make_uint4(P[qb & 255u], P[(qb >> 8) & 255u], P[(qb >> 16) & 255u], P[qb >> 24]);
+                if (d0 == 0.f) b0 = make_uint4(0u, 0u, 0u, 0u);
+                if (d1 == 0.f) b1 = make_uint4(0u, 0u, 0u, 0u);
+                fb[nb][0] = __builtin_bit_cast(half8, b0);
+                fb[nb][1] = __builtin_bit_cast(half8, b1);
+                dg[nb][0] = d0 != 0.f ? d0 * 16777216.f : 1.f;
+                dg[nb][1] = d1 != 0.f ? d1 * 16777216.f : 1.f;
+            }
+        }
+    };
 
-    // Only the first ceil(n / 16) 16-row blocks of the tile issue MFMAs; the
-    // main loop is instantiated for 1..4 active row blocks.
-    //   Prefetch: vector-memory loads complete in issue order, so waiting for
-    // slab s + 1's A also waits for every load issued before it. A and B are
-    // therefore loaded together, A DA slabs ahead (register sets s % DA) and B
-    // DEPTH >= DA slabs ahead, with the next superblock's header after them.
-    // Small tiles, bound by load latency, have the registers for DA = 4 (one
-    // row block) or 2 (two).
+    // Q4_K group sums of this thread's row, split hi/lo, into an S buffer.
+    auto store_s = [&](_Float16* sb_) {
+        const float v[4] = {ps.x, ps.y, ps.z, ps.w};
+        _Float16 h[4], l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
+        *reinterpret_cast<uint2*>(&sb_[am * 16u + 4u * ahalf]) = make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
+        *reinterpret_cast<uint2*>(&sb_[am * 16u + 8u + 4u * ahalf]) = make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
+    };
+    // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
+    // superblock's first slab its header (and Q4_K group sums).
+    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : 0u;
+    constexpr uint32_t B_PER_SB = Q4K ? NB + 1u : IQ3 ? 5u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
-        constexpr uint32_t DA = MBE == 1 ? 4u : MBE == 2 ? 2u : 1u;
-        constexpr uint32_t DEPTH = DA > 2u ? DA : 2u;
-        uint4 pah[DA][4], pal[DA][4];
+        constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;
+        // Two operand sets let the decode of slab s + 1 interleave with slab s's
+        // MFMAs; with 3-4 row blocks the registers hold one set (IQ4_NL: two),
+        // and the decode follows the MFMAs in program order.
+        constexpr uint32_t NFB = (IQ4 || MBE <= 2) ? 2u : 1u;
+        typedef __attribute__((address_space(3))) void lds_void;
+        auto dma_a = [&](uint32_t buf, uint32_t s) {
+#pragma unroll
+            for (int i = 0; i < MBE; ++i) {
+                const uint32_t roff = 8u * (2u * i + wave) * 64u;
+                _Float16* const dh = (buf ? Ah1 : Ah0) + roff;
+                _Float16* const dl = (buf ? Al1 : Al0) + roff;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_h, (lds_void*)dh, 16, avo[i], 128u * s, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_l, (lds_void*)dl, 16, avo[i], 128u * s, 0, 0);
+            }
+        };
         floatx4 acc[MBE][NB];
-        float dlast[NB] = {1.f, 1.f, 1.f, 1.f};  // IQ4_NL: the accumulator's unit
+        float dlast[NB] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
         for (int i = 0; i < MBE; ++i)
 #pragma unroll
             for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // Prologue: A(0) into buffer 0; B ring; header of superblock 0; decode B(0).
+        dma_a(0u, 0u);
         if constexpr (!IQ4) load_hdr(0);
-        if constexpr (Q4K) INGOT_LOAD_S(0u);
+        if constexpr (Q4K) {
+            INGOT_LOAD_S(0u);
+            store_s(Ss[0]);
+        }
 #pragma unroll
-        for (uint32_t d = 0; d < DEPTH; ++d) {
-            if (d < DA) INGOT_LOAD_A(d, d);
-            load_slab(d, d);
+        for (uint32_t d = 0; d < DEPTH; ++d) load_slab(d, d);
+        SbState cur, nxt;
+        if constexpr (!IQ4) take_hdr(cur, 0u);
+        half8 fb[NFB][NB][2];
+        float dgs[NFB][NB][2];
+        {
+            uint4 qv[NB];
+            uint2 dv[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                qv[nb] = nq[0][nb];
+                if constexpr (IQ4) {
+                    qv[nb].z = n1[0][nb];
+                    dv[nb] = nd[0][nb];
+                }
+            }
+            load_slab(0, DEPTH);
+            decode(cur, 0u, qv, dv, fb[0], dgs[0]);
         }
         for (uint32_t s0 = 0; s0 < slabs; s0 += UNR) {
             const uint32_t sb = s0 >> 2;
-            uint32_t sc[NB][2], mn[NB][2];
-            uint32_t gw[NB][4], aw[NB][2];  // IQ3_XXS: this superblock's grid and sign/scale words
-            float dsc[NB], dmn[NB];
-            if constexpr (!IQ4) {
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const uint32_t db = dbits(nb, sb);
-                    dsc[nb] = unit(db);
-                    if constexpr (Q4K) {
-                        hdr[nb] = nhdr[nb];
-                        q4k_sc_mn(hdr[nb], sc[nb][0], sc[nb][1], mn[nb][0], mn[nb][1]);
-                        dmn[nb] = half_bits_to_float(hdr[nb].x >> 16) * 16777216.f;
-                        if (half_bits_to_float(hdr[nb].x) == 0.f) sc[nb][0] = sc[nb][1] = 0u;
-                    } else {
-                        // The lane's 4 grid words and 2 sign/scale words, aligned.
-                        const bool odd = (sb & 1u) != 0u;
-                        const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
-                        const uint32_t v[3] = {n3[nb].x, n3[nb].y, n3[nb].z};
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) gw[nb][i] = odd ? w[i + 1] : __builtin_amdgcn_alignbit(w[i + 1], w[i], 16u);
-#pragma unroll
-                        for (int i = 0; i < 2; ++i) aw[nb][i] = odd ? v[i + 1] : __builtin_amdgcn_alignbit(v[i + 1], v[i], 16u);
-                        sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;  // B multiplier (0 zeroes B)
-                    }
-                }
-            }
             _Float16* const sbuf = Ss[sb & 1u];
 #pragma unroll
             for (uint32_t sq = 0; sq < UNR; ++sq) {
@@ -1523,90 +1588,43 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 if constexpr (IQ4) {
                     if (s >= slabs) break;  // uniform
                 }
-                _Float16* const bh = Ash[sq & 1u];
-                _Float16* const bl = Asl[sq & 1u];
-                const uint32_t aset = sq % DA;
-#pragma unroll
-                for (int j = 0; j < MBE; ++j) {
-                    const uint32_t r_ = ar0 + 16u * j;
-                    const uint32_t off = r_ * 64u + 8u * (ac ^ ((r_ >> 1) & 7u));
-                    *reinterpret_cast<uint4*>(&bh[off]) = pah[aset][j];
-                    *reinterpret_cast<uint4*>(&bl[off]) = pal[aset][j];
-                }
-                if constexpr (Q4K) {
-                    if (sq == 0) {
-                        const float v[4] = {ps.x, ps.y, ps.z, ps.w};
-                        _Float16 h[4], l[4];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
-                        *reinterpret_cast<uint2*>(&sbuf[am * 16u + 4u * ahalf]) =
-                            make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
-                        *reinterpret_cast<uint2*>(&sbuf[am * 16u + 8u + 4u * ahalf]) =
-                            make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
-                    }
-                }
-                INGOT_LOAD_A(aset, s + DA);
+                __syncthreads();  // A(s), S of this superblock visible; the other A buffer free
+                // Loads of this slab, in this order and kept together: A(s + 1) into
+                // the other buffer (unconditionally: past the last slab it re-reads
+                // the last one into a buffer nobody reads; drained at the end), the
+                // B ring, the next superblock's header. The wait before the next
+                // barrier counts the loads issued after the A DMA.
+                __builtin_amdgcn_sched_barrier(0);
+                const bool more = s + 1u < slabs;
+                dma_a((sq + 1u) & 1u, more ? s + 1u : s);
+                // B of slab s + 1 out of the ring, B(s + 1 + DEPTH) into its slot.
+                const uint32_t rs = (sq + 1u) % DEPTH;
                 uint4 qv[NB];
                 uint2 dv[NB];
-                const uint32_t slot = sq % DEPTH;
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    qv[nb] = nq[slot][nb];
+                    qv[nb] = nq[rs][nb];
                     if constexpr (IQ4) {
-                        qv[nb].z = n1[slot][nb];
-                        dv[nb] = nd[slot][nb];
+                        qv[nb].z = n1[rs][nb];
+                        dv[nb] = nd[rs][nb];
                     }
                 }
-                load_slab(slot, s + DEPTH);
+                load_slab(rs, s + 1u + DEPTH);
                 if constexpr (!IQ4) {
                     if (sq == 0) {
                         load_hdr(sb + 1);
                         if constexpr (Q4K) INGOT_LOAD_S(sb + 1u);
                     }
                 }
-                // B operands of this slab, fb[nb][gi] for the lane's 8 values of MFMA gi.
-                half8 fb[NB][2];
-                float dg[NB][2];     // IQ4_NL: unit D of blocks 2 s + gi
-                bool dzero = false;  // IQ4_NL: some block of the lane has d == 0
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    if constexpr (Q4K) {
-                        // groups 2 sq (low nibbles) and 2 sq + 1 (high nibbles)
-                        const uint32_t scw = sc[nb][sq >> 1] >> (16u * (sq & 1u));
-                        const uint32_t s0_ = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
-                        const uint32_t s1_ = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
-                        fb[nb][0] = q4_operand(qv[nb].x & 0x0f0f0f0fu, qv[nb].y & 0x0f0f0f0fu, s0_);
-                        fb[nb][1] = q4_operand((qv[nb].x >> 4) & 0x0f0f0f0fu, (qv[nb].y >> 4) & 0x0f0f0f0fu, s1_);
-                    } else if constexpr (IQ3) {
-                        // Lane kq, slab sq: grid bytes 16 kq + 4 sq .. +3 of the superblock
-                        // (values 64 kq + 16 sq .. +15; MFMA gi takes bytes 2 gi, 2 gi + 1),
-                        // sign/scale word of group 2 kq + sq / 2, sign chunks 2 (sq & 1) + gi.
-                        const uint32_t g = gw[nb][sq];
-                        const uint32_t x = aw[nb][sq >> 1];
-                        const uint32_t f = sc[nb][0] * (2u * (x >> 28) + 1u);
-                        const uint32_t f2 = f | (f << 16);
-#pragma unroll
-                        for (int gi = 0; gi < 2; ++gi) {
-                            const uint4 m = lds_iq3_signmask()[(x >> (14u * (sq & 1u) + 7u * gi)) & 127u];
-                            const uint32_t e0 = lds_iq3xxs_grid()[(g >> (16 * gi)) & 255u];
-                            const uint32_t e1 = lds_iq3xxs_grid()[(g >> (16 * gi + 8)) & 255u];
-                            fb[nb][gi] = __builtin_bit_cast(
-                                half8, make_uint4(mad_u16x2(bytes01(e0), f2, m.x), mad_u16x2(bytes23(e0), f2, m.y),
-                                                  mad_u16x2(bytes01(e1), f2, m.z), mad_u16x2(bytes23(e1), f2, m.w)));
-                        }
-                    } else {
-                        // The codebook lookups wait until the MFMA loop (fewer live
-                        // registers); here the quant words and block units D = d 2^24
-                        // (1 for d == 0, whose B is then zeroed).
-                        qv[nb].x = __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u);
-                        const float d0 = half_bits_to_float(dv[nb].x & 0xffffu);
-                        const float d1 = half_bits_to_float(dv[nb].y >> 16);
-                        dg[nb][0] = d0 != 0.f ? d0 * 16777216.f : 1.f;
-                        dg[nb][1] = d1 != 0.f ? d1 * 16777216.f : 1.f;
-                        dzero |= d0 == 0.f || d1 == 0.f;
-                    }
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (!IQ4) {
+                    if (sq == 3 && more) take_hdr(nxt, sb + 1u);
                 }
-                __syncthreads();
+                // Decode B(s + 1) while this slab's MFMAs issue.
+                const uint32_t cb = NFB == 2u ? (sq & 1u) : 0u, nb_ = NFB == 2u ? cb ^ 1u : 0u;
+                if (NFB == 2u && more) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[nb_], dgs[nb_]);
+                const _Float16* const bh = (sq & 1u) ? Ah1 : Ah0;
+                const _Float16* const bl = (sq & 1u) ? Al1 : Al0;
                 if constexpr (!IQ4) {
 #pragma unroll
                     for (int gi = 0; gi < 2; ++gi)
@@ -1620,29 +1638,15 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                                 const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
 #pragma unroll
                                 for (int nb = 0; nb < NB; ++nb)
-                                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[cb][nb][gi], acc[mb][nb], 0, 0, 0);
                             }
                 } else {
-                    // Block gi accumulates in units of its own D: the accumulator
-                    // moves from the previous block's units first.
-                    const bool zany = __builtin_amdgcn_ballot_w64(dzero) != 0u;
 #pragma unroll
                     for (int gi = 0; gi < 2; ++gi) {
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) {
-                            const uint32_t qq = gi ? qv[nb].z : qv[nb].x;
-                            const uint32_t* const P = lds_iq4nl_pairs();
-                            uint4 b = make_uint4(P[qq & 255u], P[(qq >> 8) & 255u], P[(qq >> 16) & 255u], P[qq >> 24]);
-                            if (zany) {
-                                const bool z = half_bits_to_float(gi ? dv[nb].y >> 16 : dv[nb].x & 0xffffu) == 0.f;
-                                if (z) b = make_uint4(0u, 0u, 0u, 0u);
-                            }
-                            fb[nb][gi] = __builtin_bit_cast(half8, b);
-                        }
-#pragma unroll
-                        for (int nb = 0; nb < NB; ++nb) {
-                            const float f1 = dlast[nb] * __builtin_amdgcn_rcpf(dg[nb][gi]);
-                            dlast[nb] = dg[nb][gi];
+                            const float f1 = dlast[nb] * __builtin_amdgcn_rcpf(dgs[cb][nb][gi]);
+                            dlast[nb] = dgs[cb][nb][gi];
 #pragma unroll
                             for (int mb = 0; mb < MBE; ++mb)
 #pragma unroll
@@ -1657,30 +1661,28 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                                 const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
 #pragma unroll
                                 for (int nb = 0; nb < NB; ++nb)
-                                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[nb][gi], acc[mb][nb], 0, 0, 0);
+                                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[cb][nb][gi], acc[mb][nb], 0, 0, 0);
                             }
                     }
                 }
+                if (NFB == 1u && more) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[0], dgs[0]);
                 if constexpr (Q4K) {
                     if (sq == 3) {
-                        // Mins of the superblock and the move to the next superblock's units.
                         half8 fm[NB];
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) {
-                            const uint4 v = kq < 2 ? make_uint4(bytes01(mn[nb][0]), bytes23(mn[nb][0]),
-                                                                bytes01(mn[nb][1]), bytes23(mn[nb][1]))
+                            const uint4 v = kq < 2 ? make_uint4(bytes01(cur.mn[nb][0]), bytes23(cur.mn[nb][0]),
+                                                                bytes01(cur.mn[nb][1]), bytes23(cur.mn[nb][1]))
                                                    : make_uint4(0, 0, 0, 0);
                             fm[nb] = __builtin_bit_cast(half8, v);
                         }
                         float f1[NB], f2[NB];
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) {
-                            const float rn = sb + 1 < sbs ? __builtin_amdgcn_rcpf(unit(dbits(nb, sb + 1))) : 1.f;
-                            f1[nb] = dsc[nb] * rn;
-                            f2[nb] = -dmn[nb] * rn;
+                            const float rn = more ? __builtin_amdgcn_rcpf(nxt.dsc[nb]) : 1.f;
+                            f1[nb] = cur.dsc[nb] * rn;
+                            f2[nb] = -cur.dmn[nb] * rn;
                         }
-                        // Four independent MFMAs per row block before their results are
-                        // used, so the updates do not wait on each MFMA in turn.
 #pragma unroll
                         for (int mb = 0; mb < MBE; ++mb) {
                             const half8 sa =
@@ -1696,22 +1698,34 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                                 for (int j = 0; j < 4; ++j)
                                     acc[mb][nb][j] = acc[mb][nb][j] * f1[nb] + mc[nb][j] * f2[nb];
                         }
+                        cur = nxt;
+                        // S of the next superblock into the other buffer (last read
+                        // at the previous superblock's end, two barriers ago).
+                        if (more) store_s(Ss[(sb + 1u) & 1u]);
                     }
                 } else if constexpr (IQ3) {
                     if (sq == 3) {
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) {
-                            const float f1 =
-                                dsc[nb] * (sb + 1 < sbs ? __builtin_amdgcn_rcpf(unit(dbits(nb, sb + 1))) : 1.f);
+                            const float f1 = cur.dsc[nb] * (more ? __builtin_amdgcn_rcpf(nxt.dsc[nb]) : 1.f);
 #pragma unroll
                             for (int mb = 0; mb < MBE; ++mb)
 #pragma unroll
                                 for (int j = 0; j < 4; ++j) acc[mb][nb][j] *= f1;
                         }
+                        cur = nxt;
                     }
                 }
+                // This wave's A(s + 1) has landed (the loads issued after it may
+                // stay in flight) before the barrier that publishes it; the slab's
+                // MFMAs stay on this side of it.
+                __builtin_amdgcn_sched_barrier(0);
+                if (sq == 0 && !IQ4) wait_vmcnt<B_PER_SLAB + B_PER_SB>();
+                else wait_vmcnt<B_PER_SLAB>();
             }
         }
+        // No A DMA may still be writing LDS when the block exits.
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         if constexpr (IQ4) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
@@ -1734,8 +1748,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                     split_f16(v1, h1, l1);
                     if (m < n) {
                         if (AORD == A_IQ4NL) {
-                            // columns c0 = ln and c1 = 16 + ln of the wave's 32-column group
-                            // go to 8 (ln / 4) + 2 (ln % 4) + {0, 1}: one 4-byte store each.
                             const uint64_t o = q * ldo + row0 + 32u * wave + 8u * (ln >> 2) + 2u * (ln & 3u);
                             *reinterpret_cast<uint32_t*>(out_h + o) = pack_h2(h0, h1);
                             *reinterpret_cast<uint32_t*>(out_l + o) = pack_h2(l0, l1);
@@ -1749,7 +1761,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                         }
                     }
                     if (out_gs != nullptr) {
-                        // 32-column sum of act over this wave's columns (16 lanes x 2).
                         float gsum = v0 + v1;
                         gsum += dpp_mov<0xb1>(gsum);
                         gsum += dpp_mov<0x4e>(gsum);
@@ -1771,8 +1782,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         case 3: run(std::integral_constant<int, 3>{}); break;
         default: run(std::integral_constant<int, 4>{}); break;
     }
-#undef INGOT_LOAD_A
-#undef INGOT_LOAD_A1
 #undef INGOT_LOAD_S
 }
 
