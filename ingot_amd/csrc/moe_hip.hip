@@ -235,7 +235,7 @@ struct DownArgs {
     uint32_t H, F, SF;
     const float *act, *sact;
     const uint32_t* ids;
-    const float *wts, *sgl;
+    const float* sgl;
     uint32_t K;
     const float* res;
     float* out;
@@ -340,24 +340,36 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
 
 }  // namespace
 
-// Decode gate/up after router routing (k_dec_gate_up2): 2 rows x every pair per 8-wave block.
-constexpr int GU_RPW = 2;
-constexpr int DEC_RPW = 2;  // down rows per wave
+// Decode gate/up (k_dec_gate_up2): 2 or 3 rows x every pair per 8-wave block.
+constexpr int DEC_RPW = 1;  // down rows per wave
 
 template <int KIND>
-static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, dim3 grid, const uint8_t* g, const uint8_t* u,
-                            uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x, const float* logits,
-                            const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale, float limit,
-                            uint32_t* ids, float* w, uint32_t* flags, float* act) {
-#define DGU(C, N)                                                                                                 \
-    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, GU_RPW, N>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x,        \
-                       logits, bias, E, K, mode, scale, limit, ids, w, flags, act)
-    if (cpl == 1 && np == 1) { DGU(1, 1); return true; }
-    if (cpl == 1 && np == 2) { DGU(1, 2); return true; }
-    if (cpl == 2 && np == 1) { DGU(2, 1); return true; }
-    if (cpl == 2 && np == 2) { DGU(2, 2); return true; }
+static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid, const uint8_t* g,
+                            const uint8_t* u, uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x,
+                            const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale,
+                            float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
+#define DGU(C, N, R)                                                                                              \
+    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x, logits,    \
+                       bias, E, K, mode, scale, limit, ids, w, flags, act)
+    if (rpw == 3) {
+        if (cpl == 1 && np == 1) { DGU(1, 1, 3); return true; }
+        return false;
+    }
+    if (cpl == 1 && np == 1) { DGU(1, 1, 2); return true; }
+    if (cpl == 1 && np == 2) { DGU(1, 2, 2); return true; }
+    if (cpl == 2 && np == 1) { DGU(2, 1, 2); return true; }
+    if (cpl == 2 && np == 2) { DGU(2, 2, 2); return true; }
 #undef DGU
     return false;
+}
+
+// Rows per wave: 3 when that spreads the blocks more evenly over the 256 CUs
+// (F = 768 at one token: 256 blocks of 3 rows instead of 384 of 2, half of
+// the CUs running two), else 2.
+static uint32_t dec_gate_up_rows(uint32_t F, uint32_t T, uint32_t cpl, uint32_t np) {
+    if (cpl != 1 || np != 1) return 2;
+    auto per_cu = [&](uint32_t r) { return ((F + r - 1) / r * T + 255) / 256 * r; };
+    return per_cu(3) < per_cu(2) ? 3 : 2;
 }
 
 static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const uint8_t* u, uint64_t gs,
@@ -365,9 +377,10 @@ static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, c
                                const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale, float limit,
                                uint32_t* ids, float* w, uint32_t* flags, float* act) {
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
-    dim3 grid((F + GU_RPW - 1) / GU_RPW, T);
+    const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
+    dim3 grid((F + rpw - 1) / rpw, T);
     switch (kind) {
-#define K_(KV) case KV: return dec_gate_up_cpl<KV>(s, cpl, np, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act);
+#define K_(KV) case KV: return dec_gate_up_cpl<KV>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act);
         K_(0) K_(2) K_(8) K_(12) K_(17) K_(18) K_(20)
 #undef K_
         default: return false;
@@ -378,11 +391,11 @@ template <int KD, int KS>
 static bool dec_down_vpl(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
 #define DD(V)                                                                                                      \
     case V:                                                                                                        \
-        hipLaunchKernelGGL((k_dec_down<KD, KS, V, DEC_RPW>), grid, dim3(256), 0, s, a.down, a.dstride, a.sdown,    \
-                           a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.wts, a.sgl, a.K, a.res, a.out);     \
+        hipLaunchKernelGGL((k_dec_down<KD, KS, V, DEC_RPW>), grid, dim3(DOWN_THREADS), 0, s, a.down, a.dstride,    \
+                           a.sdown, a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.sgl, a.K, a.res, a.out);   \
         return true;
     switch (vpl) {
-        DD(1) DD(2) DD(3) DD(4) DD(5) DD(6) DD(7) DD(8)
+        DD(1) DD(2) DD(3) DD(4) DD(5) DD(6)  // K F + SF <= DOWN_LDS_FLOATS: at most 384 chunks
         default: return false;
     }
 #undef DD
@@ -398,7 +411,7 @@ static bool can_fuse_shared(uint32_t kd, int ks) {
 static bool gemv_down(hipStream_t s, uint32_t kd, int ks, const DownArgs& a, uint32_t T) {
     const uint32_t nv = a.K * (a.F / 32) + (ks >= 0 ? a.SF / 32 : 0);
     const uint32_t vpl = (nv + 63) / 64;
-    dim3 grid((a.H + 4 * DEC_RPW - 1) / (4 * DEC_RPW), T);
+    dim3 grid((a.H + DOWN_WAVES * DEC_RPW - 1) / (DOWN_WAVES * DEC_RPW), T);
     if (ks < 0) {
         switch (kd) {
             case 0: return dec_down_vpl<0, -1>(s, vpl, grid, a);
@@ -972,7 +985,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
                                     limit, sact);
         };
         L->stage_name[ST_GATEUP] = "k_dec_gate_up2";
-        DownArgs a{down.d, sdown.d, down.stride, sdown.stride, H, F, SF, act, sact, ids, wts, sgl, K, res, d_out};
+        DownArgs a{down.d, sdown.d, down.stride, sdown.stride, H, F, SF, act, sact, ids, sgl, K, res, d_out};
         if (!hs || fuse_shared) {
             const int ks = hs ? ks_ : -1;
             L->stage[ST_DOWN] = [=](hipStream_t ss) { gemv_down(ss, down.kind, ks, a, T); };

@@ -3,12 +3,13 @@
 // Decode (few pairs) and prefill (many pairs) take different kernels:
 //   router   k_router        logits = W_r x (fixed fp32 order), optional fused
 //                            RMSNorm, optional shared-expert gate logit
-//   route    k_route         per-token top-K on 64-bit (orderable value, ~id)
-//                            keys; softmax or sigmoid+bias weights
-//   decode   k_dec_gate_up2  routing of the block's token (block_route), then
-//                            act[p] = SwiGLU(G_e x_t, U_e x_t), one wave per pair
+//   route    k_route         per-token top-K, one wave per token (wave_route);
+//                            softmax or sigmoid+bias weights
+//   decode   k_dec_gate_up2  routing of the block's token in every wave
+//                            (wave_route), then act[p] = w_k SwiGLU(G_e x_t, U_e x_t),
+//                            one wave per pair
 //            k_gemv_gate_up  the same for the shared expert (no routing)
-//            k_dec_down      out[t] = sum_k w_k D_e act[p] (+ shared, + residual)
+//            k_dec_down      out[t] = sum_k D_e act[p] (+ shared, + residual)
 //   prefill  k_dispatch      stable expert grouping, tile list (one block)
 //            k_gemm_f16      f16-MFMA grouped GEMM on integer weight operands
 //                            (Q4_K, IQ3_XXS, IQ4_NL), A split into f16 hi + lo
@@ -69,11 +70,6 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
-    return ((uint64_t)hi << 32) | lo;
-}
-
 __device__ __forceinline__ float swiglu(float g, float u, float limit) {
     if (limit > 0.f) {
         g = fminf(g, limit);
@@ -82,144 +78,118 @@ __device__ __forceinline__ float swiglu(float g, float u, float limit) {
     return g / (1.0f + expf(-g)) * u;
 }
 
-// ------------------------------------------------------ block-level routing
-// The same selection and weights as k_route for one token, computed by a
-// whole block without a serial chain: every candidate's rank is the number of
-// larger keys (keys are unique), so candidate i with rank r < K is the r-th
-// selection. LDS: keys [E] u64, vals [E] f32, sel_id/sel_v/w [K].
-struct RouteLds {
-    uint64_t* keys;
-    float* vals;
-    uint32_t* rank;
-    uint32_t* sel_id;
-    float* sel_v;
-    float* w;
-};
-
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t l) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), (int)l);
-    return ((uint64_t)hi << 32) | lo;
+// ------------------------------------------------------------ wave routing
+// Wave-wide maximum of a uint32: DPP quad xor 1 and xor 2, half-row and row
+// mirrors give every lane its 16-lane row maximum; the four row maxima are
+// read with readlane. The whole wave must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_max(uint32_t v) {
+    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = dpp_max<0xb1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max<0x4e>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max<0x141>(v);  // row_half_mirror
+    v = dpp_max<0x140>(v);  // row_mirror
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
 }
 
-// Selection for larger E (E <= 2 * blockDim.x, K <= 64, blockDim.x / 64 * K
-// <= 1024), from keys[0..E) (zero above E) and vals in LDS; writes
-// sel_id/sel_v[0..K). Each wave ranks its own keys (lane j holds keys j and
-// j + blockDim.x of its wave's range) against the wave's keys read by lane
-// broadcasts; a wave's keys of rank < K are candidates, and every global top-K
-// key is one (whatever beats it is also in the global top K). The candidates,
-// at most K per wave, are then ranked against each other: a candidate's rank
-// among them is its global rank when that rank is below K.
-__device__ inline void block_route_select_large(uint32_t E, uint32_t K, RouteLds s) {
-    const uint32_t tid = threadIdx.x, nt = blockDim.x, wave = tid >> 6, slots = (nt >> 6) * K;
-    const uint32_t e0 = tid, e1 = tid + nt;
-    const uint64_t k0 = e0 < E ? s.keys[e0] : 0ull, k1 = e1 < E ? s.keys[e1] : 0ull;
-    const float v0 = e0 < E ? s.vals[e0] : 0.f, v1 = e1 < E ? s.vals[e1] : 0.f;
-    uint32_t r0 = 0, r1 = 0;
-    const bool two = E > nt;
-#pragma unroll 8
-    for (uint32_t src = 0; src < 64u; ++src) {
-        const uint64_t a = readlane_u64(k0, src);
-        r0 += a > k0 ? 1u : 0u;
-        r1 += a > k1 ? 1u : 0u;
-        if (two) {
-            const uint64_t b = readlane_u64(k1, src);
-            r0 += b > k0 ? 1u : 0u;
-            r1 += b > k1 ? 1u : 0u;
-        }
-    }
-    __syncthreads();  // every thread holds its keys: the key array becomes the candidate slots
-    for (uint32_t i = tid; i < slots; i += nt) s.keys[i] = 0;
-    __syncthreads();
-    if (k0 != 0ull && r0 < K) {
-        s.keys[wave * K + r0] = k0;
-        s.vals[wave * K + r0] = v0;
-        s.rank[wave * K + r0] = e0;
-    }
-    if (k1 != 0ull && r1 < K) {
-        s.keys[wave * K + r1] = k1;
-        s.vals[wave * K + r1] = v1;
-        s.rank[wave * K + r1] = e1;
-    }
-    __syncthreads();
-    if (tid < slots) {
-        const uint64_t mine = s.keys[tid];
-        if (mine != 0ull) {
-            uint32_t c = 0;
-            for (uint32_t i = 0; i < slots; ++i) c += s.keys[i] > mine ? 1u : 0u;
-            if (c < K) {
-                s.sel_id[c] = s.rank[tid];
-                s.sel_v[c] = s.vals[tid];
-            }
-        }
-    }
-}
-
-__device__ inline void block_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
-                                   uint32_t sigmoid_mode, float scale, RouteLds s, uint32_t* __restrict__ flags) {
+// Top-K selection of one token by one wave, E <= 64 * NE, the whole wave
+// active (src/lib.rs:43-60, kernels/glm.metal:81-98). Candidate j of a lane is
+// expert e = lane + 64 j with selection key s = logit (+ bias) (softmax) or
+// sigmoid(logit) (+ bias) (sigmoid routing), and weight input wv = s
+// (softmax) or sigmoid(logit). Each of the K rounds takes the wave maximum of
+// the keys in IEEE total order (f32::total_cmp, as uint32 through
+// ingot_orderable), the lowest id holding it (ballots, ids ascending with j
+// and lane), and retires that candidate: higher keys first, equal keys toward
+// the lower id. Lane k < K ends with selection k's id and weight input.
+// Returns whether this lane saw a non-finite logit or bias.
+template <int NE>
+__device__ inline bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
+                                  uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
     INGOT_NO_CONTRACT
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t key[NE];
+    float wv[NE];
+    uint32_t live = 0;  // bit j: candidate j exists and is not selected yet
     bool bad = false;
-    for (uint32_t e = tid; e < E; e += nt) {
-        float v = l[e];
-        float b = bias ? bias[e] : 0.f;
-        bad |= !isfinite(v) || !isfinite(b);
-        float key_v, wv;
-        if (sigmoid_mode) {
-            wv = ingot_det_sigmoid(v);
-            key_v = bias ? wv + b : wv;
-        } else {
-            key_v = bias ? v + b : v;
-            wv = key_v;
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const uint32_t e = lane + 64u * j;
+        key[j] = 0;
+        wv[j] = 0.f;
+        if (e < E) {
+            const float v = l[e];
+            const float b = bias ? bias[e] : 0.f;
+            bad |= !isfinite(v) || !isfinite(b);
+            float sk;
+            if (sigmoid_mode) {
+                wv[j] = ingot_det_sigmoid(v);
+                sk = bias ? wv[j] + b : wv[j];
+            } else {
+                sk = bias ? v + b : v;
+                wv[j] = sk;
+            }
+            key[j] = ingot_orderable(sk);
+            live |= 1u << j;
         }
-        s.keys[e] = ingot_select_key(key_v, e);
-        s.vals[e] = wv;
-        s.rank[e] = 0;
     }
-    const uint32_t E16 = (E + 15u) & ~15u;
-    for (uint32_t e = E + tid; e < E16; e += nt) s.keys[e] = 0;  // below every real key
-    if (flags && __any(bad) && (tid & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
-    __syncthreads();
-    if (E > 128u) {
-        block_route_select_large(E, K, s);
-    } else {
-        // rank[e] = number of keys above key e (keys are distinct), counted over
-        // (expert, 16-key group) items spread across the block; consecutive
-        // threads share a group, so its keys are LDS broadcasts.
-        const uint32_t G = E16 / 16u;
-        for (uint32_t item = tid; item < E * G; item += nt) {
-            const uint32_t g = item / E, e = item - g * E;
-            const uint64_t mine = s.keys[e];
-            ulonglong2 kv[8];
+    my_id = 0;
+    my_v = 0.f;
+    for (uint32_t k = 0; k < K; ++k) {
+        uint32_t m = 0;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) kv[q] = *reinterpret_cast<const ulonglong2*>(&s.keys[16u * g + 2 * q]);
-            uint32_t c = 0;
+        for (int j = 0; j < NE; ++j) m = max(m, (live >> j) & 1u ? key[j] : 0u);
+        m = wave_max_u32(m);
+        // K <= E, so some live candidate holds m (live keys are >= 0 = a retired one).
+        uint32_t id = 0;
+        bool found = false;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) c += (kv[q].x > mine ? 1u : 0u) + (kv[q].y > mine ? 1u : 0u);
-            if (c) atomicAdd(&s.rank[e], c);
-        }
-        __syncthreads();
-        for (uint32_t e = tid; e < E; e += nt) {
-            const uint32_t rank = s.rank[e];
-            if (rank < K) {
-                s.sel_id[rank] = e;
-                s.sel_v[rank] = s.vals[e];
+        for (int j = 0; j < NE; ++j) {
+            const uint64_t bj = __ballot(((live >> j) & 1u) && key[j] == m);
+            if (!found && bj) {
+                id = 64u * j + (uint32_t)__builtin_ctzll(bj);
+                found = true;
             }
         }
+        const uint32_t owner = id & 63u, slot = id >> 6;
+        float mine = wv[0];
+#pragma unroll
+        for (int j = 1; j < NE; ++j)
+            if ((uint32_t)j == slot) mine = wv[j];
+        if (lane == owner) live &= ~(1u << slot);
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)owner));
+        if (lane == k) {
+            my_id = id;
+            my_v = v;
+        }
     }
-    __syncthreads();
-    float num = 0.f, total = 0.f;
-    if (tid < K) {
-        const float top = s.sel_v[0];
-        num = sigmoid_mode ? s.sel_v[tid] : ingot_det_expf(s.sel_v[tid] - top);
-        s.w[tid] = num;
-    }
-    __syncthreads();
-    if (tid < K)
-        for (uint32_t k = 0; k < K; ++k) total += s.w[k];  // selection order, as the CPU sums
-    __syncthreads();  // every numerator read before any weight is written
-    if (tid < K) s.w[tid] = sigmoid_mode ? num / total * scale : num / total;
-    __syncthreads();
+    return bad;
+}
+
+// Routing weight of selection k held by lane k < K (wave_route's my_v):
+// softmax over the K selected logits, max-subtracted, summed in selection
+// order (src/lib.rs:53-58); sigmoid routing: score / sum of the selected
+// scores * scale (kernels/glm.metal:93-97).
+__device__ inline float wave_route_weight(float my_v, uint32_t K, uint32_t sigmoid_mode, float scale) {
+    INGOT_NO_CONTRACT
+    const float top = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), 0));
+    const float num = sigmoid_mode ? my_v : ingot_det_expf(my_v - top);
+    float total = 0.f;
+    for (uint32_t k = 0; k < K; ++k) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), (int)k));
+    return sigmoid_mode ? num / total * scale : num / total;
+}
+
+// wave_route for any E <= 1024 (the runtime E picks the candidates per lane).
+__device__ inline bool wave_route_any(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E,
+                                      uint32_t K, uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
+    if (E <= 64u) return wave_route<1>(l, bias, E, K, sigmoid_mode, my_id, my_v);
+    if (E <= 128u) return wave_route<2>(l, bias, E, K, sigmoid_mode, my_id, my_v);
+    if (E <= 256u) return wave_route<4>(l, bias, E, K, sigmoid_mode, my_id, my_v);
+    if (E <= 512u) return wave_route<8>(l, bias, E, K, sigmoid_mode, my_id, my_v);
+    return wave_route<16>(l, bias, E, K, sigmoid_mode, my_id, my_v);
 }
 
 // ---------------------------------------------------------------- router
@@ -465,93 +435,58 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
 }
 
 // ----------------------------------------------------------------- route
-// One wave per token, E <= 64 * NE. Softmax mode (src/lib.rs:43-60):
-// selection and weights on l (+ bias when given), w_k = exp(v_k - v_top) /
-// sum. Sigmoid mode (kernels/glm.metal:81-98): selection on sigmoid(l) + bias,
-// w_k = sigmoid(l_k) / sum * scale. Keys (orderable(v) << 32 | ~id) make the
-// wave maximum unique and resolve ties toward the lower id, exactly as a
-// stable descending sort with f32::total_cmp does (+0 above -0). Everything
-// stays in registers: the winner's weight input is fetched from its owning
-// lane, lane k keeps the k-th selection, and lane 0 sums the weights in
-// selection order. A non-finite logit or bias raises FLAG_NONFINITE; the ids
-// written are still valid expert indices. K <= 64.
+// One wave per token (wave_route, wave_route_weight), E <= 64 * NE. Softmax
+// mode (src/lib.rs:43-60): selection and weights on l (+ bias when given),
+// w_k = exp(v_k - v_top) / sum. Sigmoid mode (kernels/glm.metal:81-98):
+// selection on sigmoid(l) + bias, w_k = sigmoid(l_k) / sum * scale. A
+// non-finite logit or bias raises FLAG_NONFINITE; the ids written are still
+// valid expert indices. K <= 64.
 template <int NE>
 __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, const float* __restrict__ bias,
                                                uint32_t T, uint32_t E, uint32_t K, uint32_t sigmoid_mode,
                                                float scale, uint32_t* __restrict__ ids, float* __restrict__ wts,
                                                uint32_t* __restrict__ flags) {
-    INGOT_NO_CONTRACT
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (t >= T) return;
-    const float* l = logits + (uint64_t)t * E;
-    uint64_t key[NE];
-    float wv[NE];  // weight input of each candidate: l + bias (softmax) or sigmoid(l)
-    bool bad = false;
-#pragma unroll
-    for (int j = 0; j < NE; ++j) {
-        uint32_t e = lane + 64u * j;
-        key[j] = 0;
-        wv[j] = 0.f;
-        if (e < E) {
-            float v = l[e];
-            float b = bias ? bias[e] : 0.f;
-            bad |= !isfinite(v) || !isfinite(b);
-            float s;
-            if (sigmoid_mode) {
-                wv[j] = ingot_det_sigmoid(v);
-                s = bias ? wv[j] + b : wv[j];
-            } else {
-                s = bias ? v + b : v;
-                wv[j] = s;
-            }
-            key[j] = ingot_select_key(s, e);
-        }
-    }
+    if (t >= T) return;  // whole waves
+    uint32_t my_id;
+    float my_v;
+    const bool bad = wave_route<NE>(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, my_id, my_v);
     if (__any(bad) && lane == 0) atomicOr(flags, FLAG_NONFINITE);
-    uint32_t my_id = 0;
-    float my_v = 0.f;
-    for (uint32_t k = 0; k < K; ++k) {
-        uint64_t best = 0;
-#pragma unroll
-        for (int j = 0; j < NE; ++j) best = key[j] > best ? key[j] : best;
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            uint64_t o = shfl_xor_u64(best, m);
-            best = o > best ? o : best;
-        }
-        const uint32_t id = 0xffffffffu - (uint32_t)best;
-        const uint32_t owner = id & 63u, slot = id >> 6;
-        float mine = 0.f;
-#pragma unroll
-        for (int j = 0; j < NE; ++j)
-            if ((uint32_t)j == slot) {
-                mine = wv[j];
-                if (lane == owner) key[j] = 0;
-            }
-        const float v = __shfl(mine, (int)owner);
-        if (lane == k) {
-            my_id = id;
-            my_v = v;
-        }
-    }
-    // lane k < K: weight numerator of selection k
-    const float top = __shfl(my_v, 0);
-    const float num = sigmoid_mode ? my_v : ingot_det_expf(my_v - top);
-    float total = 0.f;
-    for (uint32_t k = 0; k < K; ++k) total += __shfl(num, (int)k);
+    const float w = wave_route_weight(my_v, K, sigmoid_mode, scale);
     if (lane < K) {
         ids[(uint64_t)t * K + lane] = my_id;
-        wts[(uint64_t)t * K + lane] = sigmoid_mode ? num / total * scale : num / total;
+        wts[(uint64_t)t * K + lane] = w;
+    }
+}
+
+// ------------------------------------------- decode: interleaved staging
+// The decode kernels stage 32-value chunks in LDS interleaved by lane: float4
+// i (values 4i..4i+3 in the format's chunk order, xv[q] = x[col(c, q)]) of
+// chunk c = l + 64 j sits at float4 slot (8 j + i) * 64 + l, so each of the
+// eight ds_read_b128 that fetch a wave's chunk j reads 64 consecutive float4
+// (no bank conflicts; the formats' natural column order puts eight lanes of a
+// read on the same banks).
+__device__ __forceinline__ uint32_t ilv_slot(uint32_t c, uint32_t i) { return ((c >> 6) * 8u + i) * 64u + (c & 63u); }
+__device__ __forceinline__ void load_x_ilv(const float4* __restrict__ s, uint32_t j, uint32_t lane, float* xv) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 a = s[(8u * j + i) * 64u + lane];
+        xv[4 * i] = a.x;
+        xv[4 * i + 1] = a.y;
+        xv[4 * i + 2] = a.z;
+        xv[4 * i + 3] = a.w;
     }
 }
 
 // ---------------------------------------------- decode: routed gate/up
-// grid (ceil(F / RPW), T), 512 threads (8 waves). The block routes its token
-// (block_route; block 0 of each token writes ids/weights for the down kernel)
-// while it stages the token's input in LDS. Wave w then computes rows
-// [RPW*bx, +RPW) of the gate and up projections of pairs k = w, w+8, ...;
-// each lane keeps its input chunks in registers.
+// grid (ceil(F / RPW), T), 512 threads (8 waves). Every wave routes the
+// block's token itself (wave_route: no barrier, nothing shared), so each wave
+// issues its weight loads as soon as its own selection is done; wave 0 of
+// block 0 writes the token's ids and weights for the down kernel. Wave w
+// computes rows [RPW*bx, +RPW) of the gate and up projections of pairs
+// k = w, w+8, ... and stores w_k * SwiGLU(g, u) (the routing weight folded
+// in for the down kernel); each lane keeps its input chunks in registers.
 constexpr uint32_t GU_WAVES = 8;
 
 template <int KIND, int CPL, int RPW, int NP>
@@ -563,37 +498,36 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                                                       uint32_t* __restrict__ ids, float* __restrict__ wts,
                                                       uint32_t* __restrict__ flags, float* __restrict__ act) {
     using Fm = Fmt<KIND>;
-    __shared__ float s_x[4096];
-    __shared__ uint64_t s_keys[1024];
-    __shared__ float s_vals[1024];
-    __shared__ uint32_t s_rank[1024];
-    __shared__ uint32_t s_id[64];
-    __shared__ float s_v[64], s_w[64];
+    __shared__ float4 s_x4[1024];  // interleaved chunks (ilv_slot), H <= 4096
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
     const uint32_t nch = H / 32u;
     const uint32_t r0 = blockIdx.x * RPW;
-    // The token's input (H <= 4096: at most two float4 per thread) is loaded
-    // into registers now and written to LDS after the weight loads are issued,
-    // so its latency overlaps the routing's logit loads.
-    const float4* x4 = reinterpret_cast<const float4*>(x + (uint64_t)t * H);
-    const uint32_t xi0 = threadIdx.x, xi1 = threadIdx.x + 512u;
-    const float4 xa = xi0 < H / 4u ? x4[xi0] : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4 xb = xi1 < H / 4u ? x4[xi1] : make_float4(0.f, 0.f, 0.f, 0.f);
-    stage_codebooks<KIND>();  // decoded only after block_route's barriers
-    block_route(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, scale, RouteLds{s_keys, s_vals, s_rank, s_id, s_v, s_w},
-                blockIdx.x == 0 ? flags : nullptr);
-    if (blockIdx.x == 0 && threadIdx.x < K) {
-        ids[(uint64_t)t * K + threadIdx.x] = s_id[threadIdx.x];
-        wts[(uint64_t)t * K + threadIdx.x] = s_w[threadIdx.x];
+    // The token's input, two interleaved float4 slots per thread (slot u: lane
+    // u % 64, chunk l + 64 (u / 512), float4 (u / 64) % 8), is loaded into
+    // registers now and written to LDS after the weight loads are issued, so
+    // its latency overlaps the routing's logit loads.
+    const float* xt = x + (uint64_t)t * H;
+    float4 xa[2];
+    bool xok[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const uint32_t u = threadIdx.x + 512u * m, ji = u >> 6, c = (u & 63u) + 64u * (ji >> 3);
+        xok[m] = (ji >> 3) < (uint32_t)CPL && c < nch;
+        xa[m] = xok[m] ? *reinterpret_cast<const float4*>(xt + Fm::col(c, 4u * (ji & 7u)))
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    stage_codebooks<KIND>();  // decoded only after the barrier that publishes s_x4
+    uint32_t my_id;
+    float my_v;
+    const bool bad = wave_route_any(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, my_id, my_v);
     // Weight loads of the wave's pairs k = wave + 8n (n < NP; K <= 8 NP);
     // a pair beyond K re-reads pair 0's rows and is not stored.
     typename Fm::Raw rg[NP][RPW][CPL], ru[NP][RPW][CPL];
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
         const uint32_t k = wave + GU_WAVES * n;
-        const uint32_t e = s_id[k < K ? k : 0u];
+        const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)(k < K ? k : 0u));
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const uint32_t r = min(r0 + i, F - 1);
@@ -607,14 +541,30 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
         }
     }
-    if (xi0 < H / 4u) reinterpret_cast<float4*>(s_x)[xi0] = xa;
-    if (xi1 < H / 4u) reinterpret_cast<float4*>(s_x)[xi1] = xb;
+    // Routing weights (after the loads are in flight): block 0's wave 0
+    // publishes the token's ids and weights for the down kernel.
+    const float w = wave_route_weight(my_v, K, sigmoid_mode, scale);
+    if (blockIdx.x == 0 && wave == 0) {
+        if (flags && __any(bad) && lane == 0) atomicOr(flags, FLAG_NONFINITE);
+        if (lane < K) {
+            ids[(uint64_t)t * K + lane] = my_id;
+            wts[(uint64_t)t * K + lane] = w;
+        }
+    }
+    float wk[NP];  // routing weight of each of the wave's pairs: act is stored as w_k * SwiGLU
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const uint32_t k = wave + GU_WAVES * n;
+        wk[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)(k < K ? k : 0u)));
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+        if (xok[m]) s_x4[threadIdx.x + 512u * m] = xa[m];
     __syncthreads();
     float xv[CPL][32], xs0[CPL], xs1[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const uint32_t c = min(lane + 64u * j, nch - 1);
-        Fm::load_x(s_x, c, xv[j]);
+        load_x_ilv(s_x4, j, lane, xv[j]);
         xs0[j] = xs1[j] = 0.f;
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
@@ -640,66 +590,94 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
-            if (k < K && lane == (uint32_t)i && r0 + i < F) act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit);
+            if (k < K && lane == (uint32_t)i && r0 + i < F)
+                act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit) * wk[n];
         }
     }
 }
 
 // ------------------------------------------------ decode: down + combine
-// grid (ceil(H / (4*RPW)), T), 256 threads. The token's K activations (and
-// the shared expert's) are staged in LDS once per block; each wave owns RPW
-// output rows. The K pairs' chunks (plus the shared expert's) form one
-// virtual row spread over the lanes (VPL chunks per lane), with each pair's
-// routing weight folded into its activations, so the wave sum is
-// sum_k w_k (D_e act_k)[i] (+ gate * (S_down sact)[i]) directly.
-constexpr uint32_t DOWN_LDS_FLOATS = 12288;  // 48 KB of staged activations
+// grid (ceil(H / (DOWN_WAVES * RPW)), T), DOWN_THREADS threads. The K pairs'
+// chunks (plus the shared expert's) form one virtual row spread over the
+// lanes (chunk v = l + 64 j, j < VPL); each wave owns RPW output rows, so the
+// wave sum is sum_k w_k (D_e act_k)[i] (+ gate * (S_down sact)[i]) directly.
+// The routed activations arrive already scaled by their pair's routing
+// weight (the gate/up kernel stores w_k * act). Each thread loads its share
+// of the virtual row's activations at kernel start, after the chunk ids and
+// before the weights, so the loads complete in that order; the shared
+// expert's values are scaled by its gate, and the block stages them in LDS
+// interleaved (ilv_slot) with the two 16-value sums of every chunk.
+constexpr uint32_t DOWN_WAVES = 8;
+constexpr uint32_t DOWN_THREADS = 64 * DOWN_WAVES;
+constexpr uint32_t DOWN_LDS_FLOATS = 12288;                        // 48 KB of staged activations
+constexpr uint32_t DOWN_ACT4 = DOWN_LDS_FLOATS / 4 / DOWN_THREADS;  // float4 loads per thread
 
 template <int KD, int KS, int VPL, int RPW>
-__global__ __launch_bounds__(256) void k_dec_down(const uint8_t* __restrict__ down, uint64_t dstride,
-                                                  const uint8_t* __restrict__ sdown, uint64_t sdstride, uint32_t H,
-                                                  uint32_t F, uint32_t SF, const float* __restrict__ act,
-                                                  const float* __restrict__ sact, const uint32_t* __restrict__ ids,
-                                                  const float* __restrict__ wts, const float* __restrict__ sgl,
-                                                  uint32_t K, const float* __restrict__ res, float* __restrict__ out) {
+__global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __restrict__ down, uint64_t dstride,
+                                                           const uint8_t* __restrict__ sdown, uint64_t sdstride,
+                                                           uint32_t H, uint32_t F, uint32_t SF,
+                                                           const float* __restrict__ act, const float* __restrict__ sact,
+                                                           const uint32_t* __restrict__ ids,
+                                                           const float* __restrict__ sgl, uint32_t K,
+                                                           const float* __restrict__ res, float* __restrict__ out) {
     using Fd = Fmt<KD>;
     using Fs = Fmt<(KS < 0 ? KD : KS)>;
-    __shared__ float s_act[DOWN_LDS_FLOATS];
+    __shared__ float4 s_act4[DOWN_LDS_FLOATS / 4];
+    __shared__ float s_sum[DOWN_LDS_FLOATS / 16];
     // Codebooks: decoded only after the barrier that follows the activation staging.
     stage_codebooks<KD>();
     if constexpr (KS >= 0) stage_codebooks<(KS < 0 ? KD : KS)>();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const uint32_t t = blockIdx.y;
     const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
-    const uint32_t nv = K * nchF + nchS;
-    const uint32_t r0 = (blockIdx.x * 4u + wave) * RPW;
-    // 1. this lane's chunks of the virtual row: expert row base, chunk, weight
+    const uint32_t nv = K * nchF + nchS, KF = K * F;
+    const uint32_t r0 = (blockIdx.x * DOWN_WAVES + wave) * RPW;
+    // 1. expert ids of this lane's chunks of the virtual row (chunk v: pair
+    //    v / nchF; the quotient by multiply-high, exact for v < 2^32 / nchF)
+    const uint32_t mag = 0xffffffffu / nchF + 1u;
+    uint32_t eid[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const uint32_t v = lane + 64u * j;
+        eid[j] = v < K * nchF ? ids[(uint64_t)t * K + __umulhi(v, mag)] : 0u;
+    }
+    // 2. this thread's activations: slot u = tid + DOWN_THREADS m is float4
+    //    u % 8 of chunk u / 8 (a chunk's two 16-value groups in two lane quads)
+    float4 av[DOWN_ACT4];
+    const float* at = act + (uint64_t)t * KF;
+    const float* st = sact + (uint64_t)t * SF;
+#pragma unroll
+    for (int m = 0; m < (int)DOWN_ACT4; ++m) {
+        const uint32_t u = tid + DOWN_THREADS * m, v = u >> 3, i4 = 4u * (u & 7u);
+        av[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (v < K * nchF) {
+            const uint32_t k = __umulhi(v, mag);
+            av[m] = *reinterpret_cast<const float4*>(at + k * F + Fd::col(v - k * nchF, i4));
+        } else if (KS >= 0 && v < nv) {
+            av[m] = *reinterpret_cast<const float4*>(st + Fs::col(v - K * nchF, i4));
+        }
+    }
+    const float sgv = (KS >= 0 && sgl) ? sgl[t] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. weight loads for all RPW rows
     const uint8_t* base[VPL];
-    uint32_t cc[VPL], aoff[VPL];
-    float w[VPL];
+    uint32_t cc[VPL];
     bool isS[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const uint32_t v = lane + 64u * j;
         base[j] = nullptr;
         cc[j] = 0;
-        aoff[j] = 0;
-        w[j] = 0.f;
         isS[j] = false;
         if (v < K * nchF) {
-            const uint32_t k = v / nchF, p = t * K + k;
-            base[j] = down + (uint64_t)ids[p] * H * dstride;
-            cc[j] = v % nchF;
-            aoff[j] = k * F;
-            w[j] = wts[p];
+            base[j] = down + (uint64_t)eid[j] * H * dstride;
+            cc[j] = v - __umulhi(v, mag) * nchF;
         } else if (v < nv) {
             base[j] = sdown;
             cc[j] = v - K * nchF;
-            aoff[j] = K * F;
             isS[j] = true;
-            w[j] = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
         }
     }
-    // 2. weight loads for all RPW rows, issued before the activations arrive
     typename Fd::Raw rd[RPW][VPL];
     typename Fs::Raw rs[KS >= 0 ? RPW : 1][KS >= 0 ? VPL : 1];
 #pragma unroll
@@ -712,34 +690,38 @@ __global__ __launch_bounds__(256) void k_dec_down(const uint8_t* __restrict__ do
             else rd[i][j] = Fd::load_raw(base[j] + (uint64_t)r * dstride, cc[j]);
         }
     }
-    // 3. stage the token's activations
-    {
-        const float4* a4 = reinterpret_cast<const float4*>(act + (uint64_t)t * K * F);
-        float4* d4 = reinterpret_cast<float4*>(s_act);
-        for (uint32_t i = tid; i < K * F / 4u; i += 256u) d4[i] = a4[i];
-        if (KS >= 0) {
-            const float4* s4 = reinterpret_cast<const float4*>(sact + (uint64_t)t * SF);
-            for (uint32_t i = tid; i < SF / 4u; i += 256u) d4[K * F / 4u + i] = s4[i];
+    __builtin_amdgcn_sched_barrier(0);
+    // 4. stage the activations (shared expert's times its gate) and each
+    //    chunk's two 16-value sums (xs0, xs1 of the formats' dot products)
+    const float gate = KS >= 0 ? (sgl ? ingot_det_sigmoid(sgv) : 1.0f) : 1.0f;
+#pragma unroll
+    for (int m = 0; m < (int)DOWN_ACT4; ++m) {
+        const uint32_t u = tid + DOWN_THREADS * m, v = u >> 3;
+        float4 a = av[m];
+        if (KS >= 0 && v >= K * nchF) {
+            a.x *= gate;
+            a.y *= gate;
+            a.z *= gate;
+            a.w *= gate;
         }
+        if (v < nv) s_act4[ilv_slot(v, u & 7u)] = a;
+        float g = (a.x + a.y) + (a.z + a.w);
+        g = dpp_add<0xb1>(g);  // quad_perm [1,0,3,2]
+        g = dpp_add<0x4e>(g);  // quad_perm [2,3,0,1]
+        if ((u & 3u) == 0 && v < nv) s_sum[2u * v + ((u >> 2) & 1u)] = g;
     }
     __syncthreads();
-    // 4. weighted activations of each chunk into registers, then the dot products
+    // 5. the dot products
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         if (!base[j]) continue;
-        float xv[32], xs0 = 0.f, xs1 = 0.f;
-        if (KS >= 0 && isS[j]) Fs::load_x(s_act + aoff[j], cc[j], xv);
-        else Fd::load_x(s_act + aoff[j], cc[j], xv);
-#pragma unroll
-        for (int q = 0; q < 32; ++q) xv[q] *= w[j];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            xs0 += xv[q];
-            xs1 += xv[16 + q];
-        }
+        float xv[32];
+        load_x_ilv(s_act4, j, lane, xv);
+        const float2 xs = reinterpret_cast<const float2*>(s_sum)[lane + 64u * j];
+        const float xs0 = xs.x, xs1 = xs.y;
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             if (KS >= 0 && isS[j]) acc[i] += Fs::dot_raw(rs[KS >= 0 ? i : 0][KS >= 0 ? j : 0], cc[j], xv, xs0, xs1);
