@@ -79,33 +79,40 @@ __device__ __forceinline__ float swiglu(float g, float u, float limit) {
 }
 
 // ------------------------------------------------------------ wave routing
-// Wave-wide maximum of a uint32: DPP quad xor 1 and xor 2, half-row and row
-// mirrors give every lane its 16-lane row maximum; the four row maxima are
-// read with readlane. The whole wave must be active.
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_max(uint32_t v) {
-    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false));
+// Orders one wave's LDS accesses around a point (lanes exchange data through
+// LDS; a wave's LDS instructions execute in issue order).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = dpp_max<0xb1>(v);   // quad_perm [1,0,3,2]
-    v = dpp_max<0x4e>(v);   // quad_perm [2,3,0,1]
-    v = dpp_max<0x141>(v);  // row_half_mirror
-    v = dpp_max<0x140>(v);  // row_mirror
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(a, b), max(c, d));
+
+// Per-wave LDS scratch of wave_route: K <= 64 candidates x (key, id, weight
+// input). Kernels that route use at most 8 waves per block.
+constexpr uint32_t ROUTE_MAX_WAVES = 8;
+__device__ inline uint32_t* route_lds() {
+    __shared__ __align__(16) uint32_t r[ROUTE_MAX_WAVES][3 * 64];
+    return r[threadIdx.x >> 6];
 }
 
 // Top-K selection of one token by one wave, E <= 64 * NE, the whole wave
 // active (src/lib.rs:43-60, kernels/glm.metal:81-98). Candidate j of a lane is
 // expert e = lane + 64 j with selection key s = logit (+ bias) (softmax) or
 // sigmoid(logit) (+ bias) (sigmoid routing), and weight input wv = s
-// (softmax) or sigmoid(logit). Each of the K rounds takes the wave maximum of
-// the keys in IEEE total order (f32::total_cmp, as uint32 through
-// ingot_orderable), the lowest id holding it (ballots, ids ascending with j
-// and lane), and retires that candidate: higher keys first, equal keys toward
-// the lower id. Lane k < K ends with selection k's id and weight input.
-// Returns whether this lane saw a non-finite logit or bias.
+// (softmax) or sigmoid(logit). Keys compare in IEEE total order
+// (f32::total_cmp, as uint32 through ingot_orderable); the selection is the K
+// highest keys, equal keys toward the lower id, in that order:
+//   1. a threshold T bit by bit from the top, keeping at least K keys >= T
+//      (ballot counts, no data movement); it stops as soon as exactly K keys
+//      are >= T, else ends at the K-th highest key;
+//   2. the selected set: the K keys >= T in the first case; keys above T,
+//      then keys equal to T by ascending id until there are K, in the second;
+//   3. the K candidates are compacted in id order into LDS, lane m < K takes
+//      candidate m, reads all K keys (LDS broadcast) and counts those that
+//      precede it (higher key, or equal key and lower id: an earlier
+//      position), and puts itself at that rank.
+// Lane k < K ends with selection k's id and weight input. Returns whether
+// this lane saw a non-finite logit or bias.
 template <int NE>
 __device__ inline bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
                                   uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
@@ -113,14 +120,15 @@ __device__ inline bool wave_route(const float* __restrict__ l, const float* __re
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t key[NE];
     float wv[NE];
-    uint32_t live = 0;  // bit j: candidate j exists and is not selected yet
+    bool ok[NE];
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < NE; ++j) {
         const uint32_t e = lane + 64u * j;
         key[j] = 0;
         wv[j] = 0.f;
-        if (e < E) {
+        ok[j] = e < E;
+        if (ok[j]) {
             const float v = l[e];
             const float b = bias ? bias[e] : 0.f;
             bad |= !isfinite(v) || !isfinite(b);
@@ -133,39 +141,83 @@ __device__ inline bool wave_route(const float* __restrict__ l, const float* __re
                 wv[j] = sk;
             }
             key[j] = ingot_orderable(sk);
-            live |= 1u << j;
         }
     }
-    my_id = 0;
-    my_v = 0.f;
-    for (uint32_t k = 0; k < K; ++k) {
-        uint32_t m = 0;
+    // 1. Keys of absent candidates are 0 and never counted for a threshold
+    //    above 0 (T stays 0 only when fewer than K keys are above 0).
+    uint32_t T = 0;
+    bool exact = false;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = T | (1u << bit);
+        uint32_t n = 0;
 #pragma unroll
-        for (int j = 0; j < NE; ++j) m = max(m, (live >> j) & 1u ? key[j] : 0u);
-        m = wave_max_u32(m);
-        // K <= E, so some live candidate holds m (live keys are >= 0 = a retired one).
-        uint32_t id = 0;
-        bool found = false;
-#pragma unroll
-        for (int j = 0; j < NE; ++j) {
-            const uint64_t bj = __ballot(((live >> j) & 1u) && key[j] == m);
-            if (!found && bj) {
-                id = 64u * j + (uint32_t)__builtin_ctzll(bj);
-                found = true;
+        for (int j = 0; j < NE; ++j) n += (uint32_t)__popcll(__ballot(key[j] >= c));
+        if (n >= K) {
+            T = c;
+            if (n == K) {
+                exact = true;
+                break;
             }
         }
-        const uint32_t owner = id & 63u, slot = id >> 6;
-        float mine = wv[0];
+    }
+    uint64_t sel[NE];
+    if (exact) {  // T > 0: absent candidates excluded
 #pragma unroll
-        for (int j = 1; j < NE; ++j)
-            if ((uint32_t)j == slot) mine = wv[j];
-        if (lane == owner) live &= ~(1u << slot);
-        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)owner));
-        if (lane == k) {
-            my_id = id;
-            my_v = v;
+        for (int j = 0; j < NE; ++j) sel[j] = __ballot(key[j] >= T);
+    } else {
+        // 2. K <= E: at least K - (keys above T) present candidates equal T.
+        uint32_t need = K;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            sel[j] = __ballot(ok[j] && key[j] > T);
+            need -= (uint32_t)__popcll(sel[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            uint64_t eq = __ballot(ok[j] && key[j] == T);
+            while (need != 0u && eq != 0ull) {
+                const uint64_t low = eq & (~eq + 1ull);
+                sel[j] |= low;
+                eq ^= low;
+                --need;
+            }
         }
     }
+    // 3. compaction in id order (slot j, then lane), ranking, placement
+    uint32_t* r = route_lds();
+    uint32_t before = 0;
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const uint32_t pos = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(sel[j] >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)sel[j], 0u));
+        if (((sel[j] >> lane) & 1ull) && pos < 64u) {
+            r[pos] = key[j];
+            r[64 + pos] = lane + 64u * j;
+            r[128 + pos] = __float_as_uint(wv[j]);
+        }
+        before += (uint32_t)__popcll(sel[j]);
+    }
+    wave_sync();
+    const bool cand = lane < K;
+    const uint32_t ck = cand ? r[lane] : 0u, cid = cand ? r[64 + lane] : 0u;
+    const float cv = cand ? __uint_as_float(r[128 + lane]) : 0.f;
+    uint32_t rank = 0;
+    for (uint32_t m = 0; m < K; m += 4) {
+        const uint4 k4 = *reinterpret_cast<const uint4*>(r + m);
+        const uint32_t km[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q)
+            rank += (m + q < K && (km[q] > ck || (km[q] == ck && m + q < lane))) ? 1u : 0u;
+    }
+    wave_sync();
+    if (cand) {
+        r[64 + rank] = cid;
+        r[128 + rank] = __float_as_uint(cv);
+    }
+    wave_sync();
+    my_id = cand ? min(r[64 + lane], E - 1u) : 0u;  // (always below E: a guard for the weight addresses)
+    my_v = cand ? __uint_as_float(r[128 + lane]) : 0.f;
+    wave_sync();  // the scratch is reused by the next call
     return bad;
 }
 
