@@ -44,6 +44,8 @@ __device__ __forceinline__ float flip_sign(float v, uint32_t bit) {
     return __int_as_float(__float_as_int(v) ^ (int)(bit << 31));
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 template <int KIND>
 struct Fmt;
 
@@ -69,22 +71,21 @@ struct Fmt<12> {
     }
     // Scale (sc) and min (m) of the chunk's two groups, from the 16-byte header
     // {d, dmin, scales[12]} (ggml get_scale_min_k4, kernels/iq3_mix.metal:13-15).
+    // Branch-free (lanes of a wave hold different quarters): both 6-bit
+    // unpackings are formed and selected, and the quarter's odd half moves
+    // its two bytes down.
     __device__ static void scales(uint4 hdr, uint32_t c, float& d0, float& m0, float& d1, float& m1) {
-        uint32_t qq = (c & 7u) >> 1;  // 64-column quarter: groups 2qq, 2qq+1
-        uint32_t scw, mw;
-        if (qq < 2) {
-            scw = hdr.y & 0x3f3f3f3fu;
-            mw = hdr.z & 0x3f3f3f3fu;
-        } else {
-            scw = (hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u);
-            mw = ((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u);
-        }
-        uint32_t g0 = (2u * qq) & 3u;
-        float d = half_bits_to_float(hdr.x), dm = half_bits_to_float(hdr.x >> 16);
-        d0 = d * ubyte_f(scw, g0);
-        d1 = d * ubyte_f(scw, g0 + 1);
-        m0 = dm * ubyte_f(mw, g0);
-        m1 = dm * ubyte_f(mw, g0 + 1);
+        const uint32_t qq = (c & 7u) >> 1;  // 64-column quarter: groups 2qq, 2qq+1
+        const uint32_t sc_lo = hdr.y & 0x3f3f3f3fu, mn_lo = hdr.z & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (hdr.w & 0x0f0f0f0fu) | ((hdr.y >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((hdr.w >> 4) & 0x0f0f0f0fu) | ((hdr.z >> 2) & 0x30303030u);
+        const uint32_t sh = 16u * (qq & 1u);
+        const uint32_t scw = (qq < 2u ? sc_lo : sc_hi) >> sh, mw = (qq < 2u ? mn_lo : mn_hi) >> sh;
+        const float d = half_bits_to_float(hdr.x), dm = half_bits_to_float(hdr.x >> 16);
+        d0 = d * ubyte_f(scw, 0);
+        d1 = d * ubyte_f(scw, 1);
+        m0 = dm * ubyte_f(mw, 0);
+        m1 = dm * ubyte_f(mw, 1);
     }
     // Raw bytes of a chunk for the GEMM staging path: {header, nibbles}.
     struct Raw {
@@ -98,21 +99,32 @@ struct Fmt<12> {
         r.b = *reinterpret_cast<const uint4*>(b + 16 + 32 * (q >> 1) + 16 * (q & 1u));
         return r;
     }
+    // A nibble byte (0..15) read as an OCP fp8 e4m3 value is exactly
+    // q * 2^-9 (subnormal m/8 * 2^-6 below 8, 2^-6 (1 + m/8) from 8), so one
+    // v_cvt_pk_f32_fp8 converts two nibbles; the sums carry 2^-9 and the
+    // scaled term is multiplied back by 2^9 (exact: powers of two commute
+    // with every rounding in the normal range, so the result is the
+    // q-weighted sum's).
     __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float xs0, float xs1) {
         float d0, m0, d1, m1;
         scales(r.a, c, d0, m0, d1, m1);
-        uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            uint32_t lo = w[k] & 0x0f0f0f0fu, hi = (w[k] >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                slo = __builtin_fmaf(ubyte_f(lo, j), xv[4 * k + j], slo);
-                shi = __builtin_fmaf(ubyte_f(hi, j), xv[16 + 4 * k + j], shi);
-            }
+            const uint32_t lo = w[k] & 0x0f0f0f0fu, hi = (w[k] >> 4) & 0x0f0f0f0fu;
+            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+            slo = __builtin_fmaf(l01.x, xv[4 * k], slo);
+            shi = __builtin_fmaf(h01.x, xv[16 + 4 * k], shi);
+            slo = __builtin_fmaf(l01.y, xv[4 * k + 1], slo);
+            shi = __builtin_fmaf(h01.y, xv[16 + 4 * k + 1], shi);
+            slo = __builtin_fmaf(l23.x, xv[4 * k + 2], slo);
+            shi = __builtin_fmaf(h23.x, xv[16 + 4 * k + 2], shi);
+            slo = __builtin_fmaf(l23.y, xv[4 * k + 3], slo);
+            shi = __builtin_fmaf(h23.y, xv[16 + 4 * k + 3], shi);
         }
-        return (d0 * slo + d1 * shi) - (m0 * xs0 + m1 * xs1);
+        return 512.0f * (d0 * slo + d1 * shi) - (m0 * xs0 + m1 * xs1);
     }
     __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float xs0, float xs1) {
         return dot_raw(load_raw(row, c), c, xv, xs0, xs1);

@@ -343,14 +343,14 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
 // Decode gate/up (k_dec_gate_up2): 2 or 3 rows x every pair per 8-wave block.
 constexpr int DEC_RPW = 1;  // down rows per wave
 
-template <int KIND>
+template <int KIND, int NE>
 static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid, const uint8_t* g,
                             const uint8_t* u, uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x,
                             const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale,
                             float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
 #define DGU(C, N, R)                                                                                              \
-    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x, logits,    \
-                       bias, E, K, mode, scale, limit, ids, w, flags, act)
+    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x,        \
+                       logits, bias, E, K, mode, scale, limit, ids, w, flags, act)
     if (rpw == 3) {
         if (cpl == 1 && np == 1) { DGU(1, 1, 3); return true; }
         return false;
@@ -361,6 +361,27 @@ static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t r
     if (cpl == 2 && np == 2) { DGU(2, 2, 2); return true; }
 #undef DGU
     return false;
+}
+
+// Candidates per lane of the routing (E <= 64 NE): 2 up to 128 experts, 8 for
+// the IQ2_XS 512-expert shape, 16 otherwise (one instantiation per count
+// keeps each kernel's code small).
+template <int KIND>
+static bool dec_gate_up_ne(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid, const uint8_t* g,
+                           const uint8_t* u, uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x,
+                           const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale,
+                           float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
+    if (E <= 128)
+        return dec_gate_up_cpl<KIND, 2>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale,
+                                        limit, ids, w, flags, act);
+    if constexpr (KIND == 17)
+        if (E <= 512 && cpl == 1 && np == 2 && rpw == 2) {
+            hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x, logits,
+                               bias, E, K, mode, scale, limit, ids, w, flags, act);
+            return true;
+        }
+    return dec_gate_up_cpl<KIND, 16>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale,
+                                     limit, ids, w, flags, act);
 }
 
 // Rows per wave: 3 when that spreads the blocks more evenly over the 256 CUs
@@ -380,7 +401,7 @@ static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, c
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     dim3 grid((F + rpw - 1) / rpw, T);
     switch (kind) {
-#define K_(KV) case KV: return dec_gate_up_cpl<KV>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act);
+#define K_(KV) case KV: return dec_gate_up_ne<KV>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act);
         K_(0) K_(2) K_(8) K_(12) K_(17) K_(18) K_(20)
 #undef K_
         default: return false;

@@ -5,9 +5,9 @@
 //                            RMSNorm, optional shared-expert gate logit
 //   route    k_route         per-token top-K, one wave per token (wave_route);
 //                            softmax or sigmoid+bias weights
-//   decode   k_dec_gate_up2  routing of the block's token in every wave
-//                            (wave_route), then act[p] = w_k SwiGLU(G_e x_t, U_e x_t),
-//                            one wave per pair
+//   decode   k_dec_gate_up2  each wave selects its pair's expert (wave_kth),
+//                            then act[p] = w_k SwiGLU(G_e x_t, U_e x_t), one wave
+//                            per pair
 //            k_gemv_gate_up  the same for the shared expert (no routing)
 //            k_dec_down      out[t] = sum_k D_e act[p] (+ shared, + residual)
 //   prefill  k_dispatch      stable expert grouping, tile list (one block)
@@ -95,32 +95,19 @@ __device__ inline uint32_t* route_lds() {
     return r[threadIdx.x >> 6];
 }
 
-// Top-K selection of one token by one wave, E <= 64 * NE, the whole wave
+// Selection keys of one token in one wave, E <= 64 * NE, the whole wave
 // active (src/lib.rs:43-60, kernels/glm.metal:81-98). Candidate j of a lane is
 // expert e = lane + 64 j with selection key s = logit (+ bias) (softmax) or
 // sigmoid(logit) (+ bias) (sigmoid routing), and weight input wv = s
 // (softmax) or sigmoid(logit). Keys compare in IEEE total order
-// (f32::total_cmp, as uint32 through ingot_orderable); the selection is the K
-// highest keys, equal keys toward the lower id, in that order:
-//   1. a threshold T bit by bit from the top, keeping at least K keys >= T
-//      (ballot counts, no data movement); it stops as soon as exactly K keys
-//      are >= T, else ends at the K-th highest key;
-//   2. the selected set: the K keys >= T in the first case; keys above T,
-//      then keys equal to T by ascending id until there are K, in the second;
-//   3. the K candidates are compacted in id order into LDS, lane m < K takes
-//      candidate m, reads all K keys (LDS broadcast) and counts those that
-//      precede it (higher key, or equal key and lower id: an earlier
-//      position), and puts itself at that rank.
-// Lane k < K ends with selection k's id and weight input. Returns whether
-// this lane saw a non-finite logit or bias.
+// (f32::total_cmp) as uint32 through ingot_orderable; an absent candidate
+// (e >= E) has key 0. Selection order: higher key first, equal keys toward
+// the lower id. Returns whether this lane saw a non-finite logit or bias.
 template <int NE>
-__device__ inline bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
-                                  uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
+__device__ inline bool route_keys(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E,
+                                  uint32_t sigmoid_mode, uint32_t (&key)[NE], float (&wv)[NE], bool (&ok)[NE]) {
     INGOT_NO_CONTRACT
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t key[NE];
-    float wv[NE];
-    bool ok[NE];
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < NE; ++j) {
@@ -143,29 +130,60 @@ __device__ inline bool wave_route(const float* __restrict__ l, const float* __re
             key[j] = ingot_orderable(sk);
         }
     }
-    // 1. Keys of absent candidates are 0 and never counted for a threshold
-    //    above 0 (T stays 0 only when fewer than K keys are above 0).
+    return bad;
+}
+
+// Threshold for the n highest keys (1 <= n <= E), bit by bit from the top,
+// keeping at least n keys >= T (ballot counts, no data movement). Stops with
+// exact = true as soon as exactly n keys are >= T; otherwise T ends at the
+// n-th highest key value. Absent candidates (key 0) are never counted for a
+// threshold above 0.
+template <int NE>
+__device__ inline uint32_t route_threshold(const uint32_t (&key)[NE], uint32_t n, bool& exact) {
     uint32_t T = 0;
-    bool exact = false;
+    exact = false;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t c = T | (1u << bit);
-        uint32_t n = 0;
+        uint32_t cnt = 0;
 #pragma unroll
-        for (int j = 0; j < NE; ++j) n += (uint32_t)__popcll(__ballot(key[j] >= c));
-        if (n >= K) {
+        for (int j = 0; j < NE; ++j) cnt += (uint32_t)__popcll(__ballot(key[j] >= c));
+        if (cnt >= n) {
             T = c;
-            if (n == K) {
+            if (cnt == n) {
                 exact = true;
                 break;
             }
         }
     }
+    return T;
+}
+
+// Top-K selection of one token by one wave (route_keys order):
+//   1. T = route_threshold(K);
+//   2. the selected set: the K keys >= T when exact; else keys above T, then
+//      keys equal to T by ascending id until there are K;
+//   3. the K candidates are compacted in id order into LDS, lane m < K takes
+//      candidate m, reads all K keys (LDS broadcast) and counts those that
+//      precede it (higher key, or equal key and lower id: an earlier
+//      position), and puts itself at that rank.
+// Lane k < K ends with selection k's id and weight input. Returns whether
+// this lane saw a non-finite logit or bias.
+template <int NE>
+__device__ inline bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
+                                  uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t key[NE];
+    float wv[NE];
+    bool ok[NE];
+    const bool bad = route_keys<NE>(l, bias, E, sigmoid_mode, key, wv, ok);
+    bool exact;
+    const uint32_t T = route_threshold<NE>(key, K, exact);
     uint64_t sel[NE];
     if (exact) {  // T > 0: absent candidates excluded
 #pragma unroll
         for (int j = 0; j < NE; ++j) sel[j] = __ballot(key[j] >= T);
     } else {
-        // 2. K <= E: at least K - (keys above T) present candidates equal T.
+        // K <= E: at least K - (keys above T) present candidates equal T.
         uint32_t need = K;
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
@@ -234,15 +252,67 @@ __device__ inline float wave_route_weight(float my_v, uint32_t K, uint32_t sigmo
     return sigmoid_mode ? num / total * scale : num / total;
 }
 
-// wave_route for any E <= 1024 (the runtime E picks the candidates per lane).
-__device__ inline bool wave_route_any(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E,
-                                      uint32_t K, uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
-    if (E <= 64u) return wave_route<1>(l, bias, E, K, sigmoid_mode, my_id, my_v);
-    if (E <= 128u) return wave_route<2>(l, bias, E, K, sigmoid_mode, my_id, my_v);
-    if (E <= 256u) return wave_route<4>(l, bias, E, K, sigmoid_mode, my_id, my_v);
-    if (E <= 512u) return wave_route<8>(l, bias, E, K, sigmoid_mode, my_id, my_v);
-    return wave_route<16>(l, bias, E, K, sigmoid_mode, my_id, my_v);
+// Selection k (0-based, k < K <= E) of one token alone, from the keys of
+// route_keys: the (k+1)-th highest key, equal keys toward the lower id.
+// Returns its expert id (wave-uniform); wv_k receives its weight input.
+//   exact threshold: exactly k+1 keys are >= T, so selection k is the lowest
+//   of them, and among equal lowest keys the one with the highest id;
+//   otherwise T is the (k+1)-th key value: with g keys above T, selection k
+//   is the (k+1-g)-th lowest id among the keys equal to T.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)0xffffffff, (int)v, 0xb1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)0xffffffff, (int)v, 0x4e, 0xf, 0xf, false));  // quad_perm [2,3,0,1]
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)0xffffffff, (int)v, 0x141, 0xf, 0xf, false)); // row_half_mirror
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)0xffffffff, (int)v, 0x140, 0xf, 0xf, false)); // row_mirror
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return min(min(a, b), min(c, d));
 }
+
+template <int NE>
+__device__ inline uint32_t wave_kth(const uint32_t (&key)[NE], const float (&wv)[NE], const bool (&ok)[NE],
+                                    uint32_t k, float& wv_k) {
+    bool exact;
+    const uint32_t T = route_threshold<NE>(key, k + 1u, exact);
+    uint32_t id = 0;
+    if (exact) {
+        uint32_t lo = 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) lo = min(lo, key[j] >= T ? key[j] : 0xffffffffu);
+        lo = wave_min_u32(lo);
+#pragma unroll
+        for (int j = NE - 1; j >= 0; --j) {
+            const uint64_t bj = __ballot(key[j] == lo);
+            if (bj) {
+                id = 64u * j + 63u - (uint32_t)__builtin_clzll(bj);
+                break;
+            }
+        }
+    } else {
+        uint32_t need = k + 1u;
+#pragma unroll
+        for (int j = 0; j < NE; ++j) need -= (uint32_t)__popcll(__ballot(ok[j] && key[j] > T));
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            uint64_t eq = __ballot(ok[j] && key[j] == T);
+            const uint32_t n = (uint32_t)__popcll(eq);
+            if (need <= n) {
+                for (uint32_t q = 1; q < need; ++q) eq &= eq - 1ull;
+                id = 64u * j + (uint32_t)__builtin_ctzll(eq);
+                break;
+            }
+            need -= n;
+        }
+    }
+    const uint32_t owner = id & 63u, slot = id >> 6;
+    float mine = wv[0];
+#pragma unroll
+    for (int j = 1; j < NE; ++j)
+        if ((uint32_t)j == slot) mine = wv[j];
+    wv_k = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)owner));
+    return id;
+}
+
 
 // ---------------------------------------------------------------- router
 // One wave per (group of TOK tokens, group of experts). Lane l holds the
@@ -532,16 +602,20 @@ __device__ __forceinline__ void load_x_ilv(const float4* __restrict__ s, uint32_
 }
 
 // ---------------------------------------------- decode: routed gate/up
-// grid (ceil(F / RPW), T), 512 threads (8 waves). Every wave routes the
-// block's token itself (wave_route: no barrier, nothing shared), so each wave
-// issues its weight loads as soon as its own selection is done; wave 0 of
-// block 0 writes the token's ids and weights for the down kernel. Wave w
-// computes rows [RPW*bx, +RPW) of the gate and up projections of pairs
-// k = w, w+8, ... and stores w_k * SwiGLU(g, u) (the routing weight folded
-// in for the down kernel); each lane keeps its input chunks in registers.
+// grid (ceil(F / RPW), T), 512 threads (8 waves), E <= 64 * NE. Wave w owns
+// pairs k = w, w+8, ... of the block's token: it finds each pair's expert
+// itself (wave_kth, selection k alone: no barrier, nothing shared) and issues
+// that pair's weight loads at once. The routing weights need every
+// selection's weight input: each wave leaves its pairs' in LDS, and after the
+// barrier that publishes the staged input every wave forms the softmax (or
+// sigmoid) weights in selection order (wave_route_weight); the waves of
+// block 0 write the token's ids and weights for the down kernel. Wave w
+// computes rows [RPW*bx, +RPW) of the gate and up projections and stores
+// w_k * SwiGLU(g, u) (the routing weight folded in for the down kernel);
+// each lane keeps its input chunks in registers.
 constexpr uint32_t GU_WAVES = 8;
 
-template <int KIND, int CPL, int RPW, int NP>
+template <int KIND, int CPL, int RPW, int NP, int NE>
 __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
                                                       uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
                                                       const float* __restrict__ x, const float* __restrict__ logits,
@@ -570,16 +644,28 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                        : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     stage_codebooks<KIND>();  // decoded only after the barrier that publishes s_x4
-    uint32_t my_id;
-    float my_v;
-    const bool bad = wave_route_any(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, my_id, my_v);
+    __shared__ float s_sv[64];  // weight input of each selection
+    uint32_t key[NE];
+    float wv[NE];
+    bool ok[NE];
+    const bool bad = route_keys<NE>(logits + (uint64_t)t * E, bias, E, sigmoid_mode, key, wv, ok);
+    uint32_t eid[NP];
+    float ev[NP];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const uint32_t k = wave + GU_WAVES * n;
+        if (n == 0 || k < K) eid[n] = wave_kth<NE>(key, wv, ok, k < K ? k : 0u, ev[n]);
+        else {  // no such pair: re-read pair 0's rows (not stored)
+            eid[n] = eid[0];
+            ev[n] = ev[0];
+        }
+    }
     // Weight loads of the wave's pairs k = wave + 8n (n < NP; K <= 8 NP);
     // a pair beyond K re-reads pair 0's rows and is not stored.
     typename Fm::Raw rg[NP][RPW][CPL], ru[NP][RPW][CPL];
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GU_WAVES * n;
-        const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)(k < K ? k : 0u));
+        const uint32_t e = eid[n];
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const uint32_t r = min(r0 + i, F - 1);
@@ -593,15 +679,23 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
         }
     }
-    // Routing weights (after the loads are in flight): block 0's wave 0
-    // publishes the token's ids and weights for the down kernel.
-    const float w = wave_route_weight(my_v, K, sigmoid_mode, scale);
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const uint32_t k = wave + GU_WAVES * n;
+        if (k < K && lane == 0) {
+            s_sv[k] = ev[n];
+            if (blockIdx.x == 0) ids[(uint64_t)t * K + k] = eid[n];
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+        if (xok[m]) s_x4[threadIdx.x + 512u * m] = xa[m];
+    __syncthreads();
+    // Routing weights in selection order; block 0's wave 0 publishes them.
+    const float w = wave_route_weight(lane < K ? s_sv[lane] : 0.f, K, sigmoid_mode, scale);
     if (blockIdx.x == 0 && wave == 0) {
         if (flags && __any(bad) && lane == 0) atomicOr(flags, FLAG_NONFINITE);
-        if (lane < K) {
-            ids[(uint64_t)t * K + lane] = my_id;
-            wts[(uint64_t)t * K + lane] = w;
-        }
+        if (lane < K) wts[(uint64_t)t * K + lane] = w;
     }
     float wk[NP];  // routing weight of each of the wave's pairs: act is stored as w_k * SwiGLU
 #pragma unroll
@@ -609,10 +703,6 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         const uint32_t k = wave + GU_WAVES * n;
         wk[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)(k < K ? k : 0u)));
     }
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-        if (xok[m]) s_x4[threadIdx.x + 512u * m] = xa[m];
-    __syncthreads();
     float xv[CPL][32], xs0[CPL], xs1[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
