@@ -774,15 +774,19 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
     const uint32_t nv = K * nchF + nchS, KF = K * F;
     const uint32_t r0 = (blockIdx.x * DOWN_WAVES + wave) * RPW;
+    // Every load below is unconditional (indices clamped into the virtual
+    // row), so the compiler's load counting can wait for each chunk's weights
+    // alone; lanes past the virtual row load valid bytes and discard them.
+    // One chunk format for routed and shared experts keeps the weight loads
+    // branch-free too.
+    constexpr bool UNI = KS < 0 || KS == KD;
+    const uint32_t KC = K * nchF;  // routed chunks
     // 1. expert ids of this lane's chunks of the virtual row (chunk v: pair
     //    v / nchF; the quotient by multiply-high, exact for v < 2^32 / nchF)
     const uint32_t mag = 0xffffffffu / nchF + 1u;
     uint32_t eid[VPL];
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const uint32_t v = lane + 64u * j;
-        eid[j] = v < K * nchF ? ids[(uint64_t)t * K + __umulhi(v, mag)] : 0u;
-    }
+    for (int j = 0; j < VPL; ++j) eid[j] = ids[(uint64_t)t * K + __umulhi(min(lane + 64u * j, KC - 1u), mag)];
     // 2. this thread's activations: slot u = tid + DOWN_THREADS m is float4
     //    u % 8 of chunk u / 8 (a chunk's two 16-value groups in two lane quads)
     float4 av[DOWN_ACT4];
@@ -790,46 +794,42 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     const float* st = sact + (uint64_t)t * SF;
 #pragma unroll
     for (int m = 0; m < (int)DOWN_ACT4; ++m) {
-        const uint32_t u = tid + DOWN_THREADS * m, v = u >> 3, i4 = 4u * (u & 7u);
-        av[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (v < K * nchF) {
-            const uint32_t k = __umulhi(v, mag);
-            av[m] = *reinterpret_cast<const float4*>(at + k * F + Fd::col(v - k * nchF, i4));
-        } else if (KS >= 0 && v < nv) {
-            av[m] = *reinterpret_cast<const float4*>(st + Fs::col(v - K * nchF, i4));
-        }
+        const uint32_t u = tid + DOWN_THREADS * m, i4 = 4u * (u & 7u), vc = min(u >> 3, nv - 1u);
+        const uint32_t vr = min(vc, KC - 1u), k = __umulhi(vr, mag);
+        const float* p = at + k * F + Fd::col(vr - k * nchF, i4);
+        if constexpr (KS >= 0) p = vc >= KC ? st + Fs::col(vc - KC, i4) : p;
+        av[m] = *reinterpret_cast<const float4*>(p);
     }
     const float sgv = (KS >= 0 && sgl) ? sgl[t] : 0.f;
     __builtin_amdgcn_sched_barrier(0);
     // 3. weight loads for all RPW rows
     const uint8_t* base[VPL];
+    uint64_t stride[VPL];
     uint32_t cc[VPL];
-    bool isS[VPL];
+    bool isS[VPL], has[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-        const uint32_t v = lane + 64u * j;
-        base[j] = nullptr;
-        cc[j] = 0;
-        isS[j] = false;
-        if (v < K * nchF) {
-            base[j] = down + (uint64_t)eid[j] * H * dstride;
-            cc[j] = v - __umulhi(v, mag) * nchF;
-        } else if (v < nv) {
-            base[j] = sdown;
-            cc[j] = v - K * nchF;
-            isS[j] = true;
-        }
+        const uint32_t v = lane + 64u * j, vr = min(v, KC - 1u);
+        has[j] = v < nv;
+        isS[j] = KS >= 0 && v >= KC && v < nv;
+        base[j] = isS[j] ? sdown : down + (uint64_t)eid[j] * H * dstride;
+        stride[j] = isS[j] ? sdstride : dstride;
+        cc[j] = isS[j] ? v - KC : vr - __umulhi(vr, mag) * nchF;
     }
     typename Fd::Raw rd[RPW][VPL];
-    typename Fs::Raw rs[KS >= 0 ? RPW : 1][KS >= 0 ? VPL : 1];
+    typename Fs::Raw rs[UNI ? 1 : RPW][UNI ? 1 : VPL];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
         const uint32_t r = min(r0 + i, H - 1);
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
-            if (!base[j]) continue;
-            if (KS >= 0 && isS[j]) rs[KS >= 0 ? i : 0][KS >= 0 ? j : 0] = Fs::load_raw(base[j] + (uint64_t)r * sdstride, cc[j]);
-            else rd[i][j] = Fd::load_raw(base[j] + (uint64_t)r * dstride, cc[j]);
+            if constexpr (UNI) {
+                rd[i][j] = Fd::load_raw(base[j] + (uint64_t)r * stride[j], cc[j]);
+            } else {
+                if (!has[j]) continue;
+                if (isS[j]) rs[UNI ? 0 : i][UNI ? 0 : j] = Fs::load_raw(base[j] + (uint64_t)r * stride[j], cc[j]);
+                else rd[i][j] = Fd::load_raw(base[j] + (uint64_t)r * stride[j], cc[j]);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -859,14 +859,14 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-        if (!base[j]) continue;
+        if (!has[j]) continue;
         float xv[32];
         load_x_ilv(s_act4, j, lane, xv);
         const float2 xs = reinterpret_cast<const float2*>(s_sum)[lane + 64u * j];
         const float xs0 = xs.x, xs1 = xs.y;
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
-            if (KS >= 0 && isS[j]) acc[i] += Fs::dot_raw(rs[KS >= 0 ? i : 0][KS >= 0 ? j : 0], cc[j], xv, xs0, xs1);
+            if (!UNI && isS[j]) acc[i] += Fs::dot_raw(rs[UNI ? 0 : i][UNI ? 0 : j], cc[j], xv, xs0, xs1);
             else acc[i] += Fd::dot_raw(rd[i][j], cc[j], xv, xs0, xs1);
         }
     }
