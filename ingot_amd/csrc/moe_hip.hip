@@ -148,11 +148,18 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
     // wide (T x E / 4 blocks); from 64 tokens the 64-output transposed kernel.
     const bool decode = T < 64;
     if (!decode && E % 32u == 0 && (HB == 4 || HB == 8)) {
-        const dim3 grid((T + 7) / 8, E / 32);
-        if (HB == 8)
-            hipLaunchKernelGGL((k_router_t<8>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, logits, sgl, xn);
-        else
-            hipLaunchKernelGGL((k_router_t<4>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, logits, sgl, xn);
+        // 16 experts per block when 32 would leave fewer than two blocks per CU
+        const bool eb16 = (T + 7) / 8 * (E / 32) < 512;
+        const dim3 grid((T + 7) / 8, E / (eb16 ? 16 : 32));
+#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, logits, sgl, xn)
+        if (HB == 8) {
+            if (eb16) RT(8, 16);
+            else RT(8, 32);
+        } else {
+            if (eb16) RT(4, 16);
+            else RT(4, 32);
+        }
+#undef RT
         return true;
     }
     const uint32_t epw = decode ? 1u : 8u;
@@ -1047,15 +1054,13 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
         // Dispatch stage: expert grouping, and for the f16 GEMM the split of x
         // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
-            hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, ss, ids, P, E, tm, capf, counts, first, tiles, pairs,
-                               inverse, S, K);
+            // With the f16 GEMM, blocks 1.. of the dispatch launch split x into f16 hi + lo.
+            const uint64_t n = f16 ? (uint64_t)T * H : 0ull;
+            const uint32_t nsplit = (uint32_t)((n / 4 + 1023) / 1024);
+            hipLaunchKernelGGL(k_dispatch, dim3(1 + nsplit), dim3(1024), 0, ss, ids, P, E, tm, capf, counts, first, tiles,
+                               pairs, inverse, S, K, xin, n, xh, xl, xs, (uint32_t)xord);
             if (hs && !merge)
                 hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
-            if (f16) {
-                const uint64_t n = (uint64_t)T * H;
-                hipLaunchKernelGGL(k_split_f16, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256), 0, ss, xin, n, xh, xl,
-                                   xs, (uint32_t)xord);
-            }
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch";
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {

@@ -11,6 +11,7 @@
 //            k_gemv_gate_up  the same for the shared expert (no routing)
 //            k_dec_down      out[t] = sum_k D_e act[p] (+ shared, + residual)
 //   prefill  k_dispatch      stable expert grouping, tile list (one block)
+//            (its other blocks split x into f16 hi + lo for k_gemm_f16)
 //            k_gemm_f16      f16-MFMA grouped GEMM on integer weight operands
 //                            (Q4_K, IQ3_XXS, IQ4_NL), A split into f16 hi + lo
 //            k_gemm<GATEUP>  MFMA f32 grouped GEMM, dequantised weights in LDS
@@ -425,6 +426,16 @@ __device__ __forceinline__ void transpose_step(float* v, bool hi) {
         v[i] = keep + xor_partner<M>(send);
     }
 }
+// 32 sums: five transposed steps leave output ((l >> 1) & 31) in lane l, and
+// the last step (m = 1) adds the partner's partial of the same output.
+__device__ __forceinline__ float transpose_sum32(float (&v)[32], uint32_t lane) {
+    transpose_step<32, 32>(v, lane & 32u);
+    transpose_step<16, 16>(v, lane & 16u);
+    transpose_step<8, 8>(v, lane & 8u);
+    transpose_step<4, 4>(v, lane & 4u);
+    transpose_step<2, 2>(v, lane & 2u);
+    return v[0] + xor_partner<1>(v[0]);
+}
 __device__ __forceinline__ float transpose_sum64(float (&v)[64], uint32_t lane) {
     transpose_step<64, 32>(v, lane & 32u);
     transpose_step<32, 16>(v, lane & 16u);
@@ -435,15 +446,17 @@ __device__ __forceinline__ float transpose_sum64(float (&v)[64], uint32_t lane) 
     return v[0];
 }
 
-// Prefill router: grid (ceil(T / 8), E / 32), 256 threads. Wave w of block
-// (bx, by) computes the logits of tokens 8 bx + 2 w, +1 for experts
-// 32 by .. +31: lane l keeps the fixed-order FMA chain of its columns
-// 4 l + 256 i + c (as k_router) for each of the 64 (token, expert) pairs, and
-// one transposed butterfly leaves pair (t, e) = (l / 32, l % 32) in lane l.
+// Prefill router: grid (ceil(T / 8), E / EB), 256 threads, EB = 32 or 16
+// experts per block (16: twice the blocks, two per CU, for short inputs).
+// Wave w of block (bx, by) computes the logits of tokens 8 bx + 2 w, +1 for
+// experts EB by .. +EB-1: lane l keeps the fixed-order FMA chain of its
+// columns 4 l + 256 i + c (as k_router) for each of the 2 EB (token, expert)
+// pairs, and one transposed butterfly leaves pair (t, e) = (l / 32, l % 32)
+// (EB = 32) or (l / 32, (l / 2) % 16) (EB = 16) in lane l.
 // The block's router rows pass through LDS in double-buffered chunks of 4.
 // RMSNorm (gain: written to xn by the by == 0 blocks) and the shared-expert
 // gate logit (sgvec: by == 0 blocks, wave_sum) are computed as in k_router.
-template <int HB>
+template <int HB, int EB>
 __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, const float* __restrict__ W,
                                                   const float* __restrict__ sgvec, const float* __restrict__ gain,
                                                   float eps, uint32_t T, uint32_t E, float* __restrict__ logits,
@@ -453,7 +466,8 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
     constexpr int CH = 4;                         // router rows per LDS chunk
     __shared__ float4 sw[2][CH][Q];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
-    const uint32_t t0 = blockIdx.x * 8u + 2u * wave, e0 = blockIdx.y * 32u;
+    constexpr uint32_t NC = EB / CH;  // chunks
+    const uint32_t t0 = blockIdx.x * 8u + 2u * wave, e0 = blockIdx.y * (uint32_t)EB;
     float xr[2][HB * 4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -505,12 +519,12 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             if (lane == 0 && t0 + t < T) sgl[t0 + t] = acc;
         }
     }
-    // Router rows e0 .. e0 + 31 in 8 chunks of 4 through LDS.
+    // Router rows e0 .. e0 + EB - 1 in NC chunks of 4 through LDS.
     constexpr uint32_t PER = CH * Q / 256u;  // float4 per thread per chunk
     float4 stage[PER];
-    float p[64];
+    float p[2 * EB];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) p[i] = 0.f;
+    for (int i = 0; i < 2 * EB; ++i) p[i] = 0.f;
 #pragma unroll
     for (uint32_t k = 0; k < PER; ++k) {
         const uint32_t idx = tid + 256u * k;
@@ -518,8 +532,8 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t c = 0; c < 8; ++c) {
-        if (c + 1 < 8) {
+    for (uint32_t c = 0; c < NC; ++c) {
+        if (c + 1 < NC) {
 #pragma unroll
             for (uint32_t k = 0; k < PER; ++k) {
                 const uint32_t idx = tid + 256u * k;
@@ -539,10 +553,10 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
                 float acc = 0.f;
 #pragma unroll
                 for (int j = 0; j < HB * 4; ++j) acc = __builtin_fmaf(wv[j], xr[t][j], acc);
-                p[t * 32 + CH * c + r] = acc;
+                p[t * EB + CH * c + r] = acc;
             }
         }
-        if (c + 1 < 8) {
+        if (c + 1 < NC) {
 #pragma unroll
             for (uint32_t k = 0; k < PER; ++k) {
                 const uint32_t idx = tid + 256u * k;
@@ -551,9 +565,15 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             __syncthreads();
         }
     }
-    const float v = transpose_sum64(p, lane);
-    const uint32_t t = t0 + (lane >> 5), e = e0 + (lane & 31u);
-    if (t < T) logits[(uint64_t)t * E + e] = v;
+    if constexpr (EB == 32) {
+        const float v = transpose_sum64(p, lane);
+        const uint32_t t = t0 + (lane >> 5), e = e0 + (lane & 31u);
+        if (t < T) logits[(uint64_t)t * E + e] = v;
+    } else {
+        const float v = transpose_sum32(p, lane);
+        const uint32_t t = t0 + (lane >> 5), e = e0 + ((lane >> 1) & 15u);
+        if (t < T && (lane & 1u) == 0) logits[(uint64_t)t * E + e] = v;
+    }
 }
 
 // ----------------------------------------------------------------- route
@@ -1019,12 +1039,25 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
 //   [w seg, (w + 1) seg); a histogram per wave gives each wave's start inside
 //   every expert's range; the wave then walks its segment 64 pairs at a time,
 //   and a pair's rank among earlier lanes with the same expert comes from
-//   ballots over the bits of the expert id.
+//   ballots over the bits of the expert id. A wave reads its ids DSP_BATCH
+//   per lane at a time, all loads issued before the first is used.
+// Blocks 1.. (when xh != NULL) split the token inputs into f16 hi + lo for
+// the f16 GEMM (split_f16_part), beside the dispatch.
+constexpr uint32_t DSP_BATCH = 8;
+__device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
+                                      _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g);
+
 __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
                                                    uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
                                                    uint32_t* __restrict__ first, uint32_t* __restrict__ tiles,
                                                    uint32_t* __restrict__ pairs, uint32_t* __restrict__ inverse,
-                                                   uint32_t S, uint32_t K) {
+                                                   uint32_t S, uint32_t K, const float* __restrict__ x, uint64_t xn,
+                                                   _Float16* __restrict__ xh, _Float16* __restrict__ xl,
+                                                   float* __restrict__ xs, uint32_t xorder) {
+    if (blockIdx.x > 0) {
+        split_f16_part(x, xn, xh, xl, xs, xorder, (uint64_t)(blockIdx.x - 1u) * blockDim.x + threadIdx.x);
+        return;
+    }
     __shared__ uint32_t hist[16][1024];  // per wave, per expert; then each wave's running position
     __shared__ uint32_t wsum[32];
     __shared__ uint32_t tot[3];
@@ -1035,7 +1068,14 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
     rbin[tid] = 0;
     __syncthreads();
     const uint32_t seg = (P + 15u) / 16u, s0 = min(P, wave * seg), s1 = min(P, s0 + seg);
-    for (uint32_t p = s0 + lane; p < s1; p += 64u) atomicAdd(&hist[wave][ids[p]], 1u);
+    for (uint32_t b0 = s0; b0 < s1; b0 += 64u * DSP_BATCH) {
+        uint32_t xv[DSP_BATCH];
+#pragma unroll
+        for (int i = 0; i < (int)DSP_BATCH; ++i) xv[i] = ids[min(b0 + 64u * i + lane, P - 1u)];
+#pragma unroll
+        for (int i = 0; i < (int)DSP_BATCH; ++i)
+            if (b0 + 64u * i + lane < s1) atomicAdd(&hist[wave][xv[i]], 1u);
+    }
     __syncthreads();
     // Expert tid: its count, and each wave's offset within the expert.
     uint32_t n = 0;
@@ -1109,24 +1149,32 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
     uint32_t nbits = 1;
     while ((1u << nbits) < E) ++nbits;
     const uint64_t lt = (1ull << lane) - 1ull;
-    for (uint32_t base = s0; base < s1; base += 64u) {
-        const uint32_t p = base + lane;
-        const bool live = p < s1;
-        const uint32_t x = live ? ids[p] : 0u;
-        uint64_t same = __ballot(live);
-        for (uint32_t b = 0; b < nbits; ++b) {
-            const uint64_t one = __ballot(live && ((x >> b) & 1u));
-            same &= ((x >> b) & 1u) ? one : ~one;
+    for (uint32_t b0 = s0; b0 < s1; b0 += 64u * DSP_BATCH) {
+        uint32_t xv[DSP_BATCH];
+#pragma unroll
+        for (int i = 0; i < (int)DSP_BATCH; ++i) xv[i] = ids[min(b0 + 64u * i + lane, P - 1u)];
+#pragma unroll
+        for (int i = 0; i < (int)DSP_BATCH; ++i) {
+            const uint32_t base = b0 + 64u * i;
+            if (base >= s1) break;
+            const uint32_t p = base + lane;
+            const bool live = p < s1;
+            const uint32_t e = live ? xv[i] : 0u;
+            uint64_t same = __ballot(live);
+            for (uint32_t b = 0; b < nbits; ++b) {
+                const uint64_t one = __ballot(live && ((e >> b) & 1u));
+                same &= ((e >> b) & 1u) ? one : ~one;
+            }
+            if (live) {
+                const uint32_t pos = hist[wave][e] + (uint32_t)__popcll(same & lt);
+                pairs[pos] = p;
+                inverse[p] = pos;
+            }
+            // every lane has read the running positions before the leaders advance them
+            wave_sync();
+            if (live && (same & lt) == 0) hist[wave][e] += (uint32_t)__popcll(same);
+            wave_sync();
         }
-        if (live) {
-            const uint32_t pos = hist[wave][x] + (uint32_t)__popcll(same & lt);
-            pairs[pos] = p;
-            inverse[p] = pos;
-        }
-        // every lane has read the running positions before the leaders advance them
-        __builtin_amdgcn_wave_barrier();
-        if (live && (same & lt) == 0) hist[wave][x] += (uint32_t)__popcll(same);
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1329,7 +1377,8 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
 //           4 kq + i + 16 h at position 2 i + h; A is stored in that order
 //           (A_IQ4NL).
 //   The gate/up kernel writes act in the order of the down projection's
-//   format; k_split_f16 writes x in the order of gate/up's.
+//   format; the dispatch launch's split blocks (split_f16_part) write x in
+//   the order of gate/up's.
 //   GATEUP: block b covers act columns 64 b..+63; wave w gate and up rows
 //   64 b + 32 w ..+31 (n-blocks 0,1 gate, 2,3 up). Writes act = SwiGLU split
 //   into out_h/out_l [P][F] and, for a Q4_K down projection, its 32-column
@@ -1913,9 +1962,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 // stored in column order `order` (A_NATURAL or A_IQ3XXS, whose permutation
 // keeps runs of 4 columns together; H % 256 == 0 for the latter), and the
 // natural 32-column sums xs [T][H/32] used by the Q4_K mins term.
-__global__ __launch_bounds__(256) void k_split_f16(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
-                                                   _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order) {
-    const uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4u;
+// x -> f16 hi + lo in the order `order`, and the natural 32-column sums; item
+// g covers x[4g, 4g + 4) (8 consecutive items per 32-column group, so the
+// threads of a wave cover whole groups; n is a multiple of 32).
+__device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
+                                      _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g) {
+    const uint64_t i = g * 4u;
     const bool live = i < n;
     const float4 v = live ? *reinterpret_cast<const float4*>(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float a[4] = {v.x, v.y, v.z, v.w};
@@ -1924,7 +1976,6 @@ __global__ __launch_bounds__(256) void k_split_f16(const float* __restrict__ x, 
 #pragma unroll
         for (int j = 0; j < 4; ++j) split_f16(a[j], xh[o + j], xl[o + j]);
     }
-    // 8 consecutive threads cover one 32-column group (n is a multiple of 32).
     float s = (a[0] + a[1]) + (a[2] + a[3]);
     s += dpp_mov<0xb1>(s);
     s += dpp_mov<0x4e>(s);
