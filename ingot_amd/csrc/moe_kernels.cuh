@@ -105,7 +105,7 @@ __device__ inline uint32_t* route_lds() {
 // (e >= E) has key 0. Selection order: higher key first, equal keys toward
 // the lower id. Returns whether this lane saw a non-finite logit or bias.
 template <int NE>
-__device__ inline bool route_keys(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E,
+__device__ __forceinline__ bool route_keys(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E,
                                   uint32_t sigmoid_mode, uint32_t (&key)[NE], float (&wv)[NE], bool (&ok)[NE]) {
     INGOT_NO_CONTRACT
     const uint32_t lane = threadIdx.x & 63u;
@@ -140,7 +140,7 @@ __device__ inline bool route_keys(const float* __restrict__ l, const float* __re
 // n-th highest key value. Absent candidates (key 0) are never counted for a
 // threshold above 0.
 template <int NE>
-__device__ inline uint32_t route_threshold(const uint32_t (&key)[NE], uint32_t n, bool& exact) {
+__device__ __forceinline__ uint32_t route_threshold(const uint32_t (&key)[NE], uint32_t n, bool& exact) {
     uint32_t T = 0;
     exact = false;
     for (int bit = 31; bit >= 0; --bit) {
@@ -170,7 +170,7 @@ __device__ inline uint32_t route_threshold(const uint32_t (&key)[NE], uint32_t n
 // Lane k < K ends with selection k's id and weight input. Returns whether
 // this lane saw a non-finite logit or bias.
 template <int NE>
-__device__ inline bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
+__device__ __forceinline__ bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
                                   uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t key[NE];
@@ -271,7 +271,7 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 }
 
 template <int NE>
-__device__ inline uint32_t wave_kth(const uint32_t (&key)[NE], const float (&wv)[NE], const bool (&ok)[NE],
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&key)[NE], const float (&wv)[NE], const bool (&ok)[NE],
                                     uint32_t k, float& wv_k) {
     bool exact;
     const uint32_t T = route_threshold<NE>(key, k + 1u, exact);
@@ -281,36 +281,46 @@ __device__ inline uint32_t wave_kth(const uint32_t (&key)[NE], const float (&wv)
 #pragma unroll
         for (int j = 0; j < NE; ++j) lo = min(lo, key[j] >= T ? key[j] : 0xffffffffu);
         lo = wave_min_u32(lo);
+        bool found = false;
 #pragma unroll
         for (int j = NE - 1; j >= 0; --j) {
             const uint64_t bj = __ballot(key[j] == lo);
-            if (bj) {
+            if (!found && bj) {
                 id = 64u * j + 63u - (uint32_t)__builtin_clzll(bj);
-                break;
+                found = true;
             }
         }
     } else {
         uint32_t need = k + 1u;
 #pragma unroll
         for (int j = 0; j < NE; ++j) need -= (uint32_t)__popcll(__ballot(ok[j] && key[j] > T));
+        bool found = false;
 #pragma unroll
         for (int j = 0; j < NE; ++j) {
             uint64_t eq = __ballot(ok[j] && key[j] == T);
             const uint32_t n = (uint32_t)__popcll(eq);
-            if (need <= n) {
-                for (uint32_t q = 1; q < need; ++q) eq &= eq - 1ull;
-                id = 64u * j + (uint32_t)__builtin_ctzll(eq);
-                break;
+            if (!found) {
+                if (need <= n) {
+                    for (uint32_t q = 1; q < need; ++q) eq &= eq - 1ull;
+                    id = 64u * j + (uint32_t)__builtin_ctzll(eq);
+                    found = true;
+                } else {
+                    need -= n;
+                }
             }
-            need -= n;
         }
     }
+    // The owner's candidates are read slot by slot and then selected, so the
+    // candidate array is never indexed by a run-time value (that would put it
+    // in memory).
     const uint32_t owner = id & 63u, slot = id >> 6;
-    float mine = wv[0];
+    float mine = 0.f;
 #pragma unroll
-    for (int j = 1; j < NE; ++j)
-        if ((uint32_t)j == slot) mine = wv[j];
-    wv_k = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)owner));
+    for (int j = 0; j < NE; ++j) {
+        const float rj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv[j]), (int)owner));
+        mine = (uint32_t)j == slot ? rj : mine;
+    }
+    wv_k = mine;
     return id;
 }
 
