@@ -109,27 +109,32 @@ __device__ __forceinline__ bool route_keys(const float* __restrict__ l, const fl
                                   uint32_t sigmoid_mode, uint32_t (&key)[NE], float (&wv)[NE], bool (&ok)[NE]) {
     INGOT_NO_CONTRACT
     const uint32_t lane = threadIdx.x & 63u;
+    // All loads first, unconditional (index clamped), so they are in flight
+    // together; absent candidates are masked afterwards.
+    float lv[NE], bv[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j) lv[j] = l[min(lane + 64u * j, E - 1u)];
+    if (bias) {
+#pragma unroll
+        for (int j = 0; j < NE; ++j) bv[j] = bias[min(lane + 64u * j, E - 1u)];
+    }
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < NE; ++j) {
-        const uint32_t e = lane + 64u * j;
-        key[j] = 0;
-        wv[j] = 0.f;
-        ok[j] = e < E;
-        if (ok[j]) {
-            const float v = l[e];
-            const float b = bias ? bias[e] : 0.f;
-            bad |= !isfinite(v) || !isfinite(b);
-            float sk;
-            if (sigmoid_mode) {
-                wv[j] = ingot_det_sigmoid(v);
-                sk = bias ? wv[j] + b : wv[j];
-            } else {
-                sk = bias ? v + b : v;
-                wv[j] = sk;
-            }
-            key[j] = ingot_orderable(sk);
+        ok[j] = lane + 64u * j < E;
+        const float v = lv[j];
+        const float b = bias ? bv[j] : 0.f;
+        bad |= ok[j] && (!isfinite(v) || !isfinite(b));
+        float sk;
+        if (sigmoid_mode) {
+            wv[j] = ingot_det_sigmoid(v);
+            sk = bias ? wv[j] + b : wv[j];
+        } else {
+            sk = bias ? v + b : v;
+            wv[j] = sk;
         }
+        key[j] = ok[j] ? ingot_orderable(sk) : 0u;
+        wv[j] = ok[j] ? wv[j] : 0.f;
     }
     return bad;
 }
@@ -747,23 +752,25 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
         const uint32_t k = wave + GU_WAVES * n;
-        float gs[RPW], us[RPW];
+        if (n == 0 || k < K) {  // a pair beyond K (its loads re-read pair 0's rows) is skipped
+            float gs[RPW], us[RPW];
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            gs[i] = us[i] = 0.f;
+            for (int i = 0; i < RPW; ++i) {
+                gs[i] = us[i] = 0.f;
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                if (lane + 64u * j >= nch) continue;
-                const uint32_t c = lane + 64u * j;
-                gs[i] += Fm::dot_raw(rg[n][i][j], c, xv[j], xs0[j], xs1[j]);
-                us[i] += Fm::dot_raw(ru[n][i][j], c, xv[j], xs0[j], xs1[j]);
+                for (int j = 0; j < CPL; ++j) {
+                    if (lane + 64u * j >= nch) continue;
+                    const uint32_t c = lane + 64u * j;
+                    gs[i] += Fm::dot_raw(rg[n][i][j], c, xv[j], xs0[j], xs1[j]);
+                    us[i] += Fm::dot_raw(ru[n][i][j], c, xv[j], xs0[j], xs1[j]);
+                }
             }
-        }
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            const float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
-            if (k < K && lane == (uint32_t)i && r0 + i < F)
-                act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit) * wk[n];
+            for (int i = 0; i < RPW; ++i) {
+                const float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
+                if (k < K && lane == (uint32_t)i && r0 + i < F)
+                    act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit) * wk[n];
+            }
         }
     }
 }
