@@ -212,6 +212,47 @@ __device__ inline void stage_f16_tables() {
     }
 }
 
+// Tables of the decode GEMV formats that take their inputs as f16 pairs
+// (half_x<KIND>): the input is staged as f16 hi + scaled lo, and the chunk
+// dot product runs on v_dot2 (exact f16 products, fp32 sums).
+//   iq2_xs grid (f16): entry i holds the 8 grid values of ingot_iq2xs_grid[i]
+//     as f16 numbers (value 2j in the low half of word j); signs come from
+//     the iq3 sign masks (same 7-bit sign index, same parity rule).
+template <int KIND>
+constexpr bool half_x() {
+    return KIND == 17;
+}
+__device__ inline uint4* lds_iq2xs_grid_h() {
+    __shared__ uint4 g[512];
+    return g;
+}
+__device__ inline uint32_t f16_bits_of(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+template <int KIND>
+__device__ inline void stage_half_tables() {
+    if constexpr (KIND == 17) {
+        for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) {
+            const uint64_t g = ingot_iq2xs_grid[i];
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                w[j] = f16_bits_of((float)((g >> (16 * j)) & 255u)) | (f16_bits_of((float)((g >> (16 * j + 8)) & 255u)) << 16);
+            lds_iq2xs_grid_h()[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
+            const uint32_t sg = ingot_ksign(i);
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = (((sg >> (2 * j)) & 1u) << 15) | (((sg >> (2 * j + 1)) & 1u) << 31);
+            lds_iq3_signmask()[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
+
 struct Contig {
     __device__ static uint32_t col(uint32_t c, uint32_t i) { return 32u * c + i; }
     __device__ static void load_x(const float* x, uint32_t c, float* xv) {
@@ -382,6 +423,27 @@ struct Fmt<17> : Contig {
     }
     __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
         return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+    // The same sum with the inputs as f16 pairs: xh[q] holds values 2q, 2q+1
+    // (hi), xl[q] their remainders times 2^11; the signed grid values are f16
+    // numbers (sign masks XORed in), so every v_dot2 product is exact.
+    __device__ static float dot_raw_h(const Raw& r, const uint32_t* xh, const uint32_t* xl) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint4 g = lds_iq2xs_grid_h()[r.code[l] & 511u];
+            const uint4 m = lds_iq3_signmask()[(r.code[l] >> 9) & 127u];
+            const uint32_t gs[4] = {g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w};
+            float th = 0.f, tl = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                th = dot2_f16(gs[q], xh[4 * l + q], th);
+                tl = dot2_f16(gs[q], xl[4 * l + q], tl);
+            }
+            const float t = __builtin_fmaf(tl, 1.0f / 2048.0f, th);
+            s = __builtin_fmaf(0.5f + (float)((r.scale >> (4 * (l / 2))) & 15u), t, s);
+        }
+        return half_bits_to_float(r.d) * 0.25f * s;
     }
     __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
         float s = 0.f;

@@ -636,6 +636,32 @@ __device__ __forceinline__ void load_x_ilv(const float4* __restrict__ s, uint32_
     }
 }
 
+// f16 hi + scaled lo of four values, for the formats that take f16 input
+// pairs (half_x): {hi(x0, x1), hi(x2, x3), lo(x0, x1), lo(x2, x3)}, hi rounded
+// toward zero and lo = (x - hi) * 2^11 (exact before its own rounding), so
+// x = hi + lo / 2^11 to about 2^-20 relative. Stored in the float4 slot.
+__device__ __forceinline__ float4 split_h4(float4 a) {
+    const f16x2 h01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a.x, a.y));
+    const f16x2 h23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a.z, a.w));
+    const float r0 = (a.x - (float)h01.x) * 2048.0f, r1 = (a.y - (float)h01.y) * 2048.0f;
+    const float r2 = (a.z - (float)h23.x) * 2048.0f, r3 = (a.w - (float)h23.y) * 2048.0f;
+    const uint4 u = make_uint4(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23),
+                               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1)),
+                               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r2, r3)));
+    return __builtin_bit_cast(float4, u);
+}
+__device__ __forceinline__ void load_xh_ilv(const float4* __restrict__ s, uint32_t j, uint32_t lane, uint32_t* xh,
+                                            uint32_t* xl) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint4 a = __builtin_bit_cast(uint4, s[(8u * j + i) * 64u + lane]);
+        xh[2 * i] = a.x;
+        xh[2 * i + 1] = a.y;
+        xl[2 * i] = a.z;
+        xl[2 * i + 1] = a.w;
+    }
+}
+
 // ---------------------------------------------- decode: routed gate/up
 // grid (ceil(F / RPW), T), 512 threads (8 waves), E <= 64 * NE. Wave w owns
 // pairs k = w, w+8, ... of the block's token: it finds each pair's expert
@@ -659,6 +685,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                                                       uint32_t* __restrict__ ids, float* __restrict__ wts,
                                                       uint32_t* __restrict__ flags, float* __restrict__ act) {
     using Fm = Fmt<KIND>;
+    constexpr bool HX = half_x<KIND>();  // input staged as f16 pairs (split_h4)
     __shared__ float4 s_x4[1024];  // interleaved chunks (ilv_slot), H <= 4096
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
@@ -678,7 +705,9 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         xa[m] = xok[m] ? *reinterpret_cast<const float4*>(xt + Fm::col(c, 4u * (ji & 7u)))
                        : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    stage_codebooks<KIND>();  // decoded only after the barrier that publishes s_x4
+    // decoded only after the barrier that publishes s_x4
+    if constexpr (HX) stage_half_tables<KIND>();
+    else stage_codebooks<KIND>();
     __shared__ float s_sv[64];  // weight input of each selection
     uint32_t key[NE];
     float wv[NE];
@@ -724,7 +753,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     }
 #pragma unroll
     for (int m = 0; m < 2; ++m)
-        if (xok[m]) s_x4[threadIdx.x + 512u * m] = xa[m];
+        if (xok[m]) s_x4[threadIdx.x + 512u * m] = HX ? split_h4(xa[m]) : xa[m];
     __syncthreads();
     // Routing weights in selection order; block 0's wave 0 publishes them.
     const float w = wave_route_weight(lane < K ? s_sv[lane] : 0.f, K, sigmoid_mode, scale);
@@ -738,17 +767,26 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         const uint32_t k = wave + GU_WAVES * n;
         wk[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)(k < K ? k : 0u)));
     }
-    float xv[CPL][32], xs0[CPL], xs1[CPL];
+    float xv[HX ? 1 : CPL][HX ? 1 : 32], xs0[CPL], xs1[CPL];
+    uint32_t xh[HX ? CPL : 1][16], xl[HX ? CPL : 1][16];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        load_x_ilv(s_x4, j, lane, xv[j]);
-        xs0[j] = xs1[j] = 0.f;
+        if constexpr (HX) {
+            load_xh_ilv(s_x4, j, lane, xh[j], xl[j]);
+        } else {
+            load_x_ilv(s_x4, j, lane, xv[j]);
+            xs0[j] = xs1[j] = 0.f;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            xs0[j] += xv[j][q];
-            xs1[j] += xv[j][16 + q];
+            for (int q = 0; q < 16; ++q) {
+                xs0[j] += xv[j][q];
+                xs1[j] += xv[j][16 + q];
+            }
         }
     }
+    auto dotc = [&](const typename Fm::Raw& r, int j, uint32_t c) -> float {
+        if constexpr (HX) return Fm::dot_raw_h(r, xh[j], xl[j]);
+        else return Fm::dot_raw(r, c, xv[j], xs0[j], xs1[j]);
+    };
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
         const uint32_t k = wave + GU_WAVES * n;
@@ -761,8 +799,8 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                 for (int j = 0; j < CPL; ++j) {
                     if (lane + 64u * j >= nch) continue;
                     const uint32_t c = lane + 64u * j;
-                    gs[i] += Fm::dot_raw(rg[n][i][j], c, xv[j], xs0[j], xs1[j]);
-                    us[i] += Fm::dot_raw(ru[n][i][j], c, xv[j], xs0[j], xs1[j]);
+                    gs[i] += dotc(rg[n][i][j], j, c);
+                    us[i] += dotc(ru[n][i][j], j, c);
                 }
             }
 #pragma unroll
@@ -801,11 +839,16 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
                                                            const float* __restrict__ res, float* __restrict__ out) {
     using Fd = Fmt<KD>;
     using Fs = Fmt<(KS < 0 ? KD : KS)>;
+    constexpr bool HD = half_x<KD>(), HS = KS >= 0 && half_x<(KS < 0 ? KD : KS)>();  // f16-pair inputs
     __shared__ float4 s_act4[DOWN_LDS_FLOATS / 4];
     __shared__ float s_sum[DOWN_LDS_FLOATS / 16];
     // Codebooks: decoded only after the barrier that follows the activation staging.
-    stage_codebooks<KD>();
-    if constexpr (KS >= 0) stage_codebooks<(KS < 0 ? KD : KS)>();
+    if constexpr (HD) stage_half_tables<KD>();
+    else stage_codebooks<KD>();
+    if constexpr (KS >= 0 && KS != KD) {
+        if constexpr (HS) stage_half_tables<(KS < 0 ? KD : KS)>();
+        else stage_codebooks<(KS < 0 ? KD : KS)>();
+    }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const uint32_t t = blockIdx.y;
     const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
@@ -883,7 +926,8 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
             a.z *= gate;
             a.w *= gate;
         }
-        if (v < nv) s_act4[ilv_slot(v, u & 7u)] = a;
+        const bool half = v < KC ? HD : HS;
+        if (v < nv) s_act4[ilv_slot(v, u & 7u)] = half ? split_h4(a) : a;
         float g = (a.x + a.y) + (a.z + a.w);
         g = dpp_add<0xb1>(g);  // quad_perm [1,0,3,2]
         g = dpp_add<0x4e>(g);  // quad_perm [2,3,0,1]
@@ -897,14 +941,29 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         if (!has[j]) continue;
-        float xv[32];
-        load_x_ilv(s_act4, j, lane, xv);
-        const float2 xs = reinterpret_cast<const float2*>(s_sum)[lane + 64u * j];
-        const float xs0 = xs.x, xs1 = xs.y;
+        if ((HD && !isS[j]) || (HS && isS[j])) {
+            uint32_t xh[16], xl[16];
+            load_xh_ilv(s_act4, j, lane, xh, xl);
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-            if (!UNI && isS[j]) acc[i] += Fs::dot_raw(rs[UNI ? 0 : i][UNI ? 0 : j], cc[j], xv, xs0, xs1);
-            else acc[i] += Fd::dot_raw(rd[i][j], cc[j], xv, xs0, xs1);
+            for (int i = 0; i < RPW; ++i) {
+                if constexpr (HS && !UNI) {
+                    if (isS[j]) {
+                        acc[i] += Fs::dot_raw_h(rs[UNI ? 0 : i][UNI ? 0 : j], xh, xl);
+                        continue;
+                    }
+                }
+                if constexpr (HD) acc[i] += Fd::dot_raw_h(rd[i][j], xh, xl);
+            }
+        } else {
+            float xv[32];
+            load_x_ilv(s_act4, j, lane, xv);
+            const float2 xs = reinterpret_cast<const float2*>(s_sum)[lane + 64u * j];
+            const float xs0 = xs.x, xs1 = xs.y;
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) {
+                if (!UNI && isS[j]) acc[i] += Fs::dot_raw(rs[UNI ? 0 : i][UNI ? 0 : j], cc[j], xv, xs0, xs1);
+                else acc[i] += Fd::dot_raw(rd[i][j], cc[j], xv, xs0, xs1);
+            }
         }
     }
 #pragma unroll
