@@ -1076,23 +1076,30 @@ __global__ __launch_bounds__(256) void k_gemv_shared_down_add(const uint8_t* __r
 
 // ------------------------------------------------------- prefill: dispatch
 // Block-wide exclusive scan of one value per thread (blockDim 1024 = 16 waves).
+// Inclusive prefix sum over a wave by DPP: row_shr 1, 2, 4, 8 within each
+// 16-lane row, then row_bcast 15 (rows 1, 3) and row_bcast 31 (rows 2, 3)
+// carry the row totals. The whole wave must be active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_add_u32(uint32_t v) {
+    return v + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, true);
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    v = dpp_add_u32<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_add_u32<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_add_u32<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_add_u32<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_add_u32<0x142, 0xa>(v);  // row_bcast:15
+    v = dpp_add_u32<0x143, 0xc>(v);  // row_bcast:31
+    return v;
+}
+
 __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum, uint32_t* total) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    uint32_t inc = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        uint32_t o = __shfl_up(inc, d);
-        if (lane >= (uint32_t)d) inc += o;
-    }
+    const uint32_t inc = wave_incl_scan(v);
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
     if (wave == 0) {
-        uint32_t s = lane < 16 ? wsum[lane] : 0u, si = s;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-            uint32_t o = __shfl_up(si, d);
-            if (lane >= (uint32_t)d) si += o;
-        }
+        const uint32_t s = lane < 16 ? wsum[lane] : 0u, si = wave_incl_scan(s);
         if (lane < 16) wsum[16 + lane] = si - s;
         if (lane == 15) *total = si;
     }
