@@ -1151,10 +1151,14 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
     rbin[tid] = 0;
     __syncthreads();
     const uint32_t seg = (P + 15u) / 16u, s0 = min(P, wave * seg), s1 = min(P, s0 + seg);
+    // The first batch of ids stays in registers for the placement pass.
+    uint32_t xv0[DSP_BATCH];
+#pragma unroll
+    for (int i = 0; i < (int)DSP_BATCH; ++i) xv0[i] = P ? ids[min(s0 + 64u * i + lane, P - 1u)] : 0u;
     for (uint32_t b0 = s0; b0 < s1; b0 += 64u * DSP_BATCH) {
         uint32_t xv[DSP_BATCH];
 #pragma unroll
-        for (int i = 0; i < (int)DSP_BATCH; ++i) xv[i] = ids[min(b0 + 64u * i + lane, P - 1u)];
+        for (int i = 0; i < (int)DSP_BATCH; ++i) xv[i] = b0 == s0 ? xv0[i] : ids[min(b0 + 64u * i + lane, P - 1u)];
 #pragma unroll
         for (int i = 0; i < (int)DSP_BATCH; ++i)
             if (b0 + 64u * i + lane < s1) atomicAdd(&hist[wave][xv[i]], 1u);
@@ -1235,7 +1239,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
     for (uint32_t b0 = s0; b0 < s1; b0 += 64u * DSP_BATCH) {
         uint32_t xv[DSP_BATCH];
 #pragma unroll
-        for (int i = 0; i < (int)DSP_BATCH; ++i) xv[i] = ids[min(b0 + 64u * i + lane, P - 1u)];
+        for (int i = 0; i < (int)DSP_BATCH; ++i) xv[i] = b0 == s0 ? xv0[i] : ids[min(b0 + 64u * i + lane, P - 1u)];
 #pragma unroll
         for (int i = 0; i < (int)DSP_BATCH; ++i) {
             const uint32_t base = b0 + 64u * i;
