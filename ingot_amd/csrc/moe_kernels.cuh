@@ -861,6 +861,10 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     // branch-free too.
     constexpr bool UNI = KS < 0 || KS == KD;
     const uint32_t KC = K * nchF;  // routed chunks
+    // The residual of this lane's output row (lane i < RPW writes row r0 + i),
+    // loaded first so that its latency overlaps the others'.
+    float resv = 0.f;
+    if (res) resv = res[(uint64_t)t * H + min(r0 + min(lane, (uint32_t)RPW - 1u), H - 1u)];
     // 1. expert ids of this lane's chunks of the virtual row (chunk v: pair
     //    v / nchF; the quotient by multiply-high, exact for v < 2^32 / nchF)
     const uint32_t mag = 0xffffffffu / nchF + 1u;
@@ -971,7 +975,7 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
         float sum = wave_sum_dpp(acc[i]);
         const uint32_t r = r0 + i;
         if (lane == (uint32_t)i && r < H) {
-            if (res) sum += res[(uint64_t)t * H + r];
+            if (res) sum += resv;
             out[(uint64_t)t * H + r] = sum;
         }
     }
