@@ -162,13 +162,14 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
 #undef RT
         return true;
     }
-    const uint32_t epw = decode ? 1u : 8u;
-    const uint32_t gy = (rows + 4 * epw - 1) / (4 * epw);
+    // Decode: one router row per one-wave block (every row on its own CU).
+    const uint32_t epw = decode ? 1u : 8u, wpb = decode ? 1u : 4u;
+    const uint32_t gy = (rows + wpb * epw - 1) / (wpb * epw);
 #define ROUTER(TOK, HBV)                                                                                       \
     do {                                                                                                       \
         dim3 grid((T + TOK - 1) / TOK, gy);                                                                    \
-        hipLaunchKernelGGL((k_router<TOK, HBV>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, epw,     \
-                           logits, sgl, xn);                                                                   \
+        hipLaunchKernelGGL((k_router<TOK, HBV>), grid, dim3(64 * wpb), 0, s, x, W, sgvec, gain, eps, T, E,    \
+                           epw, logits, sgl, xn);                                                              \
         return true;                                                                                           \
     } while (0)
     if (HB == 8) {

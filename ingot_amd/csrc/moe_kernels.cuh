@@ -351,6 +351,20 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
     constexpr uint32_t H = 256u * HB;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t0 = blockIdx.x * TOK;
+    // Decode (one token per block): the wave's first router row is loaded
+    // before the input, independent of it, so the two loads (and the optional
+    // RMSNorm) overlap.
+    const uint32_t rows = E + (sgvec ? 1u : 0u);
+    const uint32_t e0 = (blockIdx.y * (blockDim.x >> 6) + wave) * epw;
+    float wv0[TOK == 1 ? HB * 4 : 1];
+    if constexpr (TOK == 1) {
+        const float* wr = e0 < E ? W + (uint64_t)e0 * H : (e0 < rows ? sgvec : W);
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(wr + 4u * lane + 256u * i);
+            wv0[4 * i] = v.x; wv0[4 * i + 1] = v.y; wv0[4 * i + 2] = v.z; wv0[4 * i + 3] = v.w;
+        }
+    }
     float xr[TOK][HB * 4];
 #pragma unroll
     for (int t = 0; t < TOK; ++t) {
@@ -390,8 +404,6 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
             }
         }
     }
-    const uint32_t rows = E + (sgvec ? 1u : 0u);
-    const uint32_t e0 = (blockIdx.y * 4u + wave) * epw;
     for (uint32_t k = 0; k < epw; ++k) {
         uint32_t e = e0 + k;
         if (e >= rows) break;
@@ -399,8 +411,15 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
         float wv[HB * 4];
 #pragma unroll
         for (int i = 0; i < HB; ++i) {
-            float4 v = *reinterpret_cast<const float4*>(wr + 4u * lane + 256u * i);
-            wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
+            if (TOK == 1 && k == 0) {
+                wv[4 * i] = wv0[TOK == 1 ? 4 * i : 0];
+                wv[4 * i + 1] = wv0[TOK == 1 ? 4 * i + 1 : 0];
+                wv[4 * i + 2] = wv0[TOK == 1 ? 4 * i + 2 : 0];
+                wv[4 * i + 3] = wv0[TOK == 1 ? 4 * i + 3 : 0];
+            } else {
+                float4 v = *reinterpret_cast<const float4*>(wr + 4u * lane + 256u * i);
+                wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
+            }
         }
 #pragma unroll
         for (int t = 0; t < TOK; ++t) {
