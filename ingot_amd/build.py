@@ -2,16 +2,19 @@
 
     python -m ingot_amd.build            # HIP backend + synth library + CPU oracle
 
-* ingot_amd/libingot_moe.so   hipcc --offload-arch=gfx950 (kernels + C ABI)
+* ingot_amd/libingot_moe.so   hipcc --offload-arch=gfx950 (kernels + C ABI; the
+                              csrc/*.hip units compiled in parallel, then linked)
 * ingot_amd/libingot_synth.so g++ (synthetic inputs, quantizers)
 * oracle/liboracle.so         make -C oracle (CPU oracle, test infrastructure)
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -48,9 +51,26 @@ def build_synth(verbose: bool = False) -> str:
     return out
 
 
-def build_hip(verbose: bool = False) -> str:
+def hip_sources() -> list[str]:
+    """moe_hip.hip (C ABI, format-independent kernels) and the kinds_*.hip
+    units, each of which instantiates the kernels of a few GGUF formats."""
+    kinds = sorted(f for f in os.listdir(CSRC) if f.startswith("kinds_") and f.endswith(".hip"))
+    return [os.path.join(CSRC, "moe_hip.hip")] + [os.path.join(CSRC, f) for f in kinds]
+
+
+def build_hip(verbose: bool = False, jobs: int = 0) -> str:
+    """Compiles every unit to an object in parallel, then links libingot_moe.so."""
     out = os.path.join(HERE, "libingot_moe.so")
-    _run([HIPCC, *HIP_FLAGS, "-o", _atomic(out), os.path.join(CSRC, "moe_hip.hip")], verbose)
+    srcs = hip_sources()
+    jobs = jobs or min(len(srcs), int(os.environ.get("MAX_JOBS", "0")) or os.cpu_count() or 1)
+    flags = [f for f in HIP_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="ingot_build_") as tmp:
+        objs = [os.path.join(tmp, os.path.basename(f)[:-4] + ".o") for f in srcs]
+        cmds = [[HIPCC, *flags, "-c", "-o", o, f] for f, o in zip(srcs, objs)]
+        with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", _atomic(out), *objs], verbose)
     os.replace(_atomic(out), out)
     return out
 

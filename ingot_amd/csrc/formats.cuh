@@ -4,18 +4,20 @@
 //   chunk c of a row covers 32 columns chosen by the format so that one chunk
 //   is one natural unit of its block layout (a 32-value group of a 256-value
 //   superblock, or one 32-value block):
-//     Q4_K    superblock c/8, quarter q=(c%8)/2, half h=c%2: 16 bytes of
+//     Q4_K, Q5_K  superblock c/8, quarter q=(c%8)/2, half h=c%2: 16 bytes of
 //             nibbles holding columns 64q+16h+[0,16) (low nibbles, group 2q)
 //             and 64q+32+16h+[0,16) (high nibbles, group 2q+1)
-//     IQ2_XS  superblock c/8, group c%8: columns 32*(c%8)+[0,32)
-//     IQ3_XXS superblock c/8, group c%8: columns 32*(c%8)+[0,32)
-//     Q8_0, Q4_0, IQ4_NL, F32, F16: block / columns 32c+[0,32)
+//     other 256-value superblocks (Q2_K, Q6_K, IQ2_XXS, IQ2_XS, IQ2_S,
+//             IQ3_XXS, IQ3_S, IQ4_XS, IQ1_M): superblock c/8, group c%8:
+//             columns 32*(c%8)+[0,32)
+//     Q2_0    half c%2 of 64-value block c/2
+//     Q8_0, Q4_0, IQ4_NL, F32, F16, BF16: block / columns 32c+[0,32)
 //   Chunks 2s and 2s+1 together always cover the 64 columns [64s, 64s+64):
 //   the GEMM kernels stage weights in 64-column slabs built from two chunks.
 //
 // The formulas are the reference's (kernels/iq3_mix.metal:13-36 for Q4_K,
-// IQ2_XS and IQ3_XXS; kernels/moe.metal:14-17, :76-80 for F32, F16, Q4_0, Q8_0
-// and IQ4_NL), organised for 16-byte loads and factored scales: a chunk dot
+// Q5_K, IQ2_XS and IQ3_XXS; kernels/moe.metal:13-89 for F32, F16, Q4_0, Q8_0,
+// Q2_K, Q6_K, IQ2_XXS, IQ1_M, BF16, Q2_0, IQ2_S, IQ3_S, IQ4_NL and IQ4_XS), organised for 16-byte loads and factored scales: a chunk dot
 // product is sum_i w_i x_i with w_i = scale * small_int_i - min, evaluated as
 // scale * sum_i small_int_i x_i - min * sum_i x_i.
 #pragma once
@@ -149,7 +151,7 @@ struct Fmt<12> {
 // Formats whose chunk c covers columns 32c..32c+31 in order.
 // Codebooks in LDS. A lookup with a per-lane index into __constant__ memory
 // is a vector memory access chained after the weight load that supplies the
-// index, so every kernel that decodes IQ2_XS, IQ3_XXS or IQ4_NL copies the
+// index, so every kernel that decodes an IQ format copies the
 // codebook into LDS first: stage_codebooks<KIND>() at kernel start, followed
 // by a barrier before the first decode.
 __device__ inline uint64_t* lds_iq2xs_grid() {
@@ -164,19 +166,44 @@ __device__ inline float* lds_iq4nl_values() {
     __shared__ float v[16];
     return v;
 }
+__device__ inline uint64_t* lds_iq2xxs_grid() {
+    __shared__ uint64_t g[256];
+    return g;
+}
+__device__ inline uint64_t* lds_iq2s_grid() {
+    __shared__ uint64_t g[1024];
+    return g;
+}
+__device__ inline uint32_t* lds_iq3s_grid() {
+    __shared__ uint32_t g[512];
+    return g;
+}
+__device__ inline uint64_t* lds_iq1s_grid() {
+    __shared__ uint64_t g[2048];
+    return g;
+}
 template <int KIND>
 __device__ inline void stage_codebooks() {
     if constexpr (KIND == 17) {
         for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq2xs_grid()[i] = ingot_iq2xs_grid[i];
     } else if constexpr (KIND == 18) {
         for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_iq3xxs_grid()[i] = ingot_iq3xxs_grid[i];
-    } else if constexpr (KIND == 20) {
+    } else if constexpr (KIND == 20 || KIND == 23) {
         if (threadIdx.x < 16u) lds_iq4nl_values()[threadIdx.x] = (float)ingot_kvalues_iq4nl[threadIdx.x];
+    } else if constexpr (KIND == 16) {
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_iq2xxs_grid()[i] = ingot_iq2xxs_grid[i];
+    } else if constexpr (KIND == 22) {
+        for (uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) lds_iq2s_grid()[i] = ingot_iq2s_grid[i];
+    } else if constexpr (KIND == 21) {
+        for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq3s_grid()[i] = ingot_iq3s_grid[i];
+    } else if constexpr (KIND == 29) {
+        for (uint32_t i = threadIdx.x; i < 2048u; i += blockDim.x) lds_iq1s_grid()[i] = ingot_iq1s_grid[i];
     }
 }
 template <int KIND>
 constexpr bool has_codebook() {
-    return KIND == 17 || KIND == 18 || KIND == 20;
+    return KIND == 16 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 21 || KIND == 22 || KIND == 23 ||
+           KIND == 29;
 }
 
 // Tables of the f16 grouped GEMM, whose B operands are integers held as f16
@@ -514,6 +541,566 @@ struct Fmt<18> : Contig {
     }
 };
 
+// ------------------------------------------------------ F16 (1), BF16 (30)
+// Two bytes per value; chunk c is bytes 64c..64c+63 of the row.
+template <bool BF>
+struct Half16 : Contig {
+    static constexpr uint32_t BLOCK = 1, BYTES = 2;
+    struct Raw {
+        uint4 v[4];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        Raw r;
+        const uint4* p = reinterpret_cast<const uint4*>(row + 64u * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+        return r;
+    }
+    // Value 2j + h of the 32-bit word w.
+    __device__ static float val(uint32_t w, int h) {
+        if constexpr (BF) return __uint_as_float(h ? (w & 0xffff0000u) : (w << 16));
+        else return half_bits_to_float(h ? (w >> 16) : w);
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[8 * i + 2 * j] = val(q[j], 0);
+                w[8 * i + 2 * j + 1] = val(q[j], 1);
+            }
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t q[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s = __builtin_fmaf(val(q[j], 0), xv[8 * i + 2 * j], s);
+                s = __builtin_fmaf(val(q[j], 1), xv[8 * i + 2 * j + 1], s);
+            }
+        }
+        return s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+template <>
+struct Fmt<1> : Half16<false> {};
+template <>
+struct Fmt<30> : Half16<true> {};
+
+// -------------------------------------------------------------- Q2_0 (42)
+// 18-byte blocks of 64 values (2-byte aligned): fp16 d @0, 16 bytes of 2-bit
+// codes @2, value k in bits 2(k%4) of byte k/4. w = d * (code - 1).
+// Chunk c is half c%2 of block c/2.
+template <>
+struct Fmt<42> : Contig {
+    static constexpr uint32_t BLOCK = 64, BYTES = 18;
+    struct Raw {
+        uint32_t d;
+        uint32_t q[2];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 1) * BYTES;
+        Raw r;
+        r.d = ld_u16(b);
+        r.q[0] = ld_u32_a2(b + 2 + 8 * (c & 1u));
+        r.q[1] = ld_u32_a2(b + 6 + 8 * (c & 1u));
+        return r;
+    }
+    __device__ static float code(const Raw& r, int i) { return (float)((r.q[i >> 4] >> (2 * (i & 15))) & 3u); }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        const float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) w[i] = d * (code(r, i) - 1.0f);
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float xs0, float xs1) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s = __builtin_fmaf(code(r, i), xv[i], s);
+        return half_bits_to_float(r.d) * (s - (xs0 + xs1));
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// --------------------------------------------------------------- Q2_K (10)
+// 84-byte superblocks: 16 scale bytes @0 (scale low nibble, min high nibble,
+// per 16 values), 64 bytes of 2-bit quants @16, fp16 d @80 and dmin @82.
+// Value k: quant bits 2((k%128)/32) of byte 16 + 32(k/128) + k%32.
+// w = d * (sc & 15) * q - dmin * (sc >> 4). Chunk c: group g = c%8 of
+// superblock c/8, i.e. bytes 16 + 32(g/4) .. +32 at shift 2(g%4).
+template <>
+struct Fmt<10> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 84;
+    struct Raw {
+        uint32_t dd, sc;
+        uint32_t q[8];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t g = c & 7u;
+        Raw r;
+        r.dd = ld_u32_a2(b + 80);
+        r.sc = ld_u16(b + 2 * g);
+        const uint8_t* q = b + 16 + 32 * (g >> 2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.q[i] = ld_u32_a2(q + 4 * i);
+        return r;
+    }
+    __device__ static uint32_t qword(const Raw& r, uint32_t c, int i) { return (r.q[i] >> (2 * (c & 3u))) & 0x03030303u; }
+    __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
+        const float d = half_bits_to_float(r.dd), dm = half_bits_to_float(r.dd >> 16);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t sc = (r.sc >> (8 * h)) & 255u;
+            const float ds = d * (float)(sc & 15u), m = dm * (float)(sc >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = qword(r, c, 4 * h + i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[16 * h + 4 * i + j] = ds * ubyte_f(q, j) - m;
+            }
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float xs0, float xs1) {
+        float s[2] = {0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = qword(r, c, 4 * h + i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[h] = __builtin_fmaf(ubyte_f(q, j), xv[16 * h + 4 * i + j], s[h]);
+            }
+        const float d = half_bits_to_float(r.dd), dm = half_bits_to_float(r.dd >> 16);
+        const uint32_t s0 = r.sc & 255u, s1 = (r.sc >> 8) & 255u;
+        return d * ((float)(s0 & 15u) * s[0] + (float)(s1 & 15u) * s[1]) -
+               dm * ((float)(s0 >> 4) * xs0 + (float)(s1 >> 4) * xs1);
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// --------------------------------------------------------------- Q5_K (13)
+// 176-byte superblocks: Q4_K's 16-byte header {d, dmin, scales[12]} @0, 32
+// bytes of fifth bits @16 (bit g of byte k%32 for value k of group g), 128
+// bytes of nibbles @48 laid out as Q4_K's. Chunks follow Q4_K's (16 nibble
+// bytes, both nibbles), so the fifth bits are bits 2qq and 2qq+1 of the 16
+// bytes @16 + 16h. w = d*sc*q - dmin*m, q = nibble | bit << 4.
+template <>
+struct Fmt<13> : Fmt<12> {
+    static constexpr uint32_t BYTES = 176;
+    struct Raw {
+        uint4 a, b, h;
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t q = c & 7u;
+        Raw r;
+        r.a = *reinterpret_cast<const uint4*>(b);
+        r.b = *reinterpret_cast<const uint4*>(b + 48 + 32 * (q >> 1) + 16 * (q & 1u));
+        r.h = *reinterpret_cast<const uint4*>(b + 16 + 16 * (q & 1u));
+        return r;
+    }
+    // Bytes 4k..4k+3 of the low (h = 0) or high (h = 1) group as 5-bit values.
+    __device__ static uint32_t q5(const Raw& r, uint32_t c, int k, int h) {
+        const uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w}, hb[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+        const uint32_t bit = 2u * ((c & 7u) >> 1) + (uint32_t)h;
+        return ((w[k] >> (4 * h)) & 0x0f0f0f0fu) | (((hb[k] >> bit) & 0x01010101u) << 4);
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
+        float d0, m0, d1, m1;
+        scales(r.a, c, d0, m0, d1, m1);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = q5(r, c, k, 0), hi = q5(r, c, k, 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[4 * k + j] = d0 * ubyte_f(lo, j) - m0;
+                w[16 + 4 * k + j] = d1 * ubyte_f(hi, j) - m1;
+            }
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float xs0, float xs1) {
+        float d0, m0, d1, m1;
+        scales(r.a, c, d0, m0, d1, m1);
+        float slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = q5(r, c, k, 0), hi = q5(r, c, k, 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                slo = __builtin_fmaf(ubyte_f(lo, j), xv[4 * k + j], slo);
+                shi = __builtin_fmaf(ubyte_f(hi, j), xv[16 + 4 * k + j], shi);
+            }
+        }
+        return d0 * slo + d1 * shi - (m0 * xs0 + m1 * xs1);
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float xs0, float xs1) {
+        return dot_raw(load_raw(row, c), c, xv, xs0, xs1);
+    }
+};
+
+// --------------------------------------------------------------- Q6_K (14)
+// 210-byte superblocks (2-byte aligned): 128 bytes of low nibbles @0, 64
+// bytes of high 2-bit pairs @128, 16 int8 scales @192 (per 16 values), fp16
+// d @208. Value k (n = k/128, l = k%32, t = (k%128)/32): low nibble
+// (t >= 2: high half) of byte 64n + 32(t%2) + l, high bits 2t of byte
+// 128 + 32n + l, scale 192 + 8n + 2t + l/16. w = d * scale * (q - 32).
+template <>
+struct Fmt<14> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 210;
+    struct Raw {
+        uint32_t d, sc;
+        uint32_t ql[8], qh[8];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t g = c & 7u, n = g >> 2, t = g & 3u;
+        Raw r;
+        r.d = ld_u16(b + 208);
+        r.sc = ld_u16(b + 192 + 8 * n + 2 * t);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            r.ql[i] = ld_u32_a2(b + 64 * n + 32 * (t & 1u) + 4 * i);
+            r.qh[i] = ld_u32_a2(b + 128 + 32 * n + 4 * i);
+        }
+        return r;
+    }
+    __device__ static uint32_t q6(const Raw& r, uint32_t c, int i) {
+        const uint32_t t = c & 3u;
+        return ((r.ql[i] >> (t >= 2u ? 4 : 0)) & 0x0f0f0f0fu) | (((r.qh[i] >> (2 * t)) & 0x03030303u) << 4);
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
+        const float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float ds = d * (float)(int8_t)((r.sc >> (8 * h)) & 255u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = q6(r, c, 4 * h + i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[16 * h + 4 * i + j] = ds * (ubyte_f(q, j) - 32.0f);
+            }
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float xs0, float xs1) {
+        float s[2] = {0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = q6(r, c, 4 * h + i);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[h] = __builtin_fmaf(ubyte_f(q, j), xv[16 * h + 4 * i + j], s[h]);
+            }
+        const float sc0 = (float)(int8_t)(r.sc & 255u), sc1 = (float)(int8_t)((r.sc >> 8) & 255u);
+        return half_bits_to_float(r.d) *
+               (sc0 * __builtin_fmaf(-32.0f, xs0, s[0]) + sc1 * __builtin_fmaf(-32.0f, xs1, s[1]));
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// ------------------------------------------------------------ IQ2_XXS (16)
+// 66-byte superblocks (2-byte aligned): fp16 d @0, then per group of 32
+// values 8 bytes @2 + 8g: four 8-value grid indices and a u32 holding four
+// 7-bit sign indices (bits 7l) and a 4-bit scale (bits 28..31).
+// w = d * (0.5 + s) * 0.25 * grid * sign.
+template <>
+struct Fmt<16> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 66;
+    struct Raw {
+        uint32_t d, idx, aux;
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* a = row + (c >> 3) * BYTES + 2 + 8 * (c & 7u);
+        Raw r;
+        r.d = ld_u16(a - 2 - 8 * (c & 7u));
+        r.idx = ld_u32_a2(a);
+        r.aux = ld_u32_a2(a + 4);
+        return r;
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        const float db = half_bits_to_float(r.d) * (0.5f + (float)(r.aux >> 28)) * 0.25f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint64_t grid = lds_iq2xxs_grid()[byte_of(r.idx, l)];
+            const uint32_t sg = ingot_ksign((r.aux >> (7 * l)) & 127u);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) w[8 * l + v] = flip_sign(db * (float)((grid >> (8 * v)) & 255u), (sg >> v) & 1u);
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint64_t grid = lds_iq2xxs_grid()[byte_of(r.idx, l)];
+            const uint32_t sg = ingot_ksign((r.aux >> (7 * l)) & 127u);
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                s = __builtin_fmaf((float)((grid >> (8 * v)) & 255u), flip_sign(xv[8 * l + v], (sg >> v) & 1u), s);
+        }
+        return half_bits_to_float(r.d) * (0.5f + (float)(r.aux >> 28)) * 0.25f * s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// -------------------------------------------------------------- IQ2_S (22)
+// 82-byte superblocks (2-byte aligned): fp16 d @0, grid index low bytes @2
+// (4 per group), sign bytes @34 (4 per group, one bit per value), index high
+// bits @66 (one byte per group, 2 bits per 8 values), scales @74 (one byte
+// per group, 4 bits per 16 values). w = d * (0.5 + s) * 0.25 * grid * sign.
+template <>
+struct Fmt<22> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 82;
+    struct Raw {
+        uint32_t d, idx, sgn, hs;  // hs: high-bits byte | scale byte << 8
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t g = c & 7u;
+        Raw r;
+        r.d = ld_u16(b);
+        r.idx = ld_u32_a2(b + 2 + 4 * g);
+        r.sgn = ld_u32_a2(b + 34 + 4 * g);
+        r.hs = (uint32_t)b[66 + g] | ((uint32_t)b[74 + g] << 8);
+        return r;
+    }
+    __device__ static uint64_t grid(const Raw& r, int l) {
+        return lds_iq2s_grid()[byte_of(r.idx, l) | (((r.hs & 255u) << (8 - 2 * l)) & 0x300u)];
+    }
+    __device__ static float scale(const Raw& r, int l) { return 0.5f + (float)((r.hs >> (8 + 4 * (l / 2))) & 15u); }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        const float d = half_bits_to_float(r.d);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const float db = d * scale(r, l) * 0.25f;
+            const uint64_t gr = grid(r, l);
+            const uint32_t sg = byte_of(r.sgn, l);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) w[8 * l + v] = flip_sign(db * (float)((gr >> (8 * v)) & 255u), (sg >> v) & 1u);
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint64_t gr = grid(r, l);
+            const uint32_t sg = byte_of(r.sgn, l);
+            float t = 0.f;
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                t = __builtin_fmaf((float)((gr >> (8 * v)) & 255u), flip_sign(xv[8 * l + v], (sg >> v) & 1u), t);
+            s = __builtin_fmaf(scale(r, l), t, s);
+        }
+        return half_bits_to_float(r.d) * 0.25f * s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// -------------------------------------------------------------- IQ3_S (21)
+// 110-byte superblocks (2-byte aligned): fp16 d @0, 64 grid index low bytes
+// @2 (8 per group, 4 values each), index ninth bits @66 (one byte per group),
+// sign bytes @74 (4 per group), scales @106 (4 bits per group).
+// w = d * (1 + 2s) * grid * sign.
+template <>
+struct Fmt<21> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 110;
+    struct Raw {
+        uint32_t d, q0, q1, sgn, hs;  // hs: ninth-bits byte | scale << 8
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t g = c & 7u;
+        Raw r;
+        r.d = ld_u16(b);
+        r.q0 = ld_u32_a2(b + 2 + 8 * g);
+        r.q1 = ld_u32_a2(b + 6 + 8 * g);
+        r.sgn = ld_u32_a2(b + 74 + 4 * g);
+        r.hs = (uint32_t)b[66 + g] | ((((uint32_t)b[106 + g / 2] >> (4 * (g & 1u))) & 15u) << 8);
+        return r;
+    }
+    // Grid entry j (0..7) of the group: 4 values.
+    __device__ static uint32_t grid(const Raw& r, int j) {
+        const uint32_t lo = byte_of(j < 4 ? r.q0 : r.q1, j & 3);
+        return lds_iq3s_grid()[lo | (((r.hs & 255u) << (8 - j)) & 256u)];
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
+        const float db = half_bits_to_float(r.d) * (float)(1u + 2u * (r.hs >> 8));
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t sg = byte_of(r.sgn, l);
+#pragma unroll
+            for (int hg = 0; hg < 2; ++hg) {
+                const uint32_t gr = grid(r, 2 * l + hg);
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    w[8 * l + 4 * hg + v] = flip_sign(db * ubyte_f(gr, v), (sg >> (4 * hg + v)) & 1u);
+            }
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t, const float* xv, float, float) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t sg = byte_of(r.sgn, l);
+#pragma unroll
+            for (int hg = 0; hg < 2; ++hg) {
+                const uint32_t gr = grid(r, 2 * l + hg);
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    s = __builtin_fmaf(ubyte_f(gr, v), flip_sign(xv[8 * l + 4 * hg + v], (sg >> (4 * hg + v)) & 1u), s);
+            }
+        }
+        return half_bits_to_float(r.d) * (float)(1u + 2u * (r.hs >> 8)) * s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// ------------------------------------------------------------- IQ4_XS (23)
+// 136-byte superblocks (8-byte aligned): fp16 d @0, u16 of 2-bit scale high
+// parts @2, 4 bytes of 4-bit scale low parts @4, 128 nibble bytes @8 (16 per
+// group: values 0-15 low nibbles, 16-31 high nibbles, as IQ4_NL).
+// w = d * (scale - 32) * kvalues_iq4nl[q].
+template <>
+struct Fmt<23> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 136;
+    struct Raw {
+        uint32_t h0, h1;  // d | scales_h << 16, scales_l
+        uint32_t q[4];
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t g = c & 7u;
+        const uint2 h = *reinterpret_cast<const uint2*>(b);
+        const uint2 q0 = *reinterpret_cast<const uint2*>(b + 8 + 16 * g);
+        const uint2 q1 = *reinterpret_cast<const uint2*>(b + 16 + 16 * g);
+        Raw r;
+        r.h0 = h.x;
+        r.h1 = h.y;
+        r.q[0] = q0.x; r.q[1] = q0.y; r.q[2] = q1.x; r.q[3] = q1.y;
+        return r;
+    }
+    __device__ static float scale(const Raw& r, uint32_t c) {
+        const uint32_t g = c & 7u;
+        const uint32_t lo = (byte_of(r.h1, g >> 1) >> (4 * (g & 1u))) & 15u, hi = ((r.h0 >> 16) >> (2 * g)) & 3u;
+        return (float)((int)(lo | (hi << 4)) - 32);
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
+        const float ds = half_bits_to_float(r.h0) * scale(r, c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t byte = byte_of(r.q[i], j);
+                w[4 * i + j] = ds * lds_iq4nl_values()[byte & 15u];
+                w[16 + 4 * i + j] = ds * lds_iq4nl_values()[byte >> 4];
+            }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float, float) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t byte = byte_of(r.q[i], j);
+                s = __builtin_fmaf(lds_iq4nl_values()[byte & 15u], xv[4 * i + j], s);
+                s = __builtin_fmaf(lds_iq4nl_values()[byte >> 4], xv[16 + 4 * i + j], s);
+            }
+        return half_bits_to_float(r.h0) * scale(r, c) * s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
+// -------------------------------------------------------------- IQ1_M (29)
+// 56-byte superblocks (8-byte aligned): 32 grid index low bytes @0 (4 per
+// group), 16 bytes @32 (per 8 values: 3 index high bits and a delta sign
+// bit, two per byte), four u16 @48 holding 3-bit scales (per 16 values) and,
+// in their top nibbles, the fp16 d. w = d * (2s + 1) * (grid + delta),
+// grid in {-1, 0, 1}, delta = -1/8 when the bit is set, else +1/8.
+template <>
+struct Fmt<29> : Contig {
+    static constexpr uint32_t BLOCK = 256, BYTES = 56;
+    struct Raw {
+        uint32_t qs, qh, sc0, sc1;
+    };
+    __device__ static Raw load_raw(const uint8_t* row, uint32_t c) {
+        const uint8_t* b = row + (c >> 3) * BYTES;
+        const uint32_t g = c & 7u;
+        const uint2 s = *reinterpret_cast<const uint2*>(b + 48);
+        Raw r;
+        r.qs = *reinterpret_cast<const uint32_t*>(b + 4 * g);
+        r.qh = ld_u16(b + 32 + 2 * g);
+        r.sc0 = s.x;
+        r.sc1 = s.y;
+        return r;
+    }
+    __device__ static float d(const Raw& r) {
+        const uint32_t bits = ((r.sc0 >> 12) & 0xfu) | ((r.sc0 >> 24) & 0xf0u) | ((r.sc1 >> 4) & 0xf00u) |
+                              ((r.sc1 >> 16) & 0xf000u);
+        return half_bits_to_float(bits);
+    }
+    // Scale factor 2s + 1 of sub-block l (0..3) of chunk c.
+    __device__ static float scale(const Raw& r, uint32_t c, int l) {
+        const uint32_t g = c & 7u;
+        const uint32_t w = ((g >> 1) < 2u ? r.sc0 : r.sc1) >> (16 * ((g >> 1) & 1u));
+        return (float)(2u * ((w >> (6 * (g & 1u) + 3 * (l / 2))) & 7u) + 1u);
+    }
+    __device__ static uint64_t grid(const Raw& r, int l, float& delta) {
+        const uint32_t hb = (r.qh >> (8 * (l / 2) + 4 * (l % 2))) & 15u;
+        delta = (hb & 8u) ? -0.125f : 0.125f;
+        return lds_iq1s_grid()[byte_of(r.qs, l) | ((hb & 7u) << 8)];
+    }
+    __device__ static void dequant_raw(const Raw& r, uint32_t c, float* w) {
+        const float dd = d(r);
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            float delta;
+            const uint64_t gr = grid(r, l, delta);
+            const float ds = dd * scale(r, c, l);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) w[8 * l + v] = ds * ((float)(int8_t)((gr >> (8 * v)) & 255u) + delta);
+        }
+    }
+    __device__ static float dot_raw(const Raw& r, uint32_t c, const float* xv, float, float) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            float delta;
+            const uint64_t gr = grid(r, l, delta);
+            float t = 0.f, sx = 0.f;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                t = __builtin_fmaf((float)(int8_t)((gr >> (8 * v)) & 255u), xv[8 * l + v], t);
+                sx += xv[8 * l + v];
+            }
+            s = __builtin_fmaf(scale(r, c, l), __builtin_fmaf(delta, sx, t), s);
+        }
+        return d(r) * s;
+    }
+    __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
+        return dot_raw(load_raw(row, c), c, xv, a, b);
+    }
+};
+
 // Scalar decode of weight j of a row, any supported kind (slow path for the
 // generic projection / dequant drop-ins).
 __device__ inline float dequant_value(const uint8_t* row, uint32_t kind, uint32_t j) {
@@ -564,6 +1151,88 @@ __device__ inline float dequant_value(const uint8_t* row, uint32_t kind, uint32_
             float grid = (float)((ingot_iq3xxs_grid[b[2 + 8 * g + 2 * l + v / 4]] >> (8 * (v % 4))) & 255);
             float db = half_bits_to_float(ld_u16(b)) * (0.5f + (float)(aux >> 28)) * 0.5f;
             return flip_sign(db * grid, (ingot_ksign((aux >> (7 * l)) & 127) >> v) & 1u);
+        }
+        case 30: return __uint_as_float((uint32_t)ld_u16(row + 2 * j) << 16);
+        case 13: {
+            const uint8_t* b = row + (j / 256) * 176;
+            uint32_t k = j % 256, g = k / 32, sc, m;
+            const uint8_t* s = b + 4;
+            if (g < 4) {
+                sc = s[g] & 63;
+                m = s[g + 4] & 63;
+            } else {
+                sc = (s[g + 4] & 15) | ((s[g - 4] >> 6) << 4);
+                m = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+            }
+            uint32_t q = ((b[48 + 32 * (k / 64) + k % 32] >> (4 * (g % 2))) & 15) | (((b[16 + k % 32] >> g) & 1u) << 4);
+            float d1 = half_bits_to_float(ld_u16(b)) * (float)sc, m1 = half_bits_to_float(ld_u16(b + 2)) * (float)m;
+            return d1 * (float)q - m1;
+        }
+        case 10: {
+            const uint8_t* b = row + (j / 256) * 84;
+            uint32_t k = j % 256, sc = b[k / 16];
+            uint32_t q = (b[16 + (k / 128) * 32 + k % 32] >> (2 * ((k % 128) / 32))) & 3;
+            return half_bits_to_float(ld_u16(b + 80)) * (float)(sc & 15) * (float)q -
+                   half_bits_to_float(ld_u16(b + 82)) * (float)(sc >> 4);
+        }
+        case 14: {
+            const uint8_t* b = row + (j / 256) * 210;
+            uint32_t k = j % 256, n = k / 128, l = k % 32, t = (k % 128) / 32;
+            uint32_t low = (b[n * 64 + l + (t % 2) * 32] >> (t >= 2 ? 4 : 0)) & 15;
+            uint32_t high = (b[128 + n * 32 + l] >> (2 * t)) & 3;
+            return half_bits_to_float(ld_u16(b + 208)) * (float)(int8_t)b[192 + n * 8 + l / 16 + 2 * t] *
+                   (float)((int)(low | (high << 4)) - 32);
+        }
+        case 16: {
+            const uint8_t* b = row + (j / 256) * 66;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            const uint8_t* a = b + 2 + g * 8;
+            uint32_t aux = ld_u32_a2(a + 4);
+            float grid = (float)((ingot_iq2xxs_grid[a[l]] >> (8 * v)) & 255);
+            float db = half_bits_to_float(ld_u16(b)) * (0.5f + (float)(aux >> 28)) * 0.25f;
+            return flip_sign(db * grid, (ingot_ksign((aux >> (7 * l)) & 127) >> v) & 1u);
+        }
+        case 29: {
+            const uint8_t* b = row + (j / 256) * 56;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            uint32_t sc[4];
+            for (int i = 0; i < 4; ++i) sc[i] = ld_u16(b + 48 + 2 * i);
+            uint32_t bits = (sc[0] >> 12) | ((sc[1] >> 8) & 240) | ((sc[2] >> 4) & 3840) | (sc[3] & 61440);
+            uint32_t high = b[32 + g * 2 + l / 2];
+            uint32_t index = b[g * 4 + l] | (((high >> (4 * (l % 2))) & 7) << 8);
+            float delta = (high & (8u << (4 * (l % 2)))) ? -0.125f : 0.125f;
+            float grid = (float)(int8_t)((ingot_iq1s_grid[index] >> (8 * v)) & 255);
+            uint32_t scale = (sc[g / 2] >> (6 * (g % 2) + 3 * (l / 2))) & 7;
+            return half_bits_to_float(bits) * (float)(2 * scale + 1) * (grid + delta);
+        }
+        case 42: {
+            const uint8_t* b = row + (j / 64) * 18;
+            uint32_t k = j % 64;
+            return half_bits_to_float(ld_u16(b)) * (float)((int)((b[2 + k / 4] >> (2 * (k % 4))) & 3) - 1);
+        }
+        case 22: {
+            const uint8_t* b = row + (j / 256) * 82;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            uint32_t index = b[2 + 4 * g + l] | (((uint32_t)b[66 + g] << (8 - 2 * l)) & 0x300);
+            float grid = (float)((ingot_iq2s_grid[index] >> (8 * v)) & 255);
+            float db = half_bits_to_float(ld_u16(b)) * (0.5f + (float)((b[74 + g] >> (4 * (l / 2))) & 15)) * 0.25f;
+            return flip_sign(db * grid, (b[34 + 4 * g + l] >> v) & 1u);
+        }
+        case 21: {
+            const uint8_t* b = row + (j / 256) * 110;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8, hg = v / 4;
+            uint32_t index = b[2 + g * 8 + 2 * l + hg] | (((uint32_t)b[66 + g] << (8 - 2 * l - hg)) & 256);
+            float grid = (float)((ingot_iq3s_grid[index] >> (8 * (v % 4))) & 255);
+            float db = half_bits_to_float(ld_u16(b)) * (float)(1 + 2 * ((b[106 + g / 2] >> (4 * (g % 2))) & 15));
+            return flip_sign(db * grid, (b[74 + g * 4 + l] >> v) & 1u);
+        }
+        case 23: {
+            const uint8_t* b = row + (j / 256) * 136;
+            uint32_t k = j % 256, g = k / 32, v = k % 32;
+            uint32_t high = ld_u16(b + 2);
+            int scale = (int)(((b[4 + g / 2] >> (4 * (g % 2))) & 15) | (((high >> (2 * g)) & 3) << 4)) - 32;
+            uint32_t q = (b[8 + g * 16 + v % 16] >> (4 * (v / 16))) & 15;
+            return half_bits_to_float(ld_u16(b)) * (float)scale * (float)ingot_kvalues_iq4nl[q];
         }
         default: return __builtin_nanf("");
     }

@@ -1,0 +1,107 @@
+// Definitions of the per-format launchers declared in kind_launch.h. Included
+// only by the kinds_*.hip translation units, each of which instantiates the
+// formats it owns with INGOT_INSTANTIATE_KIND / INGOT_INSTANTIATE_FUSED.
+#pragma once
+#include "kind_launch.h"
+#define INGOT_KIND_UNIT  // leave out the format-independent kernels
+#include "moe_kernels.cuh"
+
+namespace ingot {
+
+template <int KIND>
+bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, dim3 grid, const GateUpArgs& a) {
+#define GU(C)                                                                                                 \
+    hipLaunchKernelGGL((k_gemv_gate_up<KIND, C, GEMV_RPW>), grid, dim3(256), 0, s, a.g, a.u, a.gs, a.us, a.F, \
+                       a.H, a.x, a.ids, a.K, a.limit, a.act)
+    if (cpl == 1) { GU(1); return true; }
+    if (cpl == 2) { GU(2); return true; }
+#undef GU
+    return false;
+}
+
+template <int KS>
+bool launch_shared_add_k(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H,
+                         uint32_t SF, const float* sact, const float* sgl, float* out) {
+    if (cpl == 1) {
+        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 1>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
+        return true;
+    }
+    if (cpl == 2) {
+        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 2>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
+        return true;
+    }
+    return false;
+}
+
+template <int KIND, bool GATEUP>
+bool launch_gemm_k(hipStream_t s, dim3 grid, const GemmArgs& a) {
+    hipLaunchKernelGGL((k_gemm<KIND, GATEUP>), grid, dim3(256), 0, s, a.w0, a.w1, a.s0, a.s1, a.rows, a.kdim, a.a,
+                       a.pairs, a.K, a.tiles, a.ldo, a.limit, a.out);
+    return true;
+}
+
+template <int KIND, int NE>
+static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid,
+                            const DecGateUpArgs& a) {
+#define DGU(C, N, R)                                                                                          \
+    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F, \
+                       a.H, a.x, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags, a.act)
+    if (rpw == 3) {
+        if (cpl == 1 && np == 1) { DGU(1, 1, 3); return true; }
+        return false;
+    }
+    if (cpl == 1 && np == 1) { DGU(1, 1, 2); return true; }
+    if (cpl == 1 && np == 2) { DGU(1, 2, 2); return true; }
+    if (cpl == 2 && np == 1) { DGU(2, 1, 2); return true; }
+    if (cpl == 2 && np == 2) { DGU(2, 2, 2); return true; }
+#undef DGU
+    return false;
+}
+
+// Candidates per lane of the routing (E <= 64 NE): 2 up to 128 experts, 8 for
+// the IQ2_XS 512-expert shape, 16 otherwise (one instantiation per count
+// keeps each kernel's code small).
+template <int KIND>
+bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid, const DecGateUpArgs& a) {
+    if (a.E <= 128) return dec_gate_up_cpl<KIND, 2>(s, cpl, np, rpw, grid, a);
+    if constexpr (KIND == 17)
+        if (a.E <= 512 && cpl == 1 && np == 2 && rpw == 2) {
+            hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F,
+                               a.H, a.x, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags,
+                               a.act);
+            return true;
+        }
+    return dec_gate_up_cpl<KIND, 16>(s, cpl, np, rpw, grid, a);
+}
+
+template <int KD, int KS>
+bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
+#define DD(V)                                                                                                      \
+    case V:                                                                                                        \
+        hipLaunchKernelGGL((k_dec_down<KD, KS, V, DEC_RPW>), grid, dim3(DOWN_THREADS), 0, s, a.down, a.dstride,    \
+                           a.sdown, a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.sgl, a.K, a.res, a.out);   \
+        return true;
+    switch (vpl) {
+        DD(1) DD(2) DD(3) DD(4) DD(5) DD(6)  // K F + SF <= DOWN_LDS_FLOATS: at most 384 chunks
+        default: return false;
+    }
+#undef DD
+}
+
+}  // namespace ingot
+
+#define INGOT_INSTANTIATE_KIND(K)                                                                                \
+    namespace ingot {                                                                                            \
+    template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, dim3, const GateUpArgs&);                      \
+    template bool launch_shared_add_k<K>(hipStream_t, uint32_t, dim3, const uint8_t*, uint64_t, uint32_t,        \
+                                         uint32_t, const float*, const float*, float*);                          \
+    template bool launch_gemm_k<K, true>(hipStream_t, dim3, const GemmArgs&);                                    \
+    template bool launch_gemm_k<K, false>(hipStream_t, dim3, const GemmArgs&);                                   \
+    template bool launch_dec_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, uint32_t, dim3, const DecGateUpArgs&); \
+    template bool launch_dec_down_k<K, -1>(hipStream_t, uint32_t, dim3, const DownArgs&);                        \
+    }
+
+#define INGOT_INSTANTIATE_FUSED(KD, KS) \
+    namespace ingot {                   \
+    template bool launch_dec_down_k<KD, KS>(hipStream_t, uint32_t, dim3, const DownArgs&); \
+    }

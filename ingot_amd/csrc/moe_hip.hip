@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "../../include/ingot_moe.h"
+#include "kind_launch.h"
 #include "moe_kernels.cuh"
 
 using namespace ingot;
@@ -96,7 +97,13 @@ int geometry(uint32_t kind, uint32_t* block, uint32_t* bytes) {
 }
 
 bool supported(uint32_t kind) {
-    return kind == 0 || kind == 1 || kind == 2 || kind == 8 || kind == 12 || kind == 17 || kind == 18 || kind == 20;
+    switch (kind) {
+#define K_(KV) case KV:
+        INGOT_KINDS(K_)
+#undef K_
+        return true;
+        default: return false;
+    }
 }
 
 // src/metal.rs:1602-1621.
@@ -188,8 +195,6 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
     return false;
 }
 
-constexpr int GEMV_RPW = 4;
-
 // Top-K routing, keys per lane NE = E/64 rounded up to a power of two.
 void launch_route(hipStream_t s, const float* logits, const float* bias, uint32_t T, uint32_t E, uint32_t K,
                   uint32_t mode, float scale, uint32_t* ids, float* w, uint32_t* flags) {
@@ -204,63 +209,18 @@ void launch_route(hipStream_t s, const float* logits, const float* bias, uint32_
 #undef ROUTE
 }
 
-template <int KIND>
-bool gate_up_cpl(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* g, const uint8_t* u, uint64_t gs, uint64_t us,
-                 uint32_t F, uint32_t H, const float* x, const uint32_t* ids, uint32_t K, float limit, float* act) {
-    if (cpl == 1) {
-        hipLaunchKernelGGL((k_gemv_gate_up<KIND, 1, GEMV_RPW>), grid, dim3(256), 0, s, g, u, gs, us, F, H, x, ids, K,
-                           limit, act);
-        return true;
-    }
-    if (cpl == 2) {
-        hipLaunchKernelGGL((k_gemv_gate_up<KIND, 2, GEMV_RPW>), grid, dim3(256), 0, s, g, u, gs, us, F, H, x, ids, K,
-                           limit, act);
-        return true;
-    }
-    return false;
-}
-
 bool launch_gemv_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const uint8_t* u, uint64_t gs, uint64_t us,
                          uint32_t F, uint32_t H, uint32_t pairs, const float* x, const uint32_t* ids, uint32_t K,
                          float limit, float* act) {
     const uint32_t cpl = (H / 32 + 63) / 64;
     dim3 grid((F + 4 * GEMV_RPW - 1) / (4 * GEMV_RPW), pairs);
+    const GateUpArgs a{g, u, gs, us, F, H, x, ids, K, limit, act};
     switch (kind) {
-        case 0: return gate_up_cpl<0>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
-        case 2: return gate_up_cpl<2>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
-        case 8: return gate_up_cpl<8>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
-        case 12: return gate_up_cpl<12>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
-        case 17: return gate_up_cpl<17>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
-        case 18: return gate_up_cpl<18>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
-        case 20: return gate_up_cpl<20>(s, cpl, grid, g, u, gs, us, F, H, x, ids, K, limit, act);
+#define K_(KV) case KV: return launch_gemv_gate_up_k<KV>(s, cpl, grid, a);
+        INGOT_KINDS(K_)
+#undef K_
         default: return false;
     }
-}
-
-struct DownArgs {
-    const uint8_t *down, *sdown;
-    uint64_t dstride, sdstride;
-    uint32_t H, F, SF;
-    const float *act, *sact;
-    const uint32_t* ids;
-    const float* sgl;
-    uint32_t K;
-    const float* res;
-    float* out;
-};
-
-template <int KS>
-bool shared_add_cpl(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H, uint32_t SF,
-                    const float* sact, const float* sgl, float* out) {
-    if (cpl == 1) {
-        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 1>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
-        return true;
-    }
-    if (cpl == 2) {
-        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 2>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
-        return true;
-    }
-    return false;
 }
 
 bool launch_shared_down_add(hipStream_t s, uint32_t ks, const uint8_t* sd, uint64_t sds, uint32_t H, uint32_t SF,
@@ -268,13 +228,9 @@ bool launch_shared_down_add(hipStream_t s, uint32_t ks, const uint8_t* sd, uint6
     const uint32_t cpl = (SF / 32 + 63) / 64;
     dim3 grid((H + 3) / 4, T);
     switch (ks) {
-        case 0: return shared_add_cpl<0>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
-        case 2: return shared_add_cpl<2>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
-        case 8: return shared_add_cpl<8>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
-        case 12: return shared_add_cpl<12>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
-        case 17: return shared_add_cpl<17>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
-        case 18: return shared_add_cpl<18>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
-        case 20: return shared_add_cpl<20>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+#define K_(KV) case KV: return launch_shared_add_k<KV>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+        INGOT_KINDS(K_)
+#undef K_
         default: return false;
     }
 }
@@ -283,22 +239,13 @@ template <bool GATEUP>
 bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, const uint8_t* w1, uint64_t s0,
                  uint64_t s1, uint32_t rows, uint32_t kdim, const float* a, const uint32_t* pairs, uint32_t K,
                  const uint32_t* tiles, uint32_t ldo, float limit, float* out) {
-#define GEMM(KV)                                                                                                 \
-    case KV:                                                                                                     \
-        hipLaunchKernelGGL((k_gemm<KV, GATEUP>), grid, dim3(256), 0, s, w0, w1, s0, s1, rows, kdim, a, pairs, K, \
-                           tiles, ldo, limit, out);                                                              \
-        return true;
+    const GemmArgs g{w0, w1, s0, s1, rows, kdim, a, pairs, K, tiles, ldo, limit, out};
     switch (kind) {
-        GEMM(0)
-        GEMM(2)
-        GEMM(8)
-        GEMM(12)
-        GEMM(17)
-        GEMM(18)
-        GEMM(20)
+#define K_(KV) case KV: return launch_gemm_k<KV, GATEUP>(s, grid, g);
+        INGOT_KINDS(K_)
+#undef K_
         default: return false;
     }
-#undef GEMM
 }
 
 // Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K;
@@ -348,50 +295,6 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
 
 }  // namespace
 
-// Decode gate/up (k_dec_gate_up2): 2 or 3 rows x every pair per 8-wave block.
-constexpr int DEC_RPW = 1;  // down rows per wave
-
-template <int KIND, int NE>
-static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid, const uint8_t* g,
-                            const uint8_t* u, uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x,
-                            const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale,
-                            float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
-#define DGU(C, N, R)                                                                                              \
-    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x,        \
-                       logits, bias, E, K, mode, scale, limit, ids, w, flags, act)
-    if (rpw == 3) {
-        if (cpl == 1 && np == 1) { DGU(1, 1, 3); return true; }
-        return false;
-    }
-    if (cpl == 1 && np == 1) { DGU(1, 1, 2); return true; }
-    if (cpl == 1 && np == 2) { DGU(1, 2, 2); return true; }
-    if (cpl == 2 && np == 1) { DGU(2, 1, 2); return true; }
-    if (cpl == 2 && np == 2) { DGU(2, 2, 2); return true; }
-#undef DGU
-    return false;
-}
-
-// Candidates per lane of the routing (E <= 64 NE): 2 up to 128 experts, 8 for
-// the IQ2_XS 512-expert shape, 16 otherwise (one instantiation per count
-// keeps each kernel's code small).
-template <int KIND>
-static bool dec_gate_up_ne(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid, const uint8_t* g,
-                           const uint8_t* u, uint64_t gs, uint64_t us, uint32_t F, uint32_t H, const float* x,
-                           const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale,
-                           float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
-    if (E <= 128)
-        return dec_gate_up_cpl<KIND, 2>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale,
-                                        limit, ids, w, flags, act);
-    if constexpr (KIND == 17)
-        if (E <= 512 && cpl == 1 && np == 2 && rpw == 2) {
-            hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, g, u, gs, us, F, H, x, logits,
-                               bias, E, K, mode, scale, limit, ids, w, flags, act);
-            return true;
-        }
-    return dec_gate_up_cpl<KIND, 16>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale,
-                                     limit, ids, w, flags, act);
-}
-
 // Rows per wave: 3 when that spreads the blocks more evenly over the 256 CUs
 // (F = 768 at one token: 256 blocks of 3 rows instead of 384 of 2, half of
 // the CUs running two), else 2.
@@ -408,33 +311,23 @@ static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, c
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     dim3 grid((F + rpw - 1) / rpw, T);
+    const DecGateUpArgs a{g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act};
     switch (kind) {
-#define K_(KV) case KV: return dec_gate_up_ne<KV>(s, cpl, np, rpw, grid, g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act);
-        K_(0) K_(2) K_(8) K_(12) K_(17) K_(18) K_(20)
+#define K_(KV) case KV: return launch_dec_gate_up_k<KV>(s, cpl, np, rpw, grid, a);
+        INGOT_KINDS(K_)
 #undef K_
         default: return false;
     }
-}
-
-template <int KD, int KS>
-static bool dec_down_vpl(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
-#define DD(V)                                                                                                      \
-    case V:                                                                                                        \
-        hipLaunchKernelGGL((k_dec_down<KD, KS, V, DEC_RPW>), grid, dim3(DOWN_THREADS), 0, s, a.down, a.dstride,    \
-                           a.sdown, a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.sgl, a.K, a.res, a.out);   \
-        return true;
-    switch (vpl) {
-        DD(1) DD(2) DD(3) DD(4) DD(5) DD(6)  // K F + SF <= DOWN_LDS_FLOATS: at most 384 chunks
-        default: return false;
-    }
-#undef DD
 }
 
 // Decode down + combine: routed-only for every kind, plus a fused shared expert
 // for the format pairs the configurations use (can_fuse_shared). Returns false
 // if no instantiation covers the shape.
 static bool can_fuse_shared(uint32_t kd, int ks) {
-    return (kd == 17 && ks == 8) || (kd == 12 && ks == 12) || (kd == 20 && ks == 20) || (kd == 8 && ks == 8);
+#define F_(KD, KS) if (kd == KD && ks == KS) return true;
+    INGOT_FUSED_DOWN(F_)
+#undef F_
+    return false;
 }
 
 static bool gemv_down(hipStream_t s, uint32_t kd, int ks, const DownArgs& a, uint32_t T) {
@@ -443,20 +336,15 @@ static bool gemv_down(hipStream_t s, uint32_t kd, int ks, const DownArgs& a, uin
     dim3 grid((a.H + DOWN_WAVES * DEC_RPW - 1) / (DOWN_WAVES * DEC_RPW), T);
     if (ks < 0) {
         switch (kd) {
-            case 0: return dec_down_vpl<0, -1>(s, vpl, grid, a);
-            case 2: return dec_down_vpl<2, -1>(s, vpl, grid, a);
-            case 8: return dec_down_vpl<8, -1>(s, vpl, grid, a);
-            case 12: return dec_down_vpl<12, -1>(s, vpl, grid, a);
-            case 17: return dec_down_vpl<17, -1>(s, vpl, grid, a);
-            case 18: return dec_down_vpl<18, -1>(s, vpl, grid, a);
-            case 20: return dec_down_vpl<20, -1>(s, vpl, grid, a);
+#define K_(KV) case KV: return launch_dec_down_k<KV, -1>(s, vpl, grid, a);
+            INGOT_KINDS(K_)
+#undef K_
             default: return false;
         }
     }
-    if (kd == 17 && ks == 8) return dec_down_vpl<17, 8>(s, vpl, grid, a);
-    if (kd == 12 && ks == 12) return dec_down_vpl<12, 12>(s, vpl, grid, a);
-    if (kd == 20 && ks == 20) return dec_down_vpl<20, 20>(s, vpl, grid, a);
-    if (kd == 8 && ks == 8) return dec_down_vpl<8, 8>(s, vpl, grid, a);
+#define F_(KD, KS) if (kd == KD && ks == KS) return launch_dec_down_k<KD, KS>(s, vpl, grid, a);
+    INGOT_FUSED_DOWN(F_)
+#undef F_
     return false;
 }
 
@@ -847,10 +735,10 @@ int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* d, ingot_layer** 
     if (d->gate.kind != d->up.kind || (has_shared && d->shared_gate.kind != d->shared_up.kind))
         return fail(ctx, INGOT_UNSUPPORTED, "gate and up must share a format");
     for (const ingot_matrix* m : {&d->gate, &d->down})
-        if (!supported(m->kind) || m->kind == 1) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+        if (!supported(m->kind)) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
     if (has_shared)
         for (const ingot_matrix* m : {&d->shared_gate, &d->shared_down})
-            if (!supported(m->kind) || m->kind == 1) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+            if (!supported(m->kind)) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
 
     ingot_layer* L = new ingot_layer();
     L->ctx = ctx;

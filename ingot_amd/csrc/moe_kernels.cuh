@@ -1153,6 +1153,7 @@ constexpr uint32_t DSP_BATCH = 8;
 __device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
                                       _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g);
 
+#ifndef INGOT_KIND_UNIT  // compiled in moe_hip.hip only
 __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
                                                    uint32_t TM, uint32_t cap, uint32_t* __restrict__ counts,
                                                    uint32_t* __restrict__ first, uint32_t* __restrict__ tiles,
@@ -1287,6 +1288,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
         }
     }
 }
+#endif  // INGOT_KIND_UNIT
 
 // ---------------------------------------------------- prefill: grouped GEMM
 // One block (256 threads, 4 waves) per (row tile, token tile). A token tile
@@ -2093,6 +2095,7 @@ __device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _
     if (live && (threadIdx.x & 7u) == 0) xs[i / 32u] = s;
 }
 
+#ifndef INGOT_KIND_UNIT  // format-independent kernels: compiled in moe_hip.hip only
 // Plain grid-stride copy of n16 16-byte words (counter calibration workload).
 __global__ __launch_bounds__(256) void k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
@@ -2190,4 +2193,5 @@ __global__ void k_check_finite(const float* __restrict__ v, uint64_t n, uint32_t
     if (__any(bad) && (threadIdx.x & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
 }
 
+#endif  // INGOT_KIND_UNIT
 }  // namespace ingot

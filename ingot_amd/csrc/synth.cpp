@@ -394,6 +394,78 @@ bool quant_row(uint32_t kind, const float* x, uint64_t cols, uint8_t* out) {
     }
 }
 
+// Formats without a quantizer here get random valid blocks: every quant,
+// index, sign and sub-scale byte uniformly random, the fp16 block scales set
+// so that weights come out about `sigma` in size (times a per-block factor in
+// [0.5, 1.5)). F16 and BF16 rows hold N(0, sigma) values. Parity tests only
+// need both sides to decode the same bytes; uniform bytes reach every
+// codebook entry, sign pattern and scale.
+struct RandomLayout {
+    uint32_t block, bytes;
+    uint32_t d_at, dmin_at;  // byte offsets of the fp16 scales (dmin_at == bytes: none)
+    float d_div, dmin_div;   // d = sigma / d_div
+};
+
+bool random_layout(uint32_t kind, RandomLayout* L) {
+    switch (kind) {
+        case 10: *L = {256, 84, 80, 82, 8.f, 16.f}; return true;       // Q2_K
+        case 13: *L = {256, 176, 0, 2, 400.f, 800.f}; return true;     // Q5_K
+        case 14: *L = {256, 210, 208, 210, 1000.f, 1.f}; return true;  // Q6_K
+        case 16: *L = {256, 66, 0, 66, 50.f, 1.f}; return true;        // IQ2_XXS
+        case 21: *L = {256, 110, 0, 110, 128.f, 1.f}; return true;     // IQ3_S
+        case 22: *L = {256, 82, 0, 82, 50.f, 1.f}; return true;        // IQ2_S
+        case 23: *L = {256, 136, 0, 136, 1000.f, 1.f}; return true;    // IQ4_XS
+        case 29: *L = {256, 56, 56, 56, 8.f, 1.f}; return true;        // IQ1_M (d in the scale words' top nibbles)
+        case 42: *L = {64, 18, 0, 18, 1.f, 1.f}; return true;          // Q2_0
+        default: return false;
+    }
+}
+
+bool random_row(uint32_t kind, uint64_t key, uint64_t r, uint64_t cols, float sigma, uint8_t* out) {
+    SplitMix64 g{ingot_synth_stream(key, r, 1, kind)};
+    if (kind == 1 || kind == 30) {
+        std::vector<float> v(cols);
+        normal_row(key, r, cols, 0.0f, sigma, v.data());
+        for (uint64_t j = 0; j < cols; ++j) {
+            uint16_t h;
+            if (kind == 1) {
+                h = f2h(v[j]);
+            } else {
+                float f = v[j];
+                ingot_round_bf16(&f, 1);
+                uint32_t u;
+                std::memcpy(&u, &f, 4);
+                h = (uint16_t)(u >> 16);
+            }
+            put16(out + 2 * j, h);
+        }
+        return true;
+    }
+    RandomLayout L;
+    if (!random_layout(kind, &L) || cols % L.block) return false;
+    const uint64_t nb = cols / L.block;
+    for (uint64_t i = 0; i < nb * L.bytes; i += 8) {
+        uint64_t v = g.next();
+        for (uint64_t b = 0; b < 8 && i + b < nb * L.bytes; ++b) out[i + b] = (uint8_t)(v >> (8 * b));
+    }
+    for (uint64_t i = 0; i < nb; ++i) {
+        uint8_t* b = out + i * L.bytes;
+        const float jit = (float)(0.5 + g.unit());
+        const uint16_t d = f2h(sigma / L.d_div * jit);
+        if (kind == 29) {
+            for (int w = 0; w < 4; ++w) {
+                uint16_t sc = (uint16_t)(b[48 + 2 * w] | (b[49 + 2 * w] << 8));
+                sc = (uint16_t)((sc & 0x0fffu) | (((d >> (4 * w)) & 15u) << 12));
+                put16(b + 48 + 2 * w, sc);
+            }
+            continue;
+        }
+        put16(b + L.d_at, d);
+        if (L.dmin_at < L.bytes) put16(b + L.dmin_at, f2h(sigma / L.dmin_div * jit));
+    }
+    return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -438,7 +510,12 @@ uint64_t ingot_quant_row_bytes(uint32_t kind, uint64_t cols) {
         case 12: return cols % 256 ? 0 : cols / 256 * 144;
         case 17: return cols % 256 ? 0 : cols / 256 * 74;
         case 18: return cols % 256 ? 0 : cols / 256 * 98;
-        default: return 0;
+        case 1: case 30: return 2 * cols;
+        default: {
+            RandomLayout L;
+            if (!random_layout(kind, &L) || cols % L.block) return 0;
+            return cols / L.block * L.bytes;
+        }
     }
 }
 
@@ -460,6 +537,7 @@ int ingot_synth_quantized(uint32_t kind, uint64_t key, uint64_t count, uint64_t 
     parallel_for(items, threads, [&](uint64_t it) {
         std::vector<float> buf(cols);
         for (uint64_t r = it * chunk; r < std::min(total, (it + 1) * chunk); ++r) {
+            if (random_row(kind, key, r, cols, sigma, dst + r * stride)) continue;
             normal_row(key, r, cols, 0.0f, sigma, buf.data());
             quant_row(kind, buf.data(), cols, dst + r * stride);
         }

@@ -30,6 +30,7 @@ ROUTE_SOFTMAX, ROUTE_SIGMOID = 0, 1
 
 # GGML type ids (src/gguf.rs:470-491)
 F32, F16, Q4_0, Q8_0, Q4_K, IQ2_XS, IQ3_XXS, IQ4_NL = 0, 1, 2, 8, 12, 17, 18, 20
+Q2_K, Q5_K, Q6_K, IQ2_XXS, IQ3_S, IQ2_S, IQ4_XS, IQ1_M, BF16, Q2_0 = 10, 13, 14, 16, 21, 22, 23, 29, 30, 42
 
 # Prefill GEMM arithmetic (ingot_layer_set_gemm_mode)
 GEMM_AUTO, GEMM_FP32 = 0, 1

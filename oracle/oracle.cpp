@@ -102,9 +102,11 @@ int oracle_validate_matrix(const oracle_matrix* m) {
     return ORACLE_OK;
 }
 
-// One weight of a row. Formulas: kernels/moe.metal:13-89 (F32 :14, F16 :15,
-// Q4_0 :16, Q8_0 :17, IQ4_NL :76-80, BF16 :62-65) and kernels/iq3_mix.metal:17-36
-// (Q4_K :19-23, IQ2_XS :25-30, IQ3_XXS :31-35). Each value is evaluated in
+// One weight of a row. Formulas: kernels/moe.metal:13-89 (F32 :13, F16 :14,
+// Q4_0 :15, Q8_0 :16, Q2_K :17-21, Q6_K :22-28, IQ2_XXS :29-36, IQ1_M :37-46,
+// BF16 :47-50, Q2_0 :51-55, IQ2_S :56-64, IQ3_S :65-75, IQ4_NL :76-80,
+// IQ4_XS :81-89) and kernels/iq3_mix.metal:17-36 (Q4_K and Q5_K :19-23,
+// IQ2_XS :25-30, IQ3_XXS :31-35). Each value is evaluated in
 // float as the ggml dequantize_row_* routines do (scale product first).
 float oracle_dequant_value(const uint8_t* row, uint32_t kind, uint64_t j) {
     switch (kind) {
@@ -157,6 +159,83 @@ float oracle_dequant_value(const uint8_t* row, uint32_t kind, uint64_t j) {
             float sign = (ingot_ksign((aux >> (7 * l)) & 127) & (1u << v)) ? -1.0f : 1.0f;
             float db = hf(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
             return db * grid * sign;
+        }
+        case 13: {  // Q5_K, kernels/iq3_mix.metal:19-23: Q4_K's nibble plus bit g of qh[k % 32] as 16
+            const uint8_t* b = row + (j / 256) * 176;
+            uint32_t k = j % 256, g = k / 32, sc, mn;
+            scale_min_k4(b + 4, g, &sc, &mn);
+            uint32_t q = (b[48 + 32 * (k / 64) + k % 32] >> (4 * (g % 2))) & 15;
+            q |= ((b[16 + k % 32] >> g) & 1u) << 4;
+            float d1 = hf(b) * (float)sc;
+            float m1 = hf(b + 2) * (float)mn;
+            return d1 * (float)q - m1;
+        }
+        case 10: {  // Q2_K, kernels/moe.metal:17-21
+            const uint8_t* b = row + (j / 256) * 84;
+            uint32_t k = j % 256, sc = b[k / 16];
+            uint32_t q = (b[16 + (k / 128) * 32 + k % 32] >> (2 * ((k % 128) / 32))) & 3;
+            return hf(b + 80) * (float)(sc & 15) * (float)q - hf(b + 82) * (float)(sc >> 4);
+        }
+        case 14: {  // Q6_K, kernels/moe.metal:22-28
+            const uint8_t* b = row + (j / 256) * 210;
+            uint32_t k = j % 256, n = k / 128, l = k % 32, t = (k % 128) / 32;
+            uint32_t low = (b[n * 64 + l + (t % 2) * 32] >> (t >= 2 ? 4 : 0)) & 15;
+            uint32_t high = (b[128 + n * 32 + l] >> (2 * t)) & 3;
+            int scale = (int8_t)b[192 + n * 8 + l / 16 + 2 * t];
+            return hf(b + 208) * (float)scale * (float)((int)(low | (high << 4)) - 32);
+        }
+        case 16: {  // IQ2_XXS, kernels/moe.metal:29-36
+            const uint8_t* b = row + (j / 256) * 66;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            const uint8_t* a = b + 2 + g * 8;
+            uint32_t packed = rd32(a + 4);
+            float grid = (float)((ingot_iq2xxs_grid[a[l]] >> (8 * v)) & 255);
+            float sign = (ingot_ksign((packed >> (7 * l)) & 127) & (1u << v)) ? -1.0f : 1.0f;
+            return hf(b) * (0.5f + (float)(packed >> 28)) * 0.25f * grid * sign;
+        }
+        case 29: {  // IQ1_M, kernels/moe.metal:37-46
+            const uint8_t* b = row + (j / 256) * 56;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            uint32_t sc[4];
+            for (int i = 0; i < 4; ++i) sc[i] = rd16(b + 48 + 2 * i);
+            uint32_t bits = (sc[0] >> 12) | ((sc[1] >> 8) & 240) | ((sc[2] >> 4) & 3840) | (sc[3] & 61440);
+            uint32_t high = b[32 + g * 2 + l / 2];
+            uint32_t index = b[g * 4 + l] | (((high >> (4 * (l % 2))) & 7) << 8);
+            float delta = (high & (8u << (4 * (l % 2)))) ? -0.125f : 0.125f;
+            float grid = (float)(int8_t)((ingot_iq1s_grid[index] >> (8 * v)) & 255);
+            uint32_t scale = (sc[g / 2] >> (6 * (g % 2) + 3 * (l / 2))) & 7;
+            return half_to_float((uint16_t)bits) * (float)(2 * scale + 1) * (grid + delta);
+        }
+        case 42: {  // Q2_0, kernels/moe.metal:51-55: consecutive 2-bit codes, 64 per block
+            const uint8_t* b = row + (j / 64) * 18;
+            uint32_t k = j % 64;
+            return hf(b) * (float)((int)((b[2 + k / 4] >> (2 * (k % 4))) & 3) - 1);
+        }
+        case 22: {  // IQ2_S, kernels/moe.metal:56-64
+            const uint8_t* b = row + (j / 256) * 82;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8;
+            uint32_t index = b[2 + 4 * g + l] | (((uint32_t)b[66 + g] << (8 - 2 * l)) & 0x300);
+            float grid = (float)((ingot_iq2s_grid[index] >> (8 * v)) & 255);
+            uint32_t scale = (b[74 + g] >> (4 * (l / 2))) & 15;
+            float sign = (b[34 + 4 * g + l] & (1u << v)) ? -1.0f : 1.0f;
+            return hf(b) * (0.5f + (float)scale) * 0.25f * grid * sign;
+        }
+        case 21: {  // IQ3_S, kernels/moe.metal:65-75
+            const uint8_t* b = row + (j / 256) * 110;
+            uint32_t k = j % 256, g = k / 32, l = (k % 32) / 8, v = k % 8, hg = v / 4;
+            uint32_t index = b[2 + g * 8 + 2 * l + hg] | (((uint32_t)b[66 + g] << (8 - 2 * l - hg)) & 256);
+            float grid = (float)((ingot_iq3s_grid[index] >> (8 * (v % 4))) & 255);
+            uint32_t scale = (b[106 + g / 2] >> (4 * (g % 2))) & 15;
+            float sign = (b[74 + g * 4 + l] & (1u << v)) ? -1.0f : 1.0f;
+            return hf(b) * (float)(1 + 2 * scale) * grid * sign;
+        }
+        case 23: {  // IQ4_XS, kernels/moe.metal:81-89
+            const uint8_t* b = row + (j / 256) * 136;
+            uint32_t k = j % 256, g = k / 32, v = k % 32;
+            uint32_t high = rd16(b + 2);
+            int scale = (int)(((b[4 + g / 2] >> (4 * (g % 2))) & 15) | (((high >> (2 * g)) & 3) << 4)) - 32;
+            uint32_t q = (b[8 + g * 16 + v % 16] >> (4 * (v / 16))) & 15;
+            return hf(b) * (float)scale * (float)ingot_kvalues_iq4nl[q];
         }
         default: return NAN;
     }

@@ -7,8 +7,8 @@ import numpy as np
 import pytest
 
 from ingot_amd import configs as CF
-from ingot_amd.moe import (F32, IQ2_XS, IQ3_XXS, IQ4_NL, Q4_0, Q4_K, Q8_0, ROUTE_SIGMOID, ROUTE_SOFTMAX, InvalidData,
-                           Matrix)
+from ingot_amd.moe import (BF16, F16, F32, IQ1_M, IQ2_S, IQ2_XS, IQ2_XXS, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, Q2_0, Q2_K,
+                           Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, ROUTE_SIGMOID, ROUTE_SOFTMAX, InvalidData, Matrix)
 from util import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -142,6 +142,20 @@ def test_dequant_and_project_match_oracle(gpu, oracle, kind):
     ref = oracle.dequant_rows(m)
     assert np.abs(got - ref).max() <= 1e-6 * max(1.0, np.abs(ref).max())
     x = CF.inputs(31, 1, cols)[0]
+    y = gpu.project(m, x)
+    yr = oracle.project(m, x)
+    assert np.abs(y - yr).max() <= 1e-4 + 5e-5 * np.abs(yr).max()
+
+
+@pytest.mark.parametrize("kind", [F16, BF16, Q2_K, Q5_K, Q6_K, IQ2_XXS, IQ2_S, IQ3_S, IQ4_XS, IQ1_M, Q2_0])
+def test_dequant_and_project_remaining_formats(gpu, oracle, kind):
+    """Gpu::dequant / Gpu::project (src/metal.rs:1581, :1622) on random valid blocks."""
+    cols = 768
+    m = CF.synth_matrix(kind, 32, 1, 65, cols)
+    got = gpu.dequant(m).reshape(65, cols)
+    ref = oracle.dequant_rows(m)
+    assert np.abs(got - ref).max() <= 1e-6 * max(1.0, np.abs(ref).max())
+    x = CF.inputs(33, 1, cols)[0]
     y = gpu.project(m, x)
     yr = oracle.project(m, x)
     assert np.abs(y - yr).max() <= 1e-4 + 5e-5 * np.abs(yr).max()

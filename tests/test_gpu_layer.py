@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 from ingot_amd import configs as CF
-from ingot_amd.moe import (IQ2_XS, IQ3_XXS, IQ4_NL, Q4_0, Q4_K, Q8_0, ROUTE_SIGMOID, InvalidData, LayerSpec, Matrix,
+from ingot_amd.moe import (BF16, F16, IQ1_M, IQ2_S, IQ2_XS, IQ2_XXS, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, Q2_0, Q2_K, Q4_0,
+                           Q4_K, Q5_K, Q6_K, Q8_0, ROUTE_SIGMOID, InvalidData, LayerSpec, Matrix,
                            MoeLayer, NonFinite)
 from util import assert_close, check_layer
 
@@ -90,6 +91,33 @@ def test_formats_decode_and_prefill(gpu, oracle, gk, dk):
     layer = MoeLayer(gpu, spec)
     for T in (1, 3, 40):  # 4 and 12 pairs: GEMV kernels; 160 pairs: grouped GEMM
         check_layer(layer, spec, CF.inputs(200 + gk, T, 2048), oracle, f"fmt {gk}/{dk} T={T}")
+    layer.destroy()
+
+
+NEW_FORMATS = [(Q2_K, Q2_K), (Q5_K, Q5_K), (Q6_K, Q6_K), (Q4_K, Q6_K), (IQ2_XXS, IQ2_XXS), (IQ2_S, IQ2_S),
+               (IQ3_S, IQ3_S), (IQ4_XS, IQ4_XS), (IQ1_M, IQ1_M), (BF16, BF16), (F16, F16), (Q2_0, Q2_0),
+               (IQ2_S, IQ4_XS), (IQ3_S, Q5_K)]
+
+
+@pytest.mark.parametrize("gk,dk", NEW_FORMATS)
+def test_remaining_formats_decode_and_prefill(gpu, oracle, gk, dk):
+    """Every other type of the reference's table (kernels/moe.metal:17-89): decode
+    GEMV kernels at 1 and 3 tokens, the fp32 grouped GEMM at 40 tokens."""
+    spec = CF.make_layer(110, 100 * gk + dk, 1024, 16, 4, 256, gk, dk)
+    layer = MoeLayer(gpu, spec)
+    for T in (1, 3, 40):
+        check_layer(layer, spec, CF.inputs(210 + gk, T, 1024), oracle, f"fmt {gk}/{dk} T={T}")
+    layer.destroy()
+
+
+@pytest.mark.parametrize("kind", [Q6_K, Q5_K, IQ1_M])
+def test_remaining_formats_wide_hidden_many_experts_shared(gpu, oracle, kind):
+    """H = 4096 (two chunks per lane), 256 experts (16 routing keys per lane),
+    and a gated shared expert in the same format (separate GEMV pair)."""
+    spec = CF.make_layer(111, kind, 4096, 256, 8, 256, kind, kind, shared_ffn=512, shared_gated=True)
+    layer = MoeLayer(gpu, spec)
+    for T in (1, 2, 24):
+        check_layer(layer, spec, CF.inputs(211 + kind, T, 4096), oracle, f"fmt {kind} H=4096 E=256 T={T}")
     layer.destroy()
 
 
