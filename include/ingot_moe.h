@@ -30,6 +30,8 @@
  *                            plus the pre-FFN RMSNorm and residual add of
  *                            Generic::hidden (src/generic.rs:716-724) when a norm
  *                            gain is given
+ *   ingot_layer_forward_add  the same with the attention output's residual add
+ *                            (add_rms, kernels/generic.metal:390-405) fused in
  *
  * Errors follow the reference: an invalid argument, shape or format is
  * INGOT_INVALID (io::ErrorKind::InvalidData via invalid(), src/lib.rs:39-41);
@@ -169,6 +171,13 @@ int ingot_layer_reserve(ingot_layer* layer, uint32_t T);
  * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL. */
 int ingot_layer_forward(ingot_layer* layer, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
                         float* d_weights);
+/* out[T][H] = s + MoE(RMSNorm(s)) with s = x + a: the residual add before the
+ * pre-FFN norm fused into the router, replacing add_rms (kernels/generic.metal:
+ * 390-405, called as rms(x, Some(a), ffn_norm) at src/generic.rs:716-724)
+ * followed by the MoE FFN and its residual add. Needs a layer created with a
+ * norm gain (else INGOT_INVALID); otherwise as ingot_layer_forward. */
+int ingot_layer_forward_add(ingot_layer* layer, const float* d_x, const float* d_a, uint32_t T, float* d_out,
+                            uint32_t* d_ids, float* d_weights);
 /* Prefill GEMM arithmetic. INGOT_GEMM_AUTO (default): Q4_K experts use the
  * split-precision f16 MFMA GEMM (fp32-accurate to ~2^-21 relative; needs
  * |activations| < 65504), other formats the fp32 MFMA GEMM.

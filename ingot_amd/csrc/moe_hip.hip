@@ -148,8 +148,9 @@ int upload(ingot_ctx* ctx, const T* h, uint64_t n, T** d) {
 // ------------------------------------------------------------------ launchers
 // Each returns false if no instantiation covers the shape.
 
-bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_sg, const float* x, const float* W,
-                   const float* sgvec, const float* gain, float eps, float* logits, float* sgl, float* xn) {
+bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_sg, const float* x,
+                   const float* addend, const float* W, const float* sgvec, const float* gain, float eps,
+                   float* logits, float* sgl, float* xn, float* xs) {
     const uint32_t rows = E + (has_sg ? 1u : 0u);
     // Below 64 tokens one token and one router row per wave keeps the grid
     // wide (T x E / 4 blocks); from 64 tokens the 64-output transposed kernel.
@@ -158,7 +159,7 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
         // 16 experts per block when 32 would leave fewer than two blocks per CU
         const bool eb16 = (T + 7) / 8 * (E / 32) < 512;
         const dim3 grid((T + 7) / 8, E / (eb16 ? 16 : 32));
-#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV>), grid, dim3(256), 0, s, x, W, sgvec, gain, eps, T, E, logits, sgl, xn)
+#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV>), grid, dim3(256), 0, s, x, addend, W, sgvec, gain, eps, T, E, logits, sgl, xn, xs)
         if (HB == 8) {
             if (eb16) RT(8, 16);
             else RT(8, 32);
@@ -175,8 +176,8 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
 #define ROUTER(TOK, HBV)                                                                                       \
     do {                                                                                                       \
         dim3 grid((T + TOK - 1) / TOK, gy);                                                                    \
-        hipLaunchKernelGGL((k_router<TOK, HBV>), grid, dim3(64 * wpb), 0, s, x, W, sgvec, gain, eps, T, E,    \
-                           epw, logits, sgl, xn);                                                              \
+        hipLaunchKernelGGL((k_router<TOK, HBV>), grid, dim3(64 * wpb), 0, s, x, addend, W, sgvec, gain, eps, T,  \
+                           E, epw, logits, sgl, xn, xs);                                                       \
         return true;                                                                                           \
     } while (0)
     if (HB == 8) {
@@ -368,6 +369,7 @@ struct ingot_layer {
              *inverse = nullptr, *stiles = nullptr;
     _Float16 *xh = nullptr, *xl = nullptr, *acth = nullptr, *actl = nullptr;
     float *xs = nullptr, *acts = nullptr;  // 32-column sums of x and act (Q4_K mins term)
+    float* resid = nullptr;                 // x + a of ingot_layer_forward_add (the new residual stream)
     uint32_t tile_cap = 0, stile_cap = 0;
     std::function<void(hipStream_t)> stage[ST_N];
     const char* stage_name[ST_N] = {};
@@ -406,6 +408,7 @@ static int reserve(ingot_layer* L, uint32_t T) {
         {(void**)&L->xh, 2ull * T * L->H},      {(void**)&L->xl, 2ull * T * L->H},
         {(void**)&L->acth, 2ull * PS * L->F},    {(void**)&L->actl, 2ull * PS * L->F},
         {(void**)&L->xs, 4ull * T * (L->H / 32)}, {(void**)&L->acts, 4ull * PS * (L->F / 32)},
+        {(void**)&L->resid, L->has_norm ? 4ull * T * L->H : 0ull},
     };
     uint64_t total = 0;
     for (auto& p : parts) total += (p.bytes + 255) & ~255ull;
@@ -837,17 +840,18 @@ int ingot_layer_reserve(ingot_layer* L, uint32_t T) {
 // dispatch + grouped MFMA GEMM (prefill) kernels.
 static const uint32_t GEMV_MAX_PAIRS = 64;
 
-int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids, float* d_weights) {
-    if (!L) return INGOT_INVALID;
+// d_a != NULL (ingot_layer_forward_add, norm layers only): the router adds
+// d_a to d_x, normalises the sum and stores it to L->resid, which is then the
+// residual the down / combine kernels add.
+static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uint32_t T, float* d_out,
+                         uint32_t* d_ids, float* d_weights) {
     ingot_ctx* ctx = L->ctx;
-    CHECK_CTX(ctx);
-    if (!d_x || !d_out || T == 0) return fail(ctx, INGOT_INVALID, "MoE input shape mismatch");
     int st = reserve(L, T);
     if (st != INGOT_OK) return st;
     hipStream_t s = ctx->stream;
     const uint32_t H = L->H, E = L->E, K = L->K, F = L->F, SF = L->SF, P = T * K;
     const float* xin = L->has_norm ? L->xn : d_x;
-    const float* res = L->has_norm ? d_x : nullptr;
+    const float* res = L->has_norm ? (d_a ? L->resid : d_x) : nullptr;
     const float* sgl = L->has_sgvec ? L->sgl : nullptr;
     for (auto& f : L->stage) f = nullptr;
 
@@ -860,13 +864,13 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
 
     // 1. router (+ RMSNorm, + shared gate logit)
     {
-        const float *x = d_x, *W = L->router, *sgv = L->sgvec, *g = L->gain;
-        float *lg = L->logits, *sl = L->sgl, *xn = L->xn;
+        const float *x = d_x, *a = d_a, *W = L->router, *sgv = L->sgvec, *g = L->gain;
+        float *lg = L->logits, *sl = L->sgl, *xn = L->xn, *rs = L->resid;
         float eps = L->eps;
         bool has_sg = L->has_sgvec;
         uint32_t HB = H / 256;
         L->stage[ST_ROUTER] = [=](hipStream_t ss) {
-            launch_router(ss, HB, T, E, has_sg, x, W, sgv, g, eps, lg, sl, xn);
+            launch_router(ss, HB, T, E, has_sg, x, a, W, sgv, g, eps, lg, sl, xn, rs);
         };
         L->stage_name[ST_ROUTER] = "k_router";
     }
@@ -997,6 +1001,22 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
     if (d_ids) HIP_TRY(ctx, hipMemcpyAsync(d_ids, L->ids, 4ull * P, hipMemcpyDeviceToDevice, s));
     if (d_weights) HIP_TRY(ctx, hipMemcpyAsync(d_weights, L->wts, 4ull * P, hipMemcpyDeviceToDevice, s));
     return INGOT_OK;
+}
+
+int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids, float* d_weights) {
+    if (!L) return INGOT_INVALID;
+    CHECK_CTX(L->ctx);
+    if (!d_x || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
+    return layer_forward(L, d_x, nullptr, T, d_out, d_ids, d_weights);
+}
+
+int ingot_layer_forward_add(ingot_layer* L, const float* d_x, const float* d_a, uint32_t T, float* d_out,
+                            uint32_t* d_ids, float* d_weights) {
+    if (!L) return INGOT_INVALID;
+    CHECK_CTX(L->ctx);
+    if (!d_x || !d_a || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
+    if (!L->has_norm) return fail(L->ctx, INGOT_INVALID, "the residual add needs the layer's RMSNorm gain");
+    return layer_forward(L, d_x, d_a, T, d_out, d_ids, d_weights);
 }
 
 int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t stage, uint32_t reps, float* ms) {

@@ -331,6 +331,31 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t (&key)[NE], const fl
 
 
 // ---------------------------------------------------------------- router
+// Residual add ahead of the norm (the reference's add_rms, kernels/generic.metal:
+// 390-405): the rows s = x + a replace the wave's inputs, and the writing wave
+// stores s, the layer's new residual stream, to xs.
+template <int NT, int HB>
+__device__ __forceinline__ void add_residual(float (&xr)[NT][HB * 4], const float* __restrict__ a,
+                                             float* __restrict__ xs, uint32_t t0, uint32_t T, uint32_t lane,
+                                             bool write) {
+    constexpr uint32_t H = 256u * HB;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const uint32_t tt = min(t0 + t, T - 1);
+#pragma unroll
+        for (int i = 0; i < HB; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(a + (uint64_t)tt * H + 4u * lane + 256u * i);
+            xr[t][4 * i] += v.x; xr[t][4 * i + 1] += v.y; xr[t][4 * i + 2] += v.z; xr[t][4 * i + 3] += v.w;
+        }
+        if (write && t0 + t < T) {
+#pragma unroll
+            for (int i = 0; i < HB; ++i)
+                *reinterpret_cast<float4*>(xs + (uint64_t)(t0 + t) * H + 4u * lane + 256u * i) =
+                    make_float4(xr[t][4 * i], xr[t][4 * i + 1], xr[t][4 * i + 2], xr[t][4 * i + 3]);
+        }
+    }
+}
+
 // One wave per (group of TOK tokens, group of experts). Lane l holds the
 // columns 4l + 256i + c (i < HB = H/256, c < 4) of each of its tokens, which
 // is the slot layout of the fixed reduction order (det_math.h): each logit is
@@ -338,15 +363,16 @@ __device__ __forceinline__ uint32_t wave_kth(const uint32_t (&key)[NE], const fl
 // bit-identical to the CPU's ingot_router_partial + ingot_butterfly64.
 // With a norm gain the wave first computes RMSNorm of its tokens in the same
 // order (sum of squares over the slots, butterfly, 1/sqrt(ss/H + eps), (x*r)*g)
-// and writes the normalised rows (block (.., 0), wave 0 only).
+// and writes the normalised rows (block (.., 0), wave 0 only). With an
+// addend a the rows are x + a first (add_residual), stored to xs.
 // Expert index E (when sgvec != NULL) is the shared-expert gate vector: its
 // product goes to sgl[t].
 template <int TOK, int HB>
-__global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ W,
-                                                const float* __restrict__ sgvec, const float* __restrict__ gain,
-                                                float eps, uint32_t T, uint32_t E, uint32_t epw,
-                                                float* __restrict__ logits, float* __restrict__ sgl,
-                                                float* __restrict__ xn) {
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ addend,
+                                                const float* __restrict__ W, const float* __restrict__ sgvec,
+                                                const float* __restrict__ gain, float eps, uint32_t T, uint32_t E,
+                                                uint32_t epw, float* __restrict__ logits, float* __restrict__ sgl,
+                                                float* __restrict__ xn, float* __restrict__ xs) {
     INGOT_NO_CONTRACT
     constexpr uint32_t H = 256u * HB;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -375,6 +401,7 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
             xr[t][4 * i] = v.x; xr[t][4 * i + 1] = v.y; xr[t][4 * i + 2] = v.z; xr[t][4 * i + 3] = v.w;
         }
     }
+    if (addend) add_residual<TOK, HB>(xr, addend, xs, t0, T, lane, blockIdx.y == 0 && wave == 0);
     if (gain) {
         float g[HB * 4];
 #pragma unroll
@@ -488,13 +515,15 @@ __device__ __forceinline__ float transpose_sum64(float (&v)[64], uint32_t lane) 
 // pairs, and one transposed butterfly leaves pair (t, e) = (l / 32, l % 32)
 // (EB = 32) or (l / 32, (l / 2) % 16) (EB = 16) in lane l.
 // The block's router rows pass through LDS in double-buffered chunks of 4.
-// RMSNorm (gain: written to xn by the by == 0 blocks) and the shared-expert
-// gate logit (sgvec: by == 0 blocks, wave_sum) are computed as in k_router.
+// The residual add (addend: s written to xs by the by == 0 blocks), RMSNorm
+// (gain: written to xn by the by == 0 blocks) and the shared-expert gate logit
+// (sgvec: by == 0 blocks, wave_sum) are computed as in k_router.
 template <int HB, int EB>
-__global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, const float* __restrict__ W,
-                                                  const float* __restrict__ sgvec, const float* __restrict__ gain,
-                                                  float eps, uint32_t T, uint32_t E, float* __restrict__ logits,
-                                                  float* __restrict__ sgl, float* __restrict__ xn) {
+__global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, const float* __restrict__ addend,
+                                                  const float* __restrict__ W, const float* __restrict__ sgvec,
+                                                  const float* __restrict__ gain, float eps, uint32_t T, uint32_t E,
+                                                  float* __restrict__ logits, float* __restrict__ sgl,
+                                                  float* __restrict__ xn, float* __restrict__ xs) {
     INGOT_NO_CONTRACT
     constexpr uint32_t H = 256u * HB, Q = H / 4u;  // Q float4 per row
     constexpr int CH = 4;                         // router rows per LDS chunk
@@ -512,6 +541,7 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             xr[t][4 * i] = v.x; xr[t][4 * i + 1] = v.y; xr[t][4 * i + 2] = v.z; xr[t][4 * i + 3] = v.w;
         }
     }
+    if (addend) add_residual<2, HB>(xr, addend, xs, t0, T, lane, blockIdx.y == 0);
     if (gain) {
         float g[HB * 4];
 #pragma unroll

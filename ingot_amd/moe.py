@@ -372,6 +372,13 @@ class MoeLayer:
         self.gpu._check(self.gpu.lib.ingot_layer_forward(self.handle, x.ptr, T, out.ptr, ids.ptr if ids else None,
                                                          weights.ptr if weights else None))
 
+    def forward_add(self, x: DeviceBuffer, a: DeviceBuffer, T: int, out: DeviceBuffer,
+                    ids: Optional[DeviceBuffer] = None, weights: Optional[DeviceBuffer] = None) -> None:
+        """out = s + MoE(RMSNorm(s)), s = x + a (norm layers): add_rms fused into the router."""
+        self.gpu._check(self.gpu.lib.ingot_layer_forward_add(self.handle, x.ptr, a.ptr, T, out.ptr,
+                                                             ids.ptr if ids else None,
+                                                             weights.ptr if weights else None))
+
     def __call__(self, x: np.ndarray):
         """Host convenience: out [T, H], ids [T, K], weights [T, K]."""
         x = _f32(x).reshape(-1, self.spec.hidden)

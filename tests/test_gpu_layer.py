@@ -121,6 +121,38 @@ def test_remaining_formats_wide_hidden_many_experts_shared(gpu, oracle, kind):
     layer.destroy()
 
 
+def test_forward_add_fuses_the_residual_add(gpu, oracle):
+    """ingot_layer_forward_add(x, a): add_rms (kernels/generic.metal:390-405) fused
+    into the router. Equals the oracle layer on s = x + a, and bit for bit the
+    plain forward of x + a, at decode and prefill sizes; refused without a norm."""
+    spec = CF.c4_layer(3)
+    H, K = spec.hidden, spec.top_k
+    layer = MoeLayer(gpu, spec)
+    for T in (1, 8, 100):
+        x = CF.inputs(40, T, H, seed=T)
+        a = (0.5 * CF.inputs(41, T, H, seed=T)).astype(np.float32)
+        s = (x + a).astype(np.float32)
+        outs = []
+        for fused in (True, False):
+            o, i, w = gpu.buffer(4 * T * H), gpu.buffer(4 * T * K), gpu.buffer(4 * T * K)
+            if fused:
+                layer.forward_add(gpu.to_device(x), gpu.to_device(a), T, o, i, w)
+            else:
+                layer.forward(gpu.to_device(s), T, o, i, w)
+            gpu.synchronize()
+            outs.append((o.download(np.float32, T * H), i.download(np.uint32, T * K), w.download(np.float32, T * K)))
+        assert all(np.array_equal(p, q) for p, q in zip(*outs)), f"T={T}: fused add differs from forward(x + a)"
+        st, ref, rids, rw = oracle.moe_forward(spec, s, oracle.F64)
+        assert st == 0 and np.array_equal(outs[0][1].reshape(T, K), rids)
+        assert_close(outs[0][0].reshape(T, H), ref, f"forward_add T={T}")
+    layer.destroy()
+    plain = MoeLayer(gpu, small_layer(Q4_K, Q4_K, H=1024, E=8, K=2))
+    with pytest.raises(InvalidData):
+        plain.forward_add(gpu.to_device(np.zeros(1024, np.float32)), gpu.to_device(np.zeros(1024, np.float32)), 1,
+                          gpu.buffer(4096))
+    plain.destroy()
+
+
 def test_hidden_4096_and_1024(gpu, oracle):
     for H in (4096, 1024, 2048):
         spec = small_layer(Q4_K, Q4_K, H=H, E=8, K=2, F=256)
