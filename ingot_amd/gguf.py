@@ -386,11 +386,19 @@ def ffn_weights(model: Gguf, layer: int, width: int, hidden: int, count: int, id
 
 
 def _f32_tensor(model: Gguf, name: str, shape: Sequence[int]) -> np.ndarray:
-    """An F32 tensor's values (Weight::require_f32, src/glm.rs:425)."""
+    """A small F32, F16 or BF16 tensor (router, bias, gate vector, norm gain)
+    as float32. The two 16-bit types widen exactly (the same values the GPU's
+    project path decodes); any other type is refused, as Weight::require_f32
+    (src/glm.rs:425) refuses non-F32 norms."""
     m = model.matrix(name, shape, [0])
-    if m.kind != 0:
-        raise InvalidData(f"{name}: expected F32")
-    return m.data.view("<f4").astype(np.float32)
+    raw = np.ascontiguousarray(m.data)
+    if m.kind == 0:
+        return raw.view("<f4").astype(np.float32)
+    if m.kind == 1:
+        return raw.view("<f2").astype(np.float32)
+    if m.kind == 30:
+        return (raw.view("<u2").astype(np.uint32) << 16).view(np.float32)
+    raise InvalidData(f"{name}: expected F32, F16 or BF16")
 
 
 def layer_spec(model: Gguf, layer: int, norm: bool = False) -> LayerSpec:

@@ -406,3 +406,33 @@ def test_moe_layer_missing_tensors_and_keys(tmp_path, capsys):
     rc, _, se = run_cli(capsys, [p2, 0, x, tmp_path / "o.f32"])
     assert rc == 1 and "missing tensor: blk.0.ffn_gate_inp.weight" in se
     assert not (tmp_path / "o.f32").exists()
+
+
+@pytest.mark.parametrize("kind", [1, 30, 8])
+def test_layer_spec_16_bit_router(tmp_path, kind):
+    """F16 and BF16 routers and gate vectors widen exactly to float32; other
+    types are refused for these small tensors."""
+    spec = CF.make_layer(54, 0, 256, 4, 2, 256, Q8_0, Q8_0, shared_ffn=256, shared_gated=True)
+    tensors = []
+    for name, dims, k, data in G.layer_tensors(spec, 0):
+        if "gate_inp" in name:
+            v = np.frombuffer(np.ascontiguousarray(data).tobytes(), "<f4")
+            if kind == 1:
+                data = v.astype("<f2")
+            elif kind == 30:
+                data = (CF.round_bf16(v).view(np.uint32) >> 16).astype("<u2")
+            else:
+                data = CF.quantize(Q8_0, v.reshape(1, -1)).data
+            k = kind
+        tensors.append((name, dims, k, data))
+    p = str(tmp_path / "r.gguf")
+    G.write_gguf(p, G.layer_metadata(spec, "qwen4exp", 1), tensors)
+    with G.Gguf.open(p) as g:
+        if kind == 8:
+            with pytest.raises(InvalidData, match="expected F32, F16 or BF16"):
+                G.layer_spec(g, 0)
+            return
+        got = G.layer_spec(g, 0)
+        widen = (lambda v: v.astype(np.float16).astype(np.float32)) if kind == 1 else CF.round_bf16
+        assert got.router.dtype == np.float32 and np.array_equal(got.router, widen(spec.router))
+        assert np.array_equal(got.shared_gate_vec, widen(spec.shared_gate_vec))

@@ -19,7 +19,7 @@ import pytest
 
 from ingot_amd import configs as CF
 from ingot_amd import gguf as G
-from ingot_amd.moe import IQ2_XS, IQ4_NL, Q4_K, Q8_0, MoeLayer
+from ingot_amd.moe import BF16, IQ2_S, IQ2_XS, IQ3_S, IQ4_NL, IQ4_XS, Q2_0, Q4_K, Q8_0, MoeLayer
 from ingot_amd.moe_layer import moe_layer
 from util import assert_close, check_layer
 
@@ -117,4 +117,53 @@ def test_resident_layer_from_gguf(gpu, oracle, model, layer):
         for T in (1, 4, 64):
             print(f"resident layer={layer} T={T}", flush=True)
             check_layer(resident, spec, CF.inputs(60, T, H, seed=layer), oracle, f"GGUF layer {layer} T={T}")
+        resident.destroy()
+
+
+def to_bf16(v):
+    """float32 -> (bf16 bytes, the float32 values they hold), round to nearest even."""
+    r = CF.round_bf16(np.asarray(v, np.float32))
+    return (r.view(np.uint32) >> 16).astype("<u2"), r
+
+
+def test_qwen38_style_format_mix(gpu, oracle, tmp_path):
+    """The format mix of the reference's real-file record (validation/rust-moe-layer-0.json:
+    BF16, IQ2_S, IQ3_S, IQ4_NL, IQ4_XS, Q2_0): BF16 router and shared gate, IQ2_S gate/up,
+    IQ3_S down, IQ4_XS shared gate/up, Q2_0 shared down; through the command and as a
+    resident layer."""
+    spec = CF.make_layer(61, 0, H, 64, 8, 256, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
+                         shared_down_kind=Q2_0, shared_gated=True)
+    rb, spec.router = to_bf16(spec.router)
+    gb, spec.shared_gate_vec = to_bf16(spec.shared_gate_vec)
+    tensors = []
+    for name, dims, kind, data in G.layer_tensors(spec, 0):
+        if name.endswith("ffn_gate_inp.weight"):
+            tensors.append((name, dims, BF16, rb))
+        elif name.endswith("ffn_gate_inp_shexp.weight"):
+            tensors.append((name, dims, BF16, gb))
+        else:
+            tensors.append((name, dims, kind, data))
+    path = str(tmp_path / "mix.gguf")
+    G.write_gguf(path, G.layer_metadata(spec, "qwen4exp", 1), tensors)
+    for name, x in cases():
+        inp, out = tmp_path / f"in-{name}.f32", tmp_path / f"out-{name}.f32"
+        x.astype("<f4").tofile(inp)
+        print(f"mix moe-layer case={name}", flush=True)
+        lines = parse(moe_layer([path, "0", str(inp), str(out)], gpu))
+        st, ref, ids, w = oracle.moe_forward(spec, x[None], oracle.F64)
+        assert json.loads(lines["selected_experts"]) == [int(i) for i in ids[0]]
+        np.testing.assert_allclose(np.array(json.loads(lines["routing_weights"]), np.float32), w[0],
+                                   rtol=2e-5, atol=2e-7)
+        got = np.fromfile(out, dtype="<f4")
+        if name == "zero_ties":
+            assert not got.any()
+        else:
+            assert_close(got, ref[0], f"mix moe-layer {name}")
+    with G.Gguf.open(path) as g:
+        file_spec = G.layer_spec(g, 0)
+        assert np.array_equal(file_spec.router, spec.router)
+        resident = MoeLayer(gpu, file_spec)
+        for T in (1, 4, 40):
+            print(f"mix resident T={T}", flush=True)
+            check_layer(resident, file_spec, CF.inputs(61, T, H, seed=T), oracle, f"mix resident T={T}")
         resident.destroy()
