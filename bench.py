@@ -246,6 +246,19 @@ def extra_configs(gpu, args):
     log(f"C3 layer synthesized in {time.time() - t0:.1f} s")
     single("configs[3] T=64", spec3, 64, 2, CF.inputs(3, 64, 4096, bf16=True), "hbm and mfma (ridge)")
     del spec3
+    # The real checkpoints' format mixes at the graded shapes (for the record): Qwen3-30B-A3B
+    # Q4_K_M (Q4_K gate/up, Q6_K down in about a third of its layers) and the Qwen3.8 IQ2_XS
+    # mix (validation/rust-moe-layer-0.json:9-16).
+    from ingot_amd.moe import IQ2_S, IQ3_S, IQ4_XS, Q2_0, Q4_K, Q6_K
+    specm = CF.make_layer(0, 0, 2048, 128, 8, 768, Q4_K, Q6_K)
+    single("Q4_K/Q6_K mix b=1", specm, 1, 32, CF.inputs(0, 1, 2048), "hbm")
+    specm.router_bias = np.array([1.5 * np.log((e + 1.0) ** -1.1) for e in range(128)], np.float32)
+    single("Q4_K/Q6_K mix prefill 512", specm, 512, 8, CF.inputs(0, 512, 2048), "mfma")
+    del specm
+    specq = CF.make_layer(2, 0, 2048, 512, 10, 512, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
+                          shared_down_kind=Q2_0, shared_gated=True)
+    single("IQ2_S/IQ3_S + IQ4_XS/Q2_0 shared mix b=1", specq, 1, 32, CF.inputs(2, 1, 2048), "hbm")
+    del specq
     # 48 independent layers, h <- h + MoE_l(RMSNorm_l(h)); one step = the whole stack.
     t0 = time.time()
     specs = [CF.c4_layer(l) for l in range(48)]

@@ -274,6 +274,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
     switch (aord) {                                         \
         case A_IQ4NL: F16(KV, A_IQ4NL); return true;        \
         case A_IQ3XXS: F16(KV, A_IQ3XXS); return true;      \
+        case A_F32: F16(KV, A_F32); return true;            \
         default: F16(KV, A_NATURAL); return true;           \
     }
     if constexpr (GATEUP) {
@@ -932,15 +933,18 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
         // The f16 GEMM runs when both projections' formats allow it; the shared
         // expert then joins the same launches (as tile expert E over rows
         // P..P+T-1) when it has the routed experts' formats and width, and
-        // otherwise runs on the fp32 GEMM beside them.
-        const bool f16 = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(gate.kind, H, true) &&
-                         f16_gemm_kind(down.kind, F, false);
+        // otherwise runs on the fp32 GEMM beside them. When only gate/up's
+        // format allows it (a Q4_K_M layer's Q6_K down), gate/up runs on the
+        // f16 GEMM writing fp32 act and the down projection on the fp32 GEMM,
+        // over the same 64-token tiles.
+        const bool f16gu = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(gate.kind, H, true);
+        const bool f16 = f16gu && f16_gemm_kind(down.kind, F, false);
         const bool merge = f16 && hs && SF == F && sgate.kind == gate.kind && sup.kind == up.kind &&
                            sdown.kind == down.kind && sgate.stride == gate.stride && sup.stride == up.stride &&
                            sdown.stride == down.stride;
-        const int aord = a_order(down.kind), xord = a_order(gate.kind);
-        const bool mins = down.kind == 12;
-        const uint32_t tm = f16 ? TM16 : TM;
+        const int aord = f16 ? a_order(down.kind) : A_F32, xord = a_order(gate.kind);
+        const bool mins = f16 && down.kind == 12;
+        const uint32_t tm = f16gu ? TM16 : TM;
         const uint32_t S = merge ? T : 0u, capf = cap + (merge ? scap : 0u), e_sh = merge ? E : 0xffffffffu;
         _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
         float *xs = L->xs, *acts = L->acts;
@@ -948,7 +952,7 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
         // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
             // With the f16 GEMM, blocks 1.. of the dispatch launch split x into f16 hi + lo.
-            const uint64_t n = f16 ? (uint64_t)T * H : 0ull;
+            const uint64_t n = f16gu ? (uint64_t)T * H : 0ull;
             const uint32_t nsplit = (uint32_t)((n / 4 + 1023) / 1024);
             hipLaunchKernelGGL(k_dispatch, dim3(1 + nsplit), dim3(1024), 0, ss, ids, P, E, tm, capf, counts, first, tiles,
                                pairs, inverse, S, K, xin, n, xh, xl, xs, (uint32_t)xord);
@@ -957,12 +961,12 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch";
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
-            if (f16) {
+            if (f16gu) {
                 launch_gemm_f16<true>(ss, gate.kind, aord, dim3(8 * (F / 64) * ((capf + 7) / 8)), gate.d, up.d,
                                       merge ? sgate.d : nullptr, merge ? sup.d : nullptr, e_sh, gate.stride, up.stride,
                                       F, H, (const _Float16*)xh, (const _Float16*)xl, (const float*)xs,
-                                      (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit, (float*)nullptr,
-                                      acth, actl, mins ? acts : nullptr, F / 64, T);
+                                      (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit,
+                                      f16 ? (float*)nullptr : act, acth, actl, mins ? acts : nullptr, F / 64, T);
             } else {
                 launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
                                   pairs, K, tiles, F, limit, act);
@@ -971,7 +975,7 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
                 launch_gemm<true>(ss, sgate.kind, dim3(SF / 64, scap), sgate.d, sup.d, sgate.stride, sup.stride, SF, H,
                                   xin, nullptr, 1, stiles, SF, limit, sact);
         };
-        L->stage_name[ST_GATEUP] = f16 ? "k_gemm_f16<gate_up>" : "k_gemm<gate_up>";
+        L->stage_name[ST_GATEUP] = f16gu ? "k_gemm_f16<gate_up>" : "k_gemm<gate_up>";
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
             if (f16)
                 launch_gemm_f16<false>(ss, down.kind, A_NATURAL, dim3(8 * (H / 128) * ((capf + 7) / 8)), down.d,

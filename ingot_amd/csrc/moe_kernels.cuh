@@ -1538,7 +1538,9 @@ typedef short short2v __attribute__((ext_vector_type(2)));
 //     transposed, column 64 kq + 16 sq + j -> 64 sq + 16 kq + j (kq, sq < 4):
 //     lane kq reads its grid bytes 16 kq .. +15 once per superblock and uses
 //     4 of them (16 columns) in slab sq, so slab sq's A is one contiguous run.
-enum : int { A_NATURAL = 0, A_IQ4NL = 1, A_IQ3XXS = 2 };
+//   A_F32: act in natural order as fp32 (out), for a down projection that
+//     runs on the fp32 GEMM (a format without an f16 path).
+enum : int { A_NATURAL = 0, A_IQ4NL = 1, A_IQ3XXS = 2, A_F32 = 3 };
 template <int ORD>
 __device__ __forceinline__ uint32_t a_pos(uint32_t c) {
     if constexpr (ORD == A_IQ4NL) {
@@ -2055,7 +2057,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int j = 0; j < 4; ++j) {
                 const uint32_t m = mb * 16u + 4u * kq + j;
                 const uint64_t q = q0 + m;
-                if (GATEUP) {
+                if (GATEUP && AORD == A_F32) {
+                    const float v0 = swiglu(acc[mb][0][j], acc[mb][2][j], limit);
+                    const float v1 = swiglu(acc[mb][1][j], acc[mb][3][j], limit);
+                    if (m < n) {
+                        out[q * ldo + row0 + 32u * wave + ln] = v0;
+                        out[q * ldo + row0 + 32u * wave + 16u + ln] = v1;
+                    }
+                } else if (GATEUP) {
                     const float v0 = swiglu(acc[mb][0][j], acc[mb][2][j], limit);
                     const float v1 = swiglu(acc[mb][1][j], acc[mb][3][j], limit);
                     _Float16 h0, l0, h1, l1;

@@ -96,7 +96,7 @@ def test_formats_decode_and_prefill(gpu, oracle, gk, dk):
 
 NEW_FORMATS = [(Q2_K, Q2_K), (Q5_K, Q5_K), (Q6_K, Q6_K), (Q4_K, Q6_K), (IQ2_XXS, IQ2_XXS), (IQ2_S, IQ2_S),
                (IQ3_S, IQ3_S), (IQ4_XS, IQ4_XS), (IQ1_M, IQ1_M), (BF16, BF16), (F16, F16), (Q2_0, Q2_0),
-               (IQ2_S, IQ4_XS), (IQ3_S, Q5_K)]
+               (IQ2_S, IQ4_XS), (IQ3_S, Q5_K), (IQ3_XXS, Q6_K)]
 
 
 @pytest.mark.parametrize("gk,dk", NEW_FORMATS)
@@ -107,6 +107,26 @@ def test_remaining_formats_decode_and_prefill(gpu, oracle, gk, dk):
     layer = MoeLayer(gpu, spec)
     for T in (1, 3, 40):
         check_layer(layer, spec, CF.inputs(210 + gk, T, 1024), oracle, f"fmt {gk}/{dk} T={T}")
+    layer.destroy()
+
+
+@pytest.mark.parametrize("gemm_mode", ["auto", "fp32"])
+def test_f16_gate_up_with_fp32_down(gpu, oracle, gemm_mode):
+    """A Q4_K_M layer's shape: Q4_K gate/up on the f16 GEMM writing fp32 act for a
+    Q6_K down on the fp32 GEMM over the same tiles, with a shared expert beside
+    them; the fp32 mode forces both onto the fp32 GEMM."""
+    from ingot_amd.moe import GEMM_FP32
+    spec = CF.make_layer(112, 0, 2048, 32, 8, 768, Q4_K, Q6_K, bias="zipf", shared_ffn=768,
+                         shared_down_kind=Q6_K, shared_gated=True)
+    layer = MoeLayer(gpu, spec)
+    if gemm_mode == "fp32":
+        layer.set_gemm_mode(GEMM_FP32)
+    for T in (9, 200):
+        check_layer(layer, spec, CF.inputs(212, T, 2048, seed=T), oracle, f"Q4_K/Q6_K {gemm_mode} T={T}")
+    if gemm_mode == "auto":
+        from ingot_amd.moe import STAGE_DOWN, STAGE_GATEUP
+        assert layer.stage_kernel(STAGE_GATEUP) == "k_gemm_f16<gate_up>"
+        assert layer.stage_kernel(STAGE_DOWN) == "k_gemm<down>"
     layer.destroy()
 
 
