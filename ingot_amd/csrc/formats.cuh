@@ -245,33 +245,69 @@ __device__ inline void stage_f16_tables() {
 //   iq2_xs grid (f16): entry i holds the 8 grid values of ingot_iq2xs_grid[i]
 //     as f16 numbers (value 2j in the low half of word j); signs come from
 //     the iq3 sign masks (same 7-bit sign index, same parity rule).
+//   iq2_xxs and iq2_s grids (f16): the same for their codebooks; IQ2_XXS
+//     takes the iq3 sign masks, IQ2_S its explicit sign bytes through the
+//     8-bit sign masks (entry s: bit 2j of s in bit 15, bit 2j + 1 in bit 31
+//     of word j).
+//   iq3_s grid (f16): entry i holds its 4 values as two f16 pairs.
 template <int KIND>
 constexpr bool half_x() {
-    return KIND == 17;
+    return KIND == 16 || KIND == 17 || KIND == 21 || KIND == 22;
 }
 __device__ inline uint4* lds_iq2xs_grid_h() {
     __shared__ uint4 g[512];
     return g;
 }
+__device__ inline uint4* lds_iq2xxs_grid_h() {
+    __shared__ uint4 g[256];
+    return g;
+}
+__device__ inline uint4* lds_iq2s_grid_h() {
+    __shared__ uint4 g[1024];
+    return g;
+}
+__device__ inline uint2* lds_iq3s_grid_h() {
+    __shared__ uint2 g[512];
+    return g;
+}
+__device__ inline uint4* lds_sign8mask() {
+    __shared__ uint4 m[256];
+    return m;
+}
 __device__ inline uint32_t f16_bits_of(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+// Bytes 2j, 2j + 1 of a codebook entry as an f16 pair.
+__device__ inline uint32_t grid_pair_h(uint64_t g, int j) {
+    return f16_bits_of((float)((g >> (16 * j)) & 255u)) | (f16_bits_of((float)((g >> (16 * j + 8)) & 255u)) << 16);
+}
+__device__ inline uint4 sign_mask8(uint32_t sg) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = (((sg >> (2 * j)) & 1u) << 15) | (((sg >> (2 * j + 1)) & 1u) << 31);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
 template <int KIND>
 __device__ inline void stage_half_tables() {
-    if constexpr (KIND == 17) {
-        for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) {
-            const uint64_t g = ingot_iq2xs_grid[i];
-            uint32_t w[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                w[j] = f16_bits_of((float)((g >> (16 * j)) & 255u)) | (f16_bits_of((float)((g >> (16 * j + 8)) & 255u)) << 16);
-            lds_iq2xs_grid_h()[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    if constexpr (KIND == 16 || KIND == 17) {
+        for (uint32_t i = threadIdx.x; i < (KIND == 17 ? 512u : 256u); i += blockDim.x) {
+            const uint64_t g = KIND == 17 ? ingot_iq2xs_grid[i] : ingot_iq2xxs_grid[i];
+            const uint4 h = make_uint4(grid_pair_h(g, 0), grid_pair_h(g, 1), grid_pair_h(g, 2), grid_pair_h(g, 3));
+            if constexpr (KIND == 17) lds_iq2xs_grid_h()[i] = h;
+            else lds_iq2xxs_grid_h()[i] = h;
         }
-        for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
-            const uint32_t sg = ingot_ksign(i);
-            uint32_t w[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) w[j] = (((sg >> (2 * j)) & 1u) << 15) | (((sg >> (2 * j + 1)) & 1u) << 31);
-            lds_iq3_signmask()[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) lds_iq3_signmask()[i] = sign_mask8(ingot_ksign(i));
+    } else if constexpr (KIND == 21 || KIND == 22) {
+        if constexpr (KIND == 22) {
+            for (uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) {
+                const uint64_t g = ingot_iq2s_grid[i];
+                lds_iq2s_grid_h()[i] = make_uint4(grid_pair_h(g, 0), grid_pair_h(g, 1), grid_pair_h(g, 2), grid_pair_h(g, 3));
+            }
+        } else {
+            for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) {
+                const uint64_t g = ingot_iq3s_grid[i];
+                lds_iq3s_grid_h()[i] = make_uint2(grid_pair_h(g, 0), grid_pair_h(g, 1));
+            }
         }
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_sign8mask()[i] = sign_mask8(i);
     }
 }
 
@@ -852,6 +888,24 @@ struct Fmt<16> : Contig {
         }
         return half_bits_to_float(r.d) * (0.5f + (float)(r.aux >> 28)) * 0.25f * s;
     }
+    // As Fmt<17>::dot_raw_h: f16 grid values with the sign masks XORed in,
+    // inputs as f16 hi pairs and remainders times 2^11.
+    __device__ static float dot_raw_h(const Raw& r, const uint32_t* xh, const uint32_t* xl) {
+        float th = 0.f, tl = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint4 g = lds_iq2xxs_grid_h()[byte_of(r.idx, l)];
+            const uint4 m = lds_iq3_signmask()[(r.aux >> (7 * l)) & 127u];
+            const uint32_t gs[4] = {g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                th = dot2_f16(gs[q], xh[4 * l + q], th);
+                tl = dot2_f16(gs[q], xl[4 * l + q], tl);
+            }
+        }
+        const float s = __builtin_fmaf(tl, 1.0f / 2048.0f, th);
+        return half_bits_to_float(r.d) * (0.5f + (float)(r.aux >> 28)) * 0.25f * s;
+    }
     __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
         return dot_raw(load_raw(row, c), c, xv, a, b);
     }
@@ -907,6 +961,23 @@ struct Fmt<22> : Contig {
         }
         return half_bits_to_float(r.d) * 0.25f * s;
     }
+    __device__ static float dot_raw_h(const Raw& r, const uint32_t* xh, const uint32_t* xl) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint4 g = lds_iq2s_grid_h()[byte_of(r.idx, l) | (((r.hs & 255u) << (8 - 2 * l)) & 0x300u)];
+            const uint4 m = lds_sign8mask()[byte_of(r.sgn, l)];
+            const uint32_t gs[4] = {g.x ^ m.x, g.y ^ m.y, g.z ^ m.z, g.w ^ m.w};
+            float th = 0.f, tl = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                th = dot2_f16(gs[q], xh[4 * l + q], th);
+                tl = dot2_f16(gs[q], xl[4 * l + q], tl);
+            }
+            s = __builtin_fmaf(scale(r, l), __builtin_fmaf(tl, 1.0f / 2048.0f, th), s);
+        }
+        return half_bits_to_float(r.d) * 0.25f * s;
+    }
     __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
         return dot_raw(load_raw(row, c), c, xv, a, b);
     }
@@ -934,11 +1005,11 @@ struct Fmt<21> : Contig {
         r.hs = (uint32_t)b[66 + g] | ((((uint32_t)b[106 + g / 2] >> (4 * (g & 1u))) & 15u) << 8);
         return r;
     }
-    // Grid entry j (0..7) of the group: 4 values.
-    __device__ static uint32_t grid(const Raw& r, int j) {
-        const uint32_t lo = byte_of(j < 4 ? r.q0 : r.q1, j & 3);
-        return lds_iq3s_grid()[lo | (((r.hs & 255u) << (8 - j)) & 256u)];
+    // Codebook index of grid entry j (0..7) of the group (4 values each).
+    __device__ static uint32_t grid_index(const Raw& r, int j) {
+        return byte_of(j < 4 ? r.q0 : r.q1, j & 3) | (((r.hs & 255u) << (8 - j)) & 256u);
     }
+    __device__ static uint32_t grid(const Raw& r, int j) { return lds_iq3s_grid()[grid_index(r, j)]; }
     __device__ static void dequant_raw(const Raw& r, uint32_t, float* w) {
         const float db = half_bits_to_float(r.d) * (float)(1u + 2u * (r.hs >> 8));
 #pragma unroll
@@ -966,6 +1037,22 @@ struct Fmt<21> : Contig {
                     s = __builtin_fmaf(ubyte_f(gr, v), flip_sign(xv[8 * l + 4 * hg + v], (sg >> (4 * hg + v)) & 1u), s);
             }
         }
+        return half_bits_to_float(r.d) * (float)(1u + 2u * (r.hs >> 8)) * s;
+    }
+    __device__ static float dot_raw_h(const Raw& r, const uint32_t* xh, const uint32_t* xl) {
+        float th = 0.f, tl = 0.f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint4 m = lds_sign8mask()[byte_of(r.sgn, l)];
+            const uint2 g0 = lds_iq3s_grid_h()[grid_index(r, 2 * l)], g1 = lds_iq3s_grid_h()[grid_index(r, 2 * l + 1)];
+            const uint32_t gs[4] = {g0.x ^ m.x, g0.y ^ m.y, g1.x ^ m.z, g1.y ^ m.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                th = dot2_f16(gs[q], xh[4 * l + q], th);
+                tl = dot2_f16(gs[q], xl[4 * l + q], tl);
+            }
+        }
+        const float s = __builtin_fmaf(tl, 1.0f / 2048.0f, th);
         return half_bits_to_float(r.d) * (float)(1u + 2u * (r.hs >> 8)) * s;
     }
     __device__ static float dot(const uint8_t* row, uint32_t c, const float* xv, float a, float b) {
