@@ -9,12 +9,17 @@
 namespace ingot {
 
 template <int KIND>
-bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, dim3 grid, const GateUpArgs& a) {
-#define GU(C)                                                                                                 \
-    hipLaunchKernelGGL((k_gemv_gate_up<KIND, C, GEMV_RPW>), grid, dim3(256), 0, s, a.g, a.u, a.gs, a.us, a.F, \
-                       a.H, a.x, a.ids, a.K, a.limit, a.act)
-    if (cpl == 1) { GU(1); return true; }
-    if (cpl == 2) { GU(2); return true; }
+bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t rpw, dim3 grid, const GateUpArgs& a) {
+#define GU(C, R)                                                                                                  \
+    hipLaunchKernelGGL((k_gemv_gate_up<KIND, C, R>), grid, dim3(256), 0, s, a.g, a.u, a.gs, a.us, a.F, a.H, a.x, \
+                       a.ids, a.K, a.limit, a.act)
+    if (rpw == 1) {
+        if (cpl == 1) { GU(1, 1); return true; }
+        if (cpl == 2) { GU(2, 1); return true; }
+        return false;
+    }
+    if (cpl == 1) { GU(1, GEMV_RPW); return true; }
+    if (cpl == 2) { GU(2, GEMV_RPW); return true; }
 #undef GU
     return false;
 }
@@ -92,7 +97,7 @@ bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a
 
 #define INGOT_INSTANTIATE_KIND(K)                                                                                \
     namespace ingot {                                                                                            \
-    template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, dim3, const GateUpArgs&);                      \
+    template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, dim3, const GateUpArgs&);            \
     template bool launch_shared_add_k<K>(hipStream_t, uint32_t, dim3, const uint8_t*, uint64_t, uint32_t,        \
                                          uint32_t, const float*, const float*, float*);                          \
     template bool launch_gemm_k<K, true>(hipStream_t, dim3, const GemmArgs&);                                    \

@@ -22,7 +22,7 @@
 
 namespace ingot {
 
-constexpr int GEMV_RPW = 4;  // rows per wave of the separate gate/up GEMV
+constexpr int GEMV_RPW = 4;  // rows per wave of the separate gate/up GEMV (1 when that leaves CUs idle)
 constexpr int DEC_RPW = 1;   // down rows per wave of the decode down kernel
 
 struct GateUpArgs {
@@ -74,9 +74,10 @@ struct GemmArgs {
     float* out;
 };
 
-// k_gemv_gate_up: act = SwiGLU(G x, U x) for `pairs` (grid.y) pairs, cpl chunks per lane.
+// k_gemv_gate_up: act = SwiGLU(G x, U x) for `pairs` (grid.y) pairs, cpl chunks
+// per lane, rpw (GEMV_RPW or 1) rows per wave.
 template <int KIND>
-bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, dim3 grid, const GateUpArgs& a);
+bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t rpw, dim3 grid, const GateUpArgs& a);
 // k_gemv_shared_down_add: out[t] += sigmoid gate * D_s sact[t].
 template <int KS>
 bool launch_shared_add_k(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H,
@@ -92,7 +93,7 @@ template <int KD, int KS>
 bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a);
 
 #define INGOT_DECLARE_KIND(K)                                                                               \
-    extern template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, dim3, const GateUpArgs&);          \
+    extern template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, dim3, const GateUpArgs&); \
     extern template bool launch_shared_add_k<K>(hipStream_t, uint32_t, dim3, const uint8_t*, uint64_t,      \
                                                 uint32_t, uint32_t, const float*, const float*, float*);    \
     extern template bool launch_gemm_k<K, true>(hipStream_t, dim3, const GemmArgs&);                        \

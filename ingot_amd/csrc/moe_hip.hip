@@ -214,10 +214,12 @@ bool launch_gemv_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const u
                          uint32_t F, uint32_t H, uint32_t pairs, const float* x, const uint32_t* ids, uint32_t K,
                          float limit, float* act) {
     const uint32_t cpl = (H / 32 + 63) / 64;
-    dim3 grid((F + 4 * GEMV_RPW - 1) / (4 * GEMV_RPW), pairs);
+    // One row per wave when GEMV_RPW rows per wave would leave fewer blocks than CUs.
+    const uint32_t rpw = (F + 4 * GEMV_RPW - 1) / (4 * GEMV_RPW) * pairs < 256 ? 1u : (uint32_t)GEMV_RPW;
+    dim3 grid((F + 4 * rpw - 1) / (4 * rpw), pairs);
     const GateUpArgs a{g, u, gs, us, F, H, x, ids, K, limit, act};
     switch (kind) {
-#define K_(KV) case KV: return launch_gemv_gate_up_k<KV>(s, cpl, grid, a);
+#define K_(KV) case KV: return launch_gemv_gate_up_k<KV>(s, cpl, rpw, grid, a);
         INGOT_KINDS(K_)
 #undef K_
         default: return false;
