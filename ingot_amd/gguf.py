@@ -123,9 +123,10 @@ class _Reader:
         for _ in range(nm):
             key = self.string()
             kind = self.u32()
+            value = self.value(kind)
             if key in metadata:
                 raise InvalidData("duplicate GGUF metadata")
-            metadata[key] = self.value(kind)
+            metadata[key] = value
         alignment = metadata.get("general.alignment", 32)
         if isinstance(alignment, (float, str, list)):
             raise InvalidData("invalid alignment metadata")
