@@ -255,6 +255,10 @@ def extra_configs(gpu, args):
     specm.router_bias = np.array([1.5 * np.log((e + 1.0) ** -1.1) for e in range(128)], np.float32)
     single("Q4_K/Q6_K mix prefill 512", specm, 512, 8, CF.inputs(0, 512, 2048), "mfma")
     del specm
+    from ingot_amd.moe import Q5_K
+    spec5 = CF.make_layer(0, 0, 2048, 128, 8, 768, Q5_K, Q5_K, bias="zipf")
+    single("Q5_K prefill 512", spec5, 512, 8, CF.inputs(0, 512, 2048), "mfma")
+    del spec5
     specq = CF.make_layer(2, 0, 2048, 512, 10, 512, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
                           shared_down_kind=Q2_0, shared_gated=True)
     single("IQ2_S/IQ3_S + IQ4_XS/Q2_0 shared mix b=1", specq, 1, 32, CF.inputs(2, 1, 2048), "hbm")

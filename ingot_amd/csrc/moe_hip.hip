@@ -251,13 +251,13 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
     }
 }
 
-// Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K;
+// Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K;
 // IQ3_XXS when its rows are a whole number of dwords (kdim % 512 == 0; its
 // loads assume 4-byte aligned rows); IQ4_NL as the down projection only (its A
 // is act, which the gate/up kernel stores permuted for it).
 bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
     switch (kind) {
-        case 12: return kdim % 256 == 0;
+        case 12: case 13: return kdim % 256 == 0;
         case 18: return kdim % 512 == 0;
         case 20: return !gateup && kdim % 64 == 0;
         default: return false;
@@ -282,12 +282,14 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
     if constexpr (GATEUP) {
         switch (kind) {
             case 12: F16_GU(12)
+            case 13: F16_GU(13)
             case 18: F16_GU(18)
             default: return false;
         }
     } else {
         switch (kind) {
             case 12: F16(12, A_NATURAL); return true;
+            case 13: F16(13, A_NATURAL); return true;
             case 18: F16(18, A_NATURAL); return true;
             case 20: F16(20, A_NATURAL); return true;
             default: return false;
@@ -945,7 +947,7 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
                            sdown.kind == down.kind && sgate.stride == gate.stride && sup.stride == up.stride &&
                            sdown.stride == down.stride;
         const int aord = f16 ? a_order(down.kind) : A_F32, xord = a_order(gate.kind);
-        const bool mins = f16 && down.kind == 12;
+        const bool mins = f16 && (down.kind == 12 || down.kind == 13);
         const uint32_t tm = f16gu ? TM16 : TM;
         const uint32_t S = merge ? T : 0u, capf = cap + (merge ? scap : 0u), e_sh = merge ? E : 0xffffffffu;
         _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;

@@ -1642,11 +1642,18 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows) {
-    static_assert(KIND == 12 || KIND == 18 || KIND == 20, "f16 GEMM formats: Q4_K, IQ3_XXS, IQ4_NL");
+    static_assert(KIND == 12 || KIND == 13 || KIND == 18 || KIND == 20, "f16 GEMM formats: Q4_K, Q5_K, IQ3_XXS, IQ4_NL");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
     static_assert(KIND != 20 || !GATEUP, "IQ4_NL is read with permuted A, which only act provides");
     constexpr int NB = 4;
-    constexpr bool Q4K = KIND == 12, IQ3 = KIND == 18, IQ4 = KIND == 20;
+    // Q5_K is Q4_K with a fifth bit per value (b[16 + k % 32] bit k / 32 of its
+    // superblock, kernels/iq3_mix.metal:19-23): the same header, scales, mins
+    // and operand build, nibbles 32 bytes later in a 176-byte superblock, and
+    // a lane's 8 fifth-bit bytes (the same byte positions as its nibble bytes,
+    // bits 2 sq and 2 sq + 1 for slab sq) loaded with each header. q * sc is at
+    // most 31 * 63 = 1953, an exact f16 integer as for Q4_K.
+    constexpr bool Q5K = KIND == 13, Q4K = KIND == 12 || Q5K, IQ3 = KIND == 18, IQ4 = KIND == 20;
+    constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
     constexpr uint32_t UNR = 4u;
     // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
     // 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7), so that the fragment
@@ -1714,6 +1721,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     float4 ps;
 #define INGOT_LOAD_S(SB) ps = __builtin_bit_cast(float4, buf_load16(rgs, soff, 32u * ((SB) < sbs ? (SB) : sbs - 1u)))
     uint4 nhdr[NB];
+    uint2 nqh[Q5K ? NB : 1];
     uint32_t n5[NB], n_d[NB];
     uint3 n3[NB];
     auto load_hdr = [&](uint32_t sb) {
@@ -1721,7 +1729,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
-            if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * 144u);
+            if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
+            if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
             if constexpr (IQ3) {
                 const uint32_t u = (bsoff[nb] + sb * 98u) & ~3u;
                 nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);
@@ -1741,7 +1750,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         for (int nb = 0; nb < NB; ++nb) {
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
             if constexpr (Q4K) {
-                const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * 144u + 16u + 32u * (s & 3u));
+                const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * SBB + QOFF + 32u * (s & 3u));
                 nq[rs][nb].x = v.x;
                 nq[rs][nb].y = v.y;
             } else if constexpr (IQ4) {
@@ -1766,6 +1775,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // and the unit change).
     struct SbState {
         uint32_t sc[NB][2], mn[NB][2];
+        uint2 qh[Q5K ? NB : 1];
         uint32_t gw[NB][4], aw[NB][2];
         float dsc[NB], dmn[NB];
     };
@@ -1776,6 +1786,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             st.dsc[nb] = unit(db);
             if constexpr (Q4K) {
                 q4k_sc_mn(nhdr[nb], st.sc[nb][0], st.sc[nb][1], st.mn[nb][0], st.mn[nb][1]);
+                if constexpr (Q5K) st.qh[nb] = nqh[nb];
                 st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 16777216.f;
                 if (half_bits_to_float(nhdr[nb].x) == 0.f) st.sc[nb][0] = st.sc[nb][1] = 0u;
             } else if constexpr (IQ3) {
@@ -1800,8 +1811,17 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 const uint32_t scw = st.sc[nb][sq >> 1] >> (16u * (sq & 1u));
                 const uint32_t s0_ = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
                 const uint32_t s1_ = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
-                fb[nb][0] = q4_operand(qv[nb].x & 0x0f0f0f0fu, qv[nb].y & 0x0f0f0f0fu, s0_);
-                fb[nb][1] = q4_operand((qv[nb].x >> 4) & 0x0f0f0f0fu, (qv[nb].y >> 4) & 0x0f0f0f0fu, s1_);
+                uint32_t lx = qv[nb].x & 0x0f0f0f0fu, ly = qv[nb].y & 0x0f0f0f0fu;
+                uint32_t hx = (qv[nb].x >> 4) & 0x0f0f0f0fu, hy = (qv[nb].y >> 4) & 0x0f0f0f0fu;
+                if constexpr (Q5K) {
+                    const uint32_t b0 = 2u * sq;
+                    lx |= ((st.qh[nb].x >> b0) & 0x01010101u) << 4;
+                    ly |= ((st.qh[nb].y >> b0) & 0x01010101u) << 4;
+                    hx |= ((st.qh[nb].x >> (b0 + 1u)) & 0x01010101u) << 4;
+                    hy |= ((st.qh[nb].y >> (b0 + 1u)) & 0x01010101u) << 4;
+                }
+                fb[nb][0] = q4_operand(lx, ly, s0_);
+                fb[nb][1] = q4_operand(hx, hy, s1_);
             } else if constexpr (IQ3) {
                 const uint32_t g = st.gw[nb][sq];
                 const uint32_t x = st.aw[nb][sq >> 1];
@@ -1844,7 +1864,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
     constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : 0u;
-    constexpr uint32_t B_PER_SB = Q4K ? NB + 1u : IQ3 ? 5u * NB : 0u;
+    constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQ3 ? 5u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
         constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;
