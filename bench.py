@@ -339,7 +339,8 @@ def main():
                     help="run only a short eager workload for rocprofv3 and exit (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding)",
+        print("bench.py measures one GPU: this build has no multi-GPU path (the layer would shard by expert, "
+              "with one all-reduce of the partial outputs)",
               file=sys.stderr)
         sys.exit(2)
 
