@@ -240,6 +240,7 @@ def extra_configs(gpu, args):
     log(f"C2 layer synthesized in {time.time() - t0:.1f} s")
     for T in (1, 4):
         single(f"configs[2] b={T}", spec2, T, 32, CF.inputs(2, T, 2048), "hbm")
+    single("configs[2] shape, prefill 512", spec2, 512, 4, CF.inputs(2, 512, 2048), "mfma")
     del spec2
     t0 = time.time()
     spec3 = CF.c3_layer()

@@ -223,7 +223,16 @@ __device__ inline uint32_t* lds_iq4nl_pairs() {
 __device__ inline uint32_t iq4nl_f16_bits(int v) { return v < 0 ? 0x8000u | (uint32_t)(-v) : (uint32_t)v; }
 template <int KIND>
 __device__ inline void stage_f16_tables() {
-    if constexpr (KIND == 18) {
+    if constexpr (KIND == 17) {
+        for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq2xs_grid()[i] = ingot_iq2xs_grid[i];
+        for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
+            const uint32_t s = ingot_ksign(i);
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = (((s >> (2 * j)) & 1u) << 15) | (((s >> (2 * j + 1)) & 1u) << 31);
+            lds_iq3_signmask()[i] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    } else if constexpr (KIND == 18) {
         for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_iq3xxs_grid()[i] = ingot_iq3xxs_grid[i];
         for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
             const uint32_t s = ingot_ksign(i);

@@ -252,20 +252,20 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 }
 
 // Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K;
-// IQ3_XXS when its rows are a whole number of dwords (kdim % 512 == 0; its
-// loads assume 4-byte aligned rows); IQ4_NL as the down projection only (its A
+// IQ2_XS and IQ3_XXS when their rows are a whole number of dwords (kdim % 512
+// == 0; their loads assume 4-byte aligned rows); IQ4_NL as the down projection only (its A
 // is act, which the gate/up kernel stores permuted for it).
 bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
     switch (kind) {
         case 12: case 13: return kdim % 256 == 0;
-        case 18: return kdim % 512 == 0;
+        case 17: case 18: return kdim % 512 == 0;
         case 20: return !gateup && kdim % 64 == 0;
         default: return false;
     }
 }
 
 // Column order of A that an f16 GEMM over weights of `kind` reads.
-int a_order(uint32_t kind) { return kind == 20 ? A_IQ4NL : kind == 18 ? A_IQ3XXS : A_NATURAL; }
+int a_order(uint32_t kind) { return kind == 20 ? A_IQ4NL : (kind == 17 || kind == 18) ? A_IQ3XXS : A_NATURAL; }
 
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
 // projection's a_order).
@@ -283,6 +283,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
         switch (kind) {
             case 12: F16_GU(12)
             case 13: F16_GU(13)
+            case 17: F16_GU(17)
             case 18: F16_GU(18)
             default: return false;
         }
@@ -290,6 +291,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
         switch (kind) {
             case 12: F16(12, A_NATURAL); return true;
             case 13: F16(13, A_NATURAL); return true;
+            case 17: F16(17, A_NATURAL); return true;
             case 18: F16(18, A_NATURAL); return true;
             case 20: F16(20, A_NATURAL); return true;
             default: return false;

@@ -1642,7 +1642,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows) {
-    static_assert(KIND == 12 || KIND == 13 || KIND == 18 || KIND == 20, "f16 GEMM formats: Q4_K, Q5_K, IQ3_XXS, IQ4_NL");
+    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20,
+                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ3_XXS, IQ4_NL");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
     static_assert(KIND != 20 || !GATEUP, "IQ4_NL is read with permuted A, which only act provides");
     constexpr int NB = 4;
@@ -1653,6 +1654,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // bits 2 sq and 2 sq + 1 for slab sq) loaded with each header. q * sc is at
     // most 31 * 63 = 1953, an exact f16 integer as for Q4_K.
     constexpr bool Q5K = KIND == 13, Q4K = KIND == 12 || Q5K, IQ3 = KIND == 18, IQ4 = KIND == 20;
+    // IQ2_XS takes IQ3_XXS's path: 74-byte superblocks (2 bytes off a dword
+    // every other one, like 98), lane kq's 16 bytes of 9+7-bit codes at
+    // 2 + 16 kq (8 codes: 64 columns, two per slab, in A_IQ3XXS order), all 8
+    // scale bytes at 66, d at 0. B = (1 + 2 s) * grid * sign <= 31 * 43, an
+    // exact f16 integer, times the superblock's d / 8 (the unit d * 2^21).
+    constexpr bool IQ2 = KIND == 17, IQG = IQ2 || IQ3;
+    constexpr uint32_t IQB = IQ2 ? 74u : 98u;
     constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
     constexpr uint32_t UNR = 4u;
     // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
@@ -1731,12 +1739,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
             if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
             if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
-            if constexpr (IQ3) {
-                const uint32_t u = (bsoff[nb] + sb * 98u) & ~3u;
+            if constexpr (IQG) {
+                const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
                 nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);
                 n5[nb] = buf_load4(rw, boff[nb] + 16u * kq, u + 16u);
-                const uint2 a = buf_load8(rw, boff[nb] + 8u * kq, u + 64u);
-                n3[nb] = make_uint3(a.x, a.y, buf_load4(rw, boff[nb] + 8u * kq, u + 72u));
+                // IQ3_XXS: the lane's two aux words at 66 + 8 kq; IQ2_XS: all 8 scale bytes at 66.
+                const uint32_t ao = IQ2 ? boff[nb] : boff[nb] + 8u * kq;
+                const uint2 a = buf_load8(rw, ao, u + 64u);
+                n3[nb] = make_uint3(a.x, a.y, buf_load4(rw, ao, u + 72u));
                 n_d[nb] = buf_load4(rw, boff[nb], u);
             }
         }
@@ -1764,12 +1774,12 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     };
     auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
-        if constexpr (IQ3) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
+        if constexpr (IQG) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
         return nhdr[nb].x;
     };
     auto unit = [](uint32_t bits) {
         const float d = half_bits_to_float(bits);
-        return d != 0.f ? d * (IQ3 ? 4194304.f : 16777216.f) : 1.f;
+        return d != 0.f ? d * (IQ2 ? 2097152.f : IQ3 ? 4194304.f : 16777216.f) : 1.f;
     };
     // Superblock state for the decode (and, at the superblock's end, the mins
     // and the unit change).
@@ -1789,7 +1799,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 if constexpr (Q5K) st.qh[nb] = nqh[nb];
                 st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 16777216.f;
                 if (half_bits_to_float(nhdr[nb].x) == 0.f) st.sc[nb][0] = st.sc[nb][1] = 0u;
-            } else if constexpr (IQ3) {
+            } else if constexpr (IQG) {
                 const bool odd = (sb & 1u) != 0u;
                 const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
                 const uint32_t v[3] = {n3[nb].x, n3[nb].y, n3[nb].z};
@@ -1822,6 +1832,21 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 }
                 fb[nb][0] = q4_operand(lx, ly, s0_);
                 fb[nb][1] = q4_operand(hx, hy, s1_);
+            } else if constexpr (IQ2) {
+                const uint32_t g = st.gw[nb][sq];  // codes 8 kq + 2 sq (low half) and + 1
+                const uint32_t sw = (kq < 2u ? st.aw[nb][0] : st.aw[nb][1]) >> (16u * (kq & 1u));
+                const uint32_t f = st.sc[nb][0] * (2u * ((sw >> (8u * (sq >> 1) + 4u * (sq & 1u))) & 15u) + 1u);
+                const uint32_t f2 = f | (f << 16);
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    const uint32_t code = (g >> (16 * gi)) & 0xffffu;
+                    const uint64_t e = lds_iq2xs_grid()[code & 511u];
+                    const uint4 m = lds_iq3_signmask()[code >> 9];
+                    const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
+                    fb[nb][gi] = __builtin_bit_cast(
+                        half8, make_uint4(mad_u16x2(bytes01(lo), f2, m.x), mad_u16x2(bytes23(lo), f2, m.y),
+                                          mad_u16x2(bytes01(hi), f2, m.z), mad_u16x2(bytes23(hi), f2, m.w)));
+                }
             } else if constexpr (IQ3) {
                 const uint32_t g = st.gw[nb][sq];
                 const uint32_t x = st.aw[nb][sq >> 1];
@@ -1864,7 +1889,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
     constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : 0u;
-    constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQ3 ? 5u * NB : 0u;
+    constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQG ? 5u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
         constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;
@@ -1970,7 +1995,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                             for (int mb = 0; mb < MBE; ++mb) {
                                 const uint32_t ar = mb * 16u + ln;
-                                const uint32_t ch = IQ3 ? 2u * kq + gi : 4u * gi + kq;
+                                const uint32_t ch = IQG ? 2u * kq + gi : 4u * gi + kq;
                                 const uint32_t off = ar * 64u + 8u * (ch ^ ((ar >> 1) & 7u));
                                 const half8 a = *reinterpret_cast<const half8*>(part ? &bl[off] : &bh[off]);
 #pragma unroll
@@ -2040,7 +2065,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                         // at the previous superblock's end, two barriers ago).
                         if (more) store_s(Ss[(sb + 1u) & 1u]);
                     }
-                } else if constexpr (IQ3) {
+                } else if constexpr (IQG) {
                     if (sq == 3) {
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) {
