@@ -253,13 +253,13 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 
 // Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K;
 // IQ2_XS and IQ3_XXS when their rows are a whole number of dwords (kdim % 512
-// == 0; their loads assume 4-byte aligned rows); IQ4_NL as the down projection only (its A
-// is act, which the gate/up kernel stores permuted for it).
+// == 0; their loads assume 4-byte aligned rows); IQ4_NL (its A is read permuted:
+// x as split by the dispatch, act as stored by the gate/up kernel).
 bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
     switch (kind) {
         case 12: case 13: return kdim % 256 == 0;
         case 17: case 18: return kdim % 512 == 0;
-        case 20: return !gateup && kdim % 64 == 0;
+        case 20: return kdim % 64 == 0;
         default: return false;
     }
 }
@@ -285,6 +285,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
             case 13: F16_GU(13)
             case 17: F16_GU(17)
             case 18: F16_GU(18)
+            case 20: F16_GU(20)
             default: return false;
         }
     } else {

@@ -1645,7 +1645,6 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20,
                   "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ3_XXS, IQ4_NL");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
-    static_assert(KIND != 20 || !GATEUP, "IQ4_NL is read with permuted A, which only act provides");
     constexpr int NB = 4;
     // Q5_K is Q4_K with a fifth bit per value (b[16 + k % 32] bit k / 32 of its
     // superblock, kernels/iq3_mix.metal:19-23): the same header, scales, mins
@@ -2155,8 +2154,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)),
-// stored in column order `order` (A_NATURAL or A_IQ3XXS, whose permutation
-// keeps runs of 4 columns together; H % 256 == 0 for the latter), and the
+// stored in column order `order` (A_NATURAL; A_IQ3XXS, whose permutation
+// keeps runs of 4 columns together, H % 256 == 0; or A_IQ4NL, which spreads
+// them 2 apart within each 32-column block), and the
 // natural 32-column sums xs [T][H/32] used by the Q4_K mins term.
 // x -> f16 hi + lo in the order `order`, and the natural 32-column sums; item
 // g covers x[4g, 4g + 4) (8 consecutive items per 32-column group, so the
@@ -2168,9 +2168,17 @@ __device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _
     const float4 v = live ? *reinterpret_cast<const float4*>(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float a[4] = {v.x, v.y, v.z, v.w};
     if (live) {
-        const uint64_t o = order == A_IQ3XXS ? (i & ~255ull) | a_pos<A_IQ3XXS>((uint32_t)i & 255u) : i;
+        if (order == A_IQ4NL) {  // the 4 columns land 2 apart
 #pragma unroll
-        for (int j = 0; j < 4; ++j) split_f16(a[j], xh[o + j], xl[o + j]);
+            for (int j = 0; j < 4; ++j) {
+                const uint64_t o = (i & ~31ull) | a_pos<A_IQ4NL>((uint32_t)(i + j) & 31u);
+                split_f16(a[j], xh[o], xl[o]);
+            }
+        } else {
+            const uint64_t o = order == A_IQ3XXS ? (i & ~255ull) | a_pos<A_IQ3XXS>((uint32_t)i & 255u) : i;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) split_f16(a[j], xh[o + j], xl[o + j]);
+        }
     }
     float s = (a[0] + a[1]) + (a[2] + a[3]);
     s += dpp_mov<0xb1>(s);
