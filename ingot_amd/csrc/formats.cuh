@@ -241,7 +241,7 @@ __device__ inline void stage_f16_tables() {
             for (int j = 0; j < 4; ++j) w[j] = (((s >> (2 * j)) & 1u) << 15) | (((s >> (2 * j + 1)) & 1u) << 31);
             lds_iq3_signmask()[i] = make_uint4(w[0], w[1], w[2], w[3]);
         }
-    } else if constexpr (KIND == 20) {
+    } else if constexpr (KIND == 20 || KIND == 23) {
         for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x)
             lds_iq4nl_pairs()[i] =
                 iq4nl_f16_bits(ingot_kvalues_iq4nl[i & 15u]) | (iq4nl_f16_bits(ingot_kvalues_iq4nl[i >> 4]) << 16);

@@ -1642,8 +1642,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows) {
-    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20,
-                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ3_XXS, IQ4_NL");
+    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 23,
+                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ3_XXS, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
     constexpr int NB = 4;
     // Q5_K is Q4_K with a fifth bit per value (b[16 + k % 32] bit k / 32 of its
@@ -1659,6 +1659,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // scale bytes at 66, d at 0. B = (1 + 2 s) * grid * sign <= 31 * 43, an
     // exact f16 integer, times the superblock's d / 8 (the unit d * 2^21).
     constexpr bool IQ2 = KIND == 17, IQG = IQ2 || IQ3;
+    // IQ4_XS takes IQ4_NL's path (B = the codebook value, a unit per 32-column
+    // block): its blocks' 16 quant bytes sit at 8 + 16 g of a 136-byte
+    // superblock (dword aligned), and a block's unit is d * (scale - 32), the
+    // 6-bit scale from the 8-byte superblock header read with each slab.
+    constexpr bool IQ4X = KIND == 23, IQN = IQ4 || IQ4X;
     constexpr uint32_t IQB = IQ2 ? 74u : 98u;
     constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
     constexpr uint32_t UNR = 4u;
@@ -1762,6 +1767,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * SBB + QOFF + 32u * (s & 3u));
                 nq[rs][nb].x = v.x;
                 nq[rs][nb].y = v.y;
+            } else if constexpr (IQ4X) {
+                const uint32_t u = bsoff[nb] + (s >> 2) * 136u, g0 = 2u * (s & 3u);
+                nq[rs][nb].x = buf_load4(rw, boff[nb] + 4u * kq, u + 8u + 16u * g0);
+                n1[rs][nb] = buf_load4(rw, boff[nb] + 4u * kq, u + 24u + 16u * g0);
+                nd[rs][nb] = buf_load8(rw, boff[nb], u);
             } else if constexpr (IQ4) {
                 const uint32_t u = bsoff[nb] + 36u * s;
                 const uint2 q = buf_load8(rw, boff[nb] + 4u * kq, u);
@@ -1861,9 +1871,24 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                                           mad_u16x2(bytes01(e1), f2, m.z), mad_u16x2(bytes23(e1), f2, m.w)));
                 }
             } else {
-                const uint32_t qa = __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u), qb = qv[nb].z;
+                uint32_t qa, qb;
+                float d0, d1;
+                if constexpr (IQ4X) {
+                    qa = qv[nb].x;
+                    qb = qv[nb].z;
+                    const float d = half_bits_to_float(dv[nb].x);
+                    const uint32_t g0 = 2u * sq, sh = dv[nb].x >> 16, sl = (dv[nb].y >> (8u * sq)) & 255u;
+                    const int s0 = (int)((sl & 15u) | (((sh >> (2u * g0)) & 3u) << 4)) - 32;
+                    const int s1 = (int)((sl >> 4) | (((sh >> (2u * g0 + 2u)) & 3u) << 4)) - 32;
+                    d0 = d * (float)s0;
+                    d1 = d * (float)s1;
+                } else {
+                    qa = __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u);
+                    qb = qv[nb].z;
+                    d0 = half_bits_to_float(dv[nb].x & 0xffffu);
+                    d1 = half_bits_to_float(dv[nb].y >> 16);
+                }
                 const uint32_t* const P = lds_iq4nl_pairs();
-                const float d0 = half_bits_to_float(dv[nb].x & 0xffffu), d1 = half_bits_to_float(dv[nb].y >> 16);
                 uint4 b0 = make_uint4(P[qa & 255u], P[(qa >> 8) & 255u], P[(qa >> 16) & 255u], P[qa >> 24]);
                 uint4 b1 = make_uint4(P[qb & 255u], P[(qb >> 8) & 255u], P[(qb >> 16) & 255u], P[qb >> 24]);
                 if (d0 == 0.f) b0 = make_uint4(0u, 0u, 0u, 0u);
@@ -1887,7 +1912,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     };
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
-    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : 0u;
+    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : IQ4X ? 3u * NB : 0u;
     constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQG ? 5u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
@@ -1895,7 +1920,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         // Two operand sets let the decode of slab s + 1 interleave with slab s's
         // MFMAs; with 3-4 row blocks the registers hold one set (IQ4_NL: two),
         // and the decode follows the MFMAs in program order.
-        constexpr uint32_t NFB = (IQ4 || MBE <= 2) ? 2u : 1u;
+        constexpr uint32_t NFB = (IQN || MBE <= 2) ? 2u : 1u;
         typedef __attribute__((address_space(3))) void lds_void;
         auto dma_a = [&](uint32_t buf, uint32_t s) {
 #pragma unroll
@@ -1915,7 +1940,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
         // Prologue: A(0) into buffer 0; B ring; header of superblock 0; decode B(0).
         dma_a(0u, 0u);
-        if constexpr (!IQ4) load_hdr(0);
+        if constexpr (!IQN) load_hdr(0);
         if constexpr (Q4K) {
             INGOT_LOAD_S(0u);
             store_s(Ss[0]);
@@ -1923,7 +1948,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
         for (uint32_t d = 0; d < DEPTH; ++d) load_slab(d, d);
         SbState cur, nxt;
-        if constexpr (!IQ4) take_hdr(cur, 0u);
+        if constexpr (!IQN) take_hdr(cur, 0u);
         half8 fb[NFB][NB][2];
         float dgs[NFB][NB][2];
         {
@@ -1932,7 +1957,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 qv[nb] = nq[0][nb];
-                if constexpr (IQ4) {
+                if constexpr (IQN) {
                     qv[nb].z = n1[0][nb];
                     dv[nb] = nd[0][nb];
                 }
@@ -1946,7 +1971,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
             for (uint32_t sq = 0; sq < UNR; ++sq) {
                 const uint32_t s = s0 + sq;
-                if constexpr (IQ4) {
+                if constexpr (IQN) {
                     if (s >= slabs) break;  // uniform
                 }
                 __syncthreads();  // A(s), S of this superblock visible; the other A buffer free
@@ -1965,20 +1990,20 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     qv[nb] = nq[rs][nb];
-                    if constexpr (IQ4) {
+                    if constexpr (IQN) {
                         qv[nb].z = n1[rs][nb];
                         dv[nb] = nd[rs][nb];
                     }
                 }
                 load_slab(rs, s + 1u + DEPTH);
-                if constexpr (!IQ4) {
+                if constexpr (!IQN) {
                     if (sq == 0) {
                         load_hdr(sb + 1);
                         if constexpr (Q4K) INGOT_LOAD_S(sb + 1u);
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (!IQ4) {
+                if constexpr (!IQN) {
                     if (sq == 3 && more) take_hdr(nxt, sb + 1u);
                 }
                 // Decode B(s + 1) while this slab's MFMAs issue.
@@ -1986,7 +2011,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 if (NFB == 2u && more) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[nb_], dgs[nb_]);
                 const _Float16* const bh = (sq & 1u) ? Ah1 : Ah0;
                 const _Float16* const bl = (sq & 1u) ? Al1 : Al0;
-                if constexpr (!IQ4) {
+                if constexpr (!IQN) {
 #pragma unroll
                     for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
@@ -2081,13 +2106,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 // stay in flight) before the barrier that publishes it; the slab's
                 // MFMAs stay on this side of it.
                 __builtin_amdgcn_sched_barrier(0);
-                if (sq == 0 && !IQ4) wait_vmcnt<B_PER_SLAB + B_PER_SB>();
+                if (sq == 0 && !IQN) wait_vmcnt<B_PER_SLAB + B_PER_SB>();
                 else wait_vmcnt<B_PER_SLAB>();
             }
         }
         // No A DMA may still be writing LDS when the block exits.
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-        if constexpr (IQ4) {
+        if constexpr (IQN) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
