@@ -221,9 +221,24 @@ __device__ inline uint32_t* lds_iq4nl_pairs() {
     return p;
 }
 __device__ inline uint32_t iq4nl_f16_bits(int v) { return v < 0 ? 0x8000u | (uint32_t)(-v) : (uint32_t)v; }
+// 8-bit sign masks (entry s: bit 2j of s in bit 15, bit 2j + 1 in bit 31 of
+// word j), for the formats with explicit sign bytes.
+__device__ inline uint4* lds_sign8mask() {
+    __shared__ uint4 m[256];
+    return m;
+}
+__device__ inline uint4 sign_mask8(uint32_t sg) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = (((sg >> (2 * j)) & 1u) << 15) | (((sg >> (2 * j + 1)) & 1u) << 31);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
 template <int KIND>
 __device__ inline void stage_f16_tables() {
-    if constexpr (KIND == 17) {
+    if constexpr (KIND == 22) {
+        for (uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) lds_iq2s_grid()[i] = ingot_iq2s_grid[i];
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_sign8mask()[i] = sign_mask8(i);
+    } else if constexpr (KIND == 17) {
         for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq2xs_grid()[i] = ingot_iq2xs_grid[i];
         for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
             const uint32_t s = ingot_ksign(i);
@@ -279,20 +294,10 @@ __device__ inline uint2* lds_iq3s_grid_h() {
     __shared__ uint2 g[512];
     return g;
 }
-__device__ inline uint4* lds_sign8mask() {
-    __shared__ uint4 m[256];
-    return m;
-}
 __device__ inline uint32_t f16_bits_of(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
 // Bytes 2j, 2j + 1 of a codebook entry as an f16 pair.
 __device__ inline uint32_t grid_pair_h(uint64_t g, int j) {
     return f16_bits_of((float)((g >> (16 * j)) & 255u)) | (f16_bits_of((float)((g >> (16 * j + 8)) & 255u)) << 16);
-}
-__device__ inline uint4 sign_mask8(uint32_t sg) {
-    uint32_t w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = (((sg >> (2 * j)) & 1u) << 15) | (((sg >> (2 * j + 1)) & 1u) << 31);
-    return make_uint4(w[0], w[1], w[2], w[3]);
 }
 template <int KIND>
 __device__ inline void stage_half_tables() {

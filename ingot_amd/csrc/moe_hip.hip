@@ -252,13 +252,13 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 }
 
 // Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K;
-// IQ2_XS and IQ3_XXS when their rows are a whole number of dwords (kdim % 512
+// IQ2_XS, IQ2_S and IQ3_XXS when their rows are a whole number of dwords (kdim % 512
 // == 0; their loads assume 4-byte aligned rows); IQ4_NL and IQ4_XS (A read permuted:
 // x as split by the dispatch, act as stored by the gate/up kernel).
 bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
     switch (kind) {
         case 12: case 13: return kdim % 256 == 0;
-        case 17: case 18: return kdim % 512 == 0;
+        case 17: case 18: case 22: return kdim % 512 == 0;
         case 20: return kdim % 64 == 0;
         case 23: return kdim % 256 == 0;
         default: return false;
@@ -267,7 +267,7 @@ bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
 
 // Column order of A that an f16 GEMM over weights of `kind` reads.
 int a_order(uint32_t kind) {
-    return (kind == 20 || kind == 23) ? A_IQ4NL : (kind == 17 || kind == 18) ? A_IQ3XXS : A_NATURAL;
+    return (kind == 20 || kind == 23) ? A_IQ4NL : (kind == 17 || kind == 18 || kind == 22) ? A_IQ3XXS : A_NATURAL;
 }
 
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
@@ -289,6 +289,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
             case 17: F16_GU(17)
             case 18: F16_GU(18)
             case 20: F16_GU(20)
+            case 22: F16_GU(22)
             case 23: F16_GU(23)
             default: return false;
         }
@@ -299,6 +300,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... 
             case 17: F16(17, A_NATURAL); return true;
             case 18: F16(18, A_NATURAL); return true;
             case 20: F16(20, A_NATURAL); return true;
+            case 22: F16(22, A_NATURAL); return true;
             case 23: F16(23, A_NATURAL); return true;
             default: return false;
         }

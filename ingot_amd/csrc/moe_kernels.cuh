@@ -1642,8 +1642,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows) {
-    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 23,
-                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ3_XXS, IQ4_NL, IQ4_XS");
+    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 22 || KIND == 23,
+                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
     constexpr int NB = 4;
     // Q5_K is Q4_K with a fifth bit per value (b[16 + k % 32] bit k / 32 of its
@@ -1658,13 +1658,17 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // 2 + 16 kq (8 codes: 64 columns, two per slab, in A_IQ3XXS order), all 8
     // scale bytes at 66, d at 0. B = (1 + 2 s) * grid * sign <= 31 * 43, an
     // exact f16 integer, times the superblock's d / 8 (the unit d * 2^21).
-    constexpr bool IQ2 = KIND == 17, IQG = IQ2 || IQ3;
+    // IQ2_S too (82-byte superblocks): lane kq's 8 index bytes at 2 + 8 kq
+    // and 8 sign bytes at 34 + 8 kq, the index high bits (66) and scales (74)
+    // of its two 32-value groups among the 16 bytes at 66; B = (1 + 2 s) *
+    // grid * sign <= 31 * 43 and the unit d * 2^21, as for IQ2_XS.
+    constexpr bool IQ2 = KIND == 17, IQ2S = KIND == 22, IQG = IQ2 || IQ2S || IQ3;
     // IQ4_XS takes IQ4_NL's path (B = the codebook value, a unit per 32-column
     // block): its blocks' 16 quant bytes sit at 8 + 16 g of a 136-byte
     // superblock (dword aligned), and a block's unit is d * (scale - 32), the
     // 6-bit scale from the 8-byte superblock header read with each slab.
     constexpr bool IQ4X = KIND == 23, IQN = IQ4 || IQ4X;
-    constexpr uint32_t IQB = IQ2 ? 74u : 98u;
+    constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : 98u;
     constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
     constexpr uint32_t UNR = 4u;
     // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
@@ -1735,7 +1739,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     uint4 nhdr[NB];
     uint2 nqh[Q5K ? NB : 1];
     uint32_t n5[NB], n_d[NB];
-    uint3 n3[NB];
+    uint3 n3[NB], ns3[IQ2S ? NB : 1];
     auto load_hdr = [&](uint32_t sb) {
         sb = sb < sbs ? sb : sbs - 1u;
 #pragma unroll
@@ -1743,7 +1747,16 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
             if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
             if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
-            if constexpr (IQG) {
+            if constexpr (IQ2S) {
+                const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
+                nhdr[nb] = buf_load16(rw, boff[nb], u + 64u);  // index high bits and scales
+                n5[nb] = buf_load4(rw, boff[nb], u + 80u);
+                const uint2 q = buf_load8(rw, boff[nb] + 8u * kq, u);
+                n3[nb] = make_uint3(q.x, q.y, buf_load4(rw, boff[nb] + 8u * kq, u + 8u));
+                const uint2 g = buf_load8(rw, boff[nb] + 8u * kq, u + 32u);
+                ns3[nb] = make_uint3(g.x, g.y, buf_load4(rw, boff[nb] + 8u * kq, u + 40u));
+                n_d[nb] = buf_load4(rw, boff[nb], u);
+            } else if constexpr (IQG) {
                 const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
                 nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);
                 n5[nb] = buf_load4(rw, boff[nb] + 16u * kq, u + 16u);
@@ -1788,7 +1801,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     };
     auto unit = [](uint32_t bits) {
         const float d = half_bits_to_float(bits);
-        return d != 0.f ? d * (IQ2 ? 2097152.f : IQ3 ? 4194304.f : 16777216.f) : 1.f;
+        return d != 0.f ? d * ((IQ2 || IQ2S) ? 2097152.f : IQ3 ? 4194304.f : 16777216.f) : 1.f;
     };
     // Superblock state for the decode (and, at the superblock's end, the mins
     // and the unit change).
@@ -1808,6 +1821,25 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 if constexpr (Q5K) st.qh[nb] = nqh[nb];
                 st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 16777216.f;
                 if (half_bits_to_float(nhdr[nb].x) == 0.f) st.sc[nb][0] = st.sc[nb][1] = 0u;
+            } else if constexpr (IQ2S) {
+                // gw: the lane's index words (0, 1) and sign words (2, 3);
+                // aw[0]: index high-bit bytes of its groups 2 kq, 2 kq + 1 in
+                // bits 0..15, their scale bytes in bits 16..31.
+                const bool odd = (sb & 1u) != 0u;
+                auto al = [&](uint32_t hi, uint32_t lo) { return odd ? hi : __builtin_amdgcn_alignbit(hi, lo, 16u); };
+                st.gw[nb][0] = al(n3[nb].y, n3[nb].x);
+                st.gw[nb][1] = al(n3[nb].z, n3[nb].y);
+                st.gw[nb][2] = al(ns3[nb].y, ns3[nb].x);
+                st.gw[nb][3] = al(ns3[nb].z, ns3[nb].y);
+                const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
+                uint32_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) h[i] = al(w[i + 1], w[i]);
+                const uint32_t sh = 16u * (kq & 1u);
+                const uint32_t qh16 = ((kq < 2u ? h[0] : h[1]) >> sh) & 0xffffu;
+                const uint32_t sc16 = ((kq < 2u ? h[2] : h[3]) >> sh) & 0xffffu;
+                st.aw[nb][0] = qh16 | (sc16 << 16);
+                st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
             } else if constexpr (IQG) {
                 const bool odd = (sb & 1u) != 0u;
                 const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
@@ -1841,6 +1873,26 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 }
                 fb[nb][0] = q4_operand(lx, ly, s0_);
                 fb[nb][1] = q4_operand(hx, hy, s1_);
+            } else if constexpr (IQ2S) {
+                // codes 8 kq + 2 sq + gi: byte l = 2 (sq & 1) + gi of index
+                // and sign word sq / 2, group 2 kq + sq / 2.
+                const uint32_t grp = sq >> 1;
+                const uint32_t qsw = st.gw[nb][grp], sgw = st.gw[nb][2u + grp];
+                const uint32_t qh = (st.aw[nb][0] >> (8u * grp)) & 255u;
+                const uint32_t sc = (st.aw[nb][0] >> (16u + 8u * grp)) & 255u;
+                const uint32_t f = st.sc[nb][0] * (2u * ((sc >> (4u * (sq & 1u))) & 15u) + 1u);
+                const uint32_t f2 = f | (f << 16);
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    const uint32_t l = 2u * (sq & 1u) + (uint32_t)gi;
+                    const uint32_t idx = ((qsw >> (8u * l)) & 255u) | (((qh >> (2u * l)) & 3u) << 8);
+                    const uint64_t e = lds_iq2s_grid()[idx];
+                    const uint4 m = lds_sign8mask()[(sgw >> (8u * l)) & 255u];
+                    const uint32_t lo = (uint32_t)e, hi = (uint32_t)(e >> 32);
+                    fb[nb][gi] = __builtin_bit_cast(
+                        half8, make_uint4(mad_u16x2(bytes01(lo), f2, m.x), mad_u16x2(bytes23(lo), f2, m.y),
+                                          mad_u16x2(bytes01(hi), f2, m.z), mad_u16x2(bytes23(hi), f2, m.w)));
+                }
             } else if constexpr (IQ2) {
                 const uint32_t g = st.gw[nb][sq];  // codes 8 kq + 2 sq (low half) and + 1
                 const uint32_t sw = (kq < 2u ? st.aw[nb][0] : st.aw[nb][1]) >> (16u * (kq & 1u));
@@ -1913,7 +1965,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
     constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : IQ4X ? 3u * NB : 0u;
-    constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQG ? 5u * NB : 0u;
+    constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQ2S ? 7u * NB : IQG ? 5u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
         constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;
