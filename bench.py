@@ -213,9 +213,12 @@ def extra_configs(gpu, args):
         if stages:
             log(f"  stages (us): " + ", ".join(f"{k} {v['us']:.1f} ({v['kernel']})" for k, v in stages.items()))
 
-    def single(name, spec, T, copies, xin, bound):
+    def single(name, spec, T, copies, xin, bound, mode=None):
         base = MoeLayer(gpu, spec)
         layers = [base] + [base.clone() for _ in range(copies - 1)]
+        if mode is not None:
+            for l in layers:
+                l.set_gemm_mode(mode)
         dx = gpu.to_device(xin)
         dout = gpu.buffer(4 * T * spec.hidden)
         dids = gpu.buffer(4 * T * spec.top_k)
@@ -263,6 +266,11 @@ def extra_configs(gpu, args):
     specq = CF.make_layer(2, 0, 2048, 512, 10, 512, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
                           shared_down_kind=Q2_0, shared_gated=True)
     single("IQ2_S/IQ3_S + IQ4_XS/Q2_0 shared mix b=1", specq, 1, 32, CF.inputs(2, 1, 2048), "hbm")
+    # Prefill of the same mix: IQ2_S gate/up on the f16 GEMM (IQ3_S down on the fp32 one), and
+    # the whole layer forced onto the fp32 GEMM for comparison.
+    from ingot_amd.moe import GEMM_FP32
+    single("IQ2_S/IQ3_S mix prefill 512", specq, 512, 4, CF.inputs(2, 512, 2048), "mfma")
+    single("IQ2_S/IQ3_S mix prefill 512, fp32 GEMM", specq, 512, 4, CF.inputs(2, 512, 2048), "mfma", GEMM_FP32)
     del specq
     # 48 independent layers, h <- h + MoE_l(RMSNorm_l(h)); one step = the whole stack.
     t0 = time.time()
