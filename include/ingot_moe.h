@@ -59,20 +59,36 @@ enum ingot_status {
     INGOT_INVALID = 1,
     INGOT_NONFINITE = 2,
     INGOT_DEVICE = 3,
-    INGOT_UNSUPPORTED = 4
+    INGOT_UNSUPPORTED = 4,
+    /* No counterpart in the reference (its fp32 kernels have no operand range
+     * limit): reported by ingot_ctx_check_device_flags when an operand of the
+     * split-f16 prefill GEMM left the range in which it is exact (see
+     * ingot_layer_set_gemm_mode). The outputs of the forwards since the last
+     * check are not valid; re-run them with INGOT_GEMM_FP32. */
+    INGOT_RANGE = 5
 };
 
-/* GGML type ids the kernels decode (src/gguf.rs:470-491 lists every id the
- * reference loader accepts; ingot_geometry answers for all of them). */
+/* GGML type ids the kernels decode: every id the reference loader accepts
+ * (src/gguf.rs:470-491; ingot_geometry answers for all of them). */
 enum ingot_kind {
     INGOT_F32 = 0,
     INGOT_F16 = 1,
     INGOT_Q4_0 = 2,
     INGOT_Q8_0 = 8,
+    INGOT_Q2_K = 10,
     INGOT_Q4_K = 12,
+    INGOT_Q5_K = 13,
+    INGOT_Q6_K = 14,
+    INGOT_IQ2_XXS = 16,
     INGOT_IQ2_XS = 17,
     INGOT_IQ3_XXS = 18,
-    INGOT_IQ4_NL = 20
+    INGOT_IQ4_NL = 20,
+    INGOT_IQ3_S = 21,
+    INGOT_IQ2_S = 22,
+    INGOT_IQ4_XS = 23,
+    INGOT_IQ1_M = 29,
+    INGOT_BF16 = 30,
+    INGOT_Q2_0 = 42
 };
 
 enum ingot_routing { INGOT_ROUTE_SOFTMAX = 0, INGOT_ROUTE_SIGMOID = 1 };
@@ -135,7 +151,8 @@ int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* 
 int ingot_route_batch(ingot_ctx* ctx, const float* d_logits, const float* d_bias, uint32_t T, uint32_t E,
                       uint32_t K, uint32_t routing, float scale, uint32_t* d_ids, float* d_weights);
 /* Synchronizes, reads and clears the device flags; INGOT_NONFINITE if a
- * kernel met a non-finite router logit since the last check. */
+ * kernel met a non-finite router logit since the last check, else INGOT_RANGE
+ * if a prefill forward's activations left the split-f16 range. */
 int ingot_ctx_check_device_flags(ingot_ctx* ctx);
 
 /* ---- resident layer ---- */
@@ -178,9 +195,17 @@ int ingot_layer_forward(ingot_layer* layer, const float* d_x, uint32_t T, float*
  * norm gain (else INGOT_INVALID); otherwise as ingot_layer_forward. */
 int ingot_layer_forward_add(ingot_layer* layer, const float* d_x, const float* d_a, uint32_t T, float* d_out,
                             uint32_t* d_ids, float* d_weights);
-/* Prefill GEMM arithmetic. INGOT_GEMM_AUTO (default): Q4_K experts use the
- * split-precision f16 MFMA GEMM (fp32-accurate to ~2^-21 relative; needs
- * |activations| < 65504), other formats the fp32 MFMA GEMM.
+/* Prefill GEMM arithmetic. INGOT_GEMM_AUTO (default): experts in Q4_K, Q5_K,
+ * IQ2_XS, IQ2_S, IQ3_XXS (rows of a multiple of 512 columns), IQ4_NL and
+ * IQ4_XS use the split-precision f16 MFMA GEMM (fp32-accurate to ~2^-21
+ * relative: each operand is scaled by a power of two per token and split into
+ * f16 hi + lo; the B operand is the format's integer), other formats the fp32
+ * MFMA GEMM. x may take any finite values. The activations are scaled by
+ * 2^(2 e_t - 15) (e_t the exponent that brings the token's max |x| into
+ * [2^10, 2^11)); when a row's max |act| so scaled leaves [2^-3, 2^14) (weights
+ * far from the usual size) the forward raises the device flag that
+ * ingot_ctx_check_device_flags reports as INGOT_RANGE, and its outputs must
+ * be recomputed with INGOT_GEMM_FP32.
  * INGOT_GEMM_FP32: always the fp32 MFMA GEMM. */
 enum ingot_gemm_mode { INGOT_GEMM_AUTO = 0, INGOT_GEMM_FP32 = 1 };
 int ingot_layer_set_gemm_mode(ingot_layer* layer, uint32_t mode);
@@ -208,6 +233,18 @@ int ingot_layer_time_stage(ingot_layer* layer, uint32_t stage, uint32_t reps, fl
 int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t stage, uint32_t reps, float* ms);
 /* Name of the HIP kernel that implements `stage` in the last forward. */
 const char* ingot_layer_stage_kernel(const ingot_layer* layer, uint32_t stage);
+/* The prefill dispatch of the last forward (synchronizes; INGOT_INVALID if that
+ * forward ran the decode kernels), P = T * K pairs: counts[E] and first[E]
+ * (expert_layout), pairs[P + S] (expert_pairs; S = T when the shared expert ran
+ * in the same GEMM launches, its rows P + t naming token t as t K, else 0),
+ * inverse[P], tiles[min(tiles_cap, info[2])][4] = {expert (E: the shared
+ * expert), first packed pair, n, number of non-empty tiles}; info[3] receives
+ * {P, S, length of the tile list}. pairs must hold P + T entries. The
+ * reference's counterparts are the layout, pairs and tile buffers of
+ * kernels/prefill.metal:7-38 (src/qwen_prefill.rs:30-116); this accessor exists
+ * for parity tests of those integer arrays. */
+int ingot_layer_dispatch_debug(ingot_layer* layer, uint32_t* counts, uint32_t* first, uint32_t* pairs,
+                               uint32_t* inverse, uint32_t* tiles, uint32_t tiles_cap, uint32_t* info);
 
 /* ---- device memory helpers (so callers without a tensor library can drive it) ---- */
 int ingot_malloc(ingot_ctx* ctx, uint64_t bytes, void** d_ptr);

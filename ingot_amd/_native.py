@@ -101,6 +101,7 @@ MOE_SYMBOLS = {
     "ingot_layer_time_stage": (I32, [P, U32, U32, PF32]),
     "ingot_layers_time_stage": (I32, [C.POINTER(P), U32, U32, U32, PF32]),
     "ingot_layer_stage_kernel": (C.c_char_p, [P, U32]),
+    "ingot_layer_dispatch_debug": (I32, [P, P, P, P, P, P, U32, P]),
     "ingot_malloc": (I32, [P, U64, C.POINTER(P)]),
     "ingot_free": (I32, [P, P]),
     "ingot_memcpy_h2d": (I32, [P, P, P, U64]),

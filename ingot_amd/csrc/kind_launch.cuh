@@ -50,7 +50,7 @@ static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t r
                             const DecGateUpArgs& a) {
 #define DGU(C, N, R)                                                                                          \
     hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F, \
-                       a.H, a.x, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags, a.act)
+                       a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags, a.act)
     if (rpw == 3) {
         if (cpl == 1 && np == 1) { DGU(1, 1, 3); return true; }
         return false;
@@ -72,7 +72,7 @@ bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw
     if constexpr (KIND == 17)
         if (a.E <= 512 && cpl == 1 && np == 2 && rpw == 2) {
             hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F,
-                               a.H, a.x, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags,
+                               a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags,
                                a.act);
             return true;
         }

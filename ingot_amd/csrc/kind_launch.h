@@ -40,7 +40,7 @@ struct DecGateUpArgs {
     const uint8_t *g, *u;
     uint64_t gs, us;
     uint32_t F, H;
-    const float *x, *logits, *bias;
+    const float *x, *xstat, *logits, *bias;
     uint32_t E, K, mode;
     float scale, limit;
     uint32_t *ids;

@@ -150,7 +150,7 @@ int upload(ingot_ctx* ctx, const T* h, uint64_t n, T** d) {
 
 bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_sg, const float* x,
                    const float* addend, const float* W, const float* sgvec, const float* gain, float eps,
-                   float* logits, float* sgl, float* xn, float* xs) {
+                   float* logits, float* sgl, float* xn, float* xs, float* xstat) {
     const uint32_t rows = E + (has_sg ? 1u : 0u);
     // Below 64 tokens one token and one router row per wave keeps the grid
     // wide (T x E / 4 blocks); from 64 tokens the 64-output transposed kernel.
@@ -159,7 +159,7 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
         // 16 experts per block when 32 would leave fewer than two blocks per CU
         const bool eb16 = (T + 7) / 8 * (E / 32) < 512;
         const dim3 grid((T + 7) / 8, E / (eb16 ? 16 : 32));
-#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV>), grid, dim3(256), 0, s, x, addend, W, sgvec, gain, eps, T, E, logits, sgl, xn, xs)
+#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV>), grid, dim3(256), 0, s, x, addend, W, sgvec, gain, eps, T, E, logits, sgl, xn, xs, xstat)
         if (HB == 8) {
             if (eb16) RT(8, 16);
             else RT(8, 32);
@@ -177,7 +177,7 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
     do {                                                                                                       \
         dim3 grid((T + TOK - 1) / TOK, gy);                                                                    \
         hipLaunchKernelGGL((k_router<TOK, HBV>), grid, dim3(64 * wpb), 0, s, x, addend, W, sgvec, gain, eps, T,  \
-                           E, epw, logits, sgl, xn, xs);                                                       \
+                           E, epw, logits, sgl, xn, xs, xstat);                                                 \
         return true;                                                                                           \
     } while (0)
     if (HB == 8) {
@@ -321,13 +321,13 @@ static uint32_t dec_gate_up_rows(uint32_t F, uint32_t T, uint32_t cpl, uint32_t 
 }
 
 static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const uint8_t* u, uint64_t gs,
-                               uint64_t us, uint32_t F, uint32_t H, uint32_t T, const float* x, const float* logits,
-                               const float* bias, uint32_t E, uint32_t K, uint32_t mode, float scale, float limit,
-                               uint32_t* ids, float* w, uint32_t* flags, float* act) {
+                               uint64_t us, uint32_t F, uint32_t H, uint32_t T, const float* x, const float* xstat,
+                               const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode,
+                               float scale, float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     dim3 grid((F + rpw - 1) / rpw, T);
-    const DecGateUpArgs a{g, u, gs, us, F, H, x, logits, bias, E, K, mode, scale, limit, ids, w, flags, act};
+    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act};
     switch (kind) {
 #define K_(KV) case KV: return launch_dec_gate_up_k<KV>(s, cpl, np, rpw, grid, a);
         INGOT_KINDS(K_)
@@ -367,6 +367,23 @@ static bool gemv_down(hipStream_t s, uint32_t kd, int ks, const DownArgs& a, uin
 // ------------------------------------------------------------------ layer
 enum Stage { ST_ROUTER = 0, ST_ROUTE = 1, ST_GATEUP = 2, ST_DOWN = 3, ST_COMBINE = 4, ST_DISPATCH = 5, ST_N = 6 };
 
+// Per-forward workspace: the device buffers the kernels use beyond the
+// inputs, outputs and weights, carved from one block of memory sized for a
+// number of tokens (the layer's own allocation, or the static scratch array
+// of the allocation-free forward).
+struct Ws {
+    float *xn = nullptr, *logits = nullptr, *sgl = nullptr, *wts = nullptr, *act = nullptr, *sact = nullptr,
+          *Y = nullptr;
+    uint32_t *ids = nullptr, *counts = nullptr, *first = nullptr, *tiles = nullptr, *pairs = nullptr,
+             *inverse = nullptr, *stiles = nullptr;
+    _Float16 *xh = nullptr, *xl = nullptr, *acth = nullptr, *actl = nullptr;
+    float *xs = nullptr, *acts = nullptr;  // 32-column sums of x and act (Q4_K mins term)
+    float* resid = nullptr;                 // x + a of ingot_layer_forward_add (the new residual stream)
+    float* xstat = nullptr;                 // per token {max |x|, ||x 2^e||}: scales of the f16 splits
+    uint32_t* rowmax = nullptr;             // per-row max |act| of the f16 GEMM (range check)
+    uint32_t tile_cap = 0, stile_cap = 0;
+};
+
 struct ingot_layer {
     ingot_ctx* ctx = nullptr;
     uint32_t H = 0, E = 0, K = 0, F = 0, SF = 0, routing = 0;
@@ -375,19 +392,16 @@ struct ingot_layer {
     uint32_t gemm_mode = INGOT_GEMM_AUTO;
     float *router = nullptr, *bias = nullptr, *sgvec = nullptr, *gain = nullptr;
     DevMatrix gate, up, down, sgate, sup, sdown;
-    // workspace
+    // the layer's own workspace, for up to cap_T tokens
     uint32_t cap_T = 0;
     void* ws = nullptr;
-    float *xn = nullptr, *logits = nullptr, *sgl = nullptr, *wts = nullptr, *act = nullptr, *sact = nullptr,
-          *Y = nullptr;
-    uint32_t *ids = nullptr, *counts = nullptr, *first = nullptr, *tiles = nullptr, *pairs = nullptr,
-             *inverse = nullptr, *stiles = nullptr;
-    _Float16 *xh = nullptr, *xl = nullptr, *acth = nullptr, *actl = nullptr;
-    float *xs = nullptr, *acts = nullptr;  // 32-column sums of x and act (Q4_K mins term)
-    float* resid = nullptr;                 // x + a of ingot_layer_forward_add (the new residual stream)
-    uint32_t tile_cap = 0, stile_cap = 0;
+    Ws w;
     std::function<void(hipStream_t)> stage[ST_N];
     const char* stage_name[ST_N] = {};
+    // the dispatch buffers of the last prefill forward (ingot_layer_dispatch_debug)
+    uint32_t last_T = 0, last_P = 0, last_S = 0, last_cap = 0;
+    bool last_prefill = false;
+    Ws last;
 };
 
 static void free_dev(ingot_layer* L) {
@@ -398,49 +412,57 @@ static void free_dev(ingot_layer* L) {
     if (L->ws) (void)hipFree(L->ws);
 }
 
-static int reserve(ingot_layer* L, uint32_t T) {
-    ingot_ctx* ctx = L->ctx;
-    if (T <= L->cap_T) return INGOT_OK;
+// Lays out the workspace of up to T tokens at base (nullptr: sizes only) and
+// returns its size in bytes.
+static uint64_t carve(const ingot_layer* L, uint32_t T, void* base, Ws* out) {
     const uint64_t P = (uint64_t)T * L->K;
     // With a shared expert, rows P..P+T-1 of the packed buffers (pairs, act,
     // Y) belong to it, and the tile list has room for its tiles.
     const uint64_t PS = P + (L->SF ? T : 0);
-    const uint32_t stile_cap = (T + TM - 1) / TM;
-    const uint32_t tile_cap = (uint32_t)((P + TM - 1) / TM + L->E + (L->SF ? stile_cap : 0));
+    Ws w;
+    w.stile_cap = (T + TM - 1) / TM;
+    w.tile_cap = (uint32_t)((P + TM - 1) / TM + L->E + (L->SF ? w.stile_cap : 0));
     struct Part {
         void** p;
         uint64_t bytes;
     };
-    std::vector<Part> parts = {
-        {(void**)&L->xn, 4ull * T * L->H},       {(void**)&L->logits, 4ull * T * L->E},
-        {(void**)&L->sgl, 4ull * T},             {(void**)&L->ids, 4ull * P},
-        {(void**)&L->wts, 4ull * P},             {(void**)&L->act, 4ull * P * L->F},
-        {(void**)&L->sact, 4ull * T * (L->SF ? L->SF : 1)},
-        {(void**)&L->Y, 4ull * PS * L->H},
-        {(void**)&L->counts, 4ull * L->E},       {(void**)&L->first, 4ull * L->E},
-        {(void**)&L->tiles, 16ull * tile_cap},   {(void**)&L->pairs, 4ull * PS},
-        {(void**)&L->inverse, 4ull * P},         {(void**)&L->stiles, 16ull * stile_cap},
-        {(void**)&L->xh, 2ull * T * L->H},      {(void**)&L->xl, 2ull * T * L->H},
-        {(void**)&L->acth, 2ull * PS * L->F},    {(void**)&L->actl, 2ull * PS * L->F},
-        {(void**)&L->xs, 4ull * T * (L->H / 32)}, {(void**)&L->acts, 4ull * PS * (L->F / 32)},
-        {(void**)&L->resid, L->has_norm ? 4ull * T * L->H : 0ull},
+    const Part parts[] = {
+        {(void**)&w.xn, 4ull * T * L->H},       {(void**)&w.logits, 4ull * T * L->E},
+        {(void**)&w.sgl, 4ull * T},             {(void**)&w.ids, 4ull * P},
+        {(void**)&w.wts, 4ull * P},             {(void**)&w.act, 4ull * P * L->F},
+        {(void**)&w.sact, 4ull * T * (L->SF ? L->SF : 1)},
+        {(void**)&w.Y, 4ull * PS * L->H},
+        {(void**)&w.counts, 4ull * L->E},       {(void**)&w.first, 4ull * L->E},
+        {(void**)&w.tiles, 16ull * w.tile_cap}, {(void**)&w.pairs, 4ull * PS},
+        {(void**)&w.inverse, 4ull * P},         {(void**)&w.stiles, 16ull * w.stile_cap},
+        {(void**)&w.xh, 2ull * T * L->H},       {(void**)&w.xl, 2ull * T * L->H},
+        {(void**)&w.acth, 2ull * PS * L->F},    {(void**)&w.actl, 2ull * PS * L->F},
+        {(void**)&w.xs, 4ull * T * (L->H / 32)}, {(void**)&w.acts, 4ull * PS * (L->F / 32)},
+        {(void**)&w.resid, L->has_norm ? 4ull * T * L->H : 0ull},
+        {(void**)&w.xstat, 8ull * T},            {(void**)&w.rowmax, 4ull * PS},
     };
-    uint64_t total = 0;
-    for (auto& p : parts) total += (p.bytes + 255) & ~255ull;
+    uint64_t off = 0;
+    for (const Part& p : parts) {
+        *p.p = base ? static_cast<char*>(base) + off : nullptr;
+        off += (p.bytes + 255) & ~255ull;
+    }
+    if (out) *out = w;
+    return off;
+}
+
+static int reserve(ingot_layer* L, uint32_t T) {
+    ingot_ctx* ctx = L->ctx;
+    if (T <= L->cap_T) return INGOT_OK;
+    const uint64_t total = carve(L, T, nullptr, nullptr);
     void* ws = nullptr;
     if (L->ws) (void)hipFree(L->ws);
     L->ws = nullptr;
     L->cap_T = 0;
+    L->w = Ws();
     HIP_TRY(ctx, hipMalloc(&ws, total));
     L->ws = ws;
-    uint64_t off = 0;
-    for (auto& p : parts) {
-        *p.p = static_cast<char*>(ws) + off;
-        off += (p.bytes + 255) & ~255ull;
-    }
+    carve(L, T, ws, &L->w);
     L->cap_T = T;
-    L->tile_cap = tile_cap;
-    L->stile_cap = stile_cap;
     return INGOT_OK;
 }
 
@@ -460,6 +482,7 @@ const char* ingot_status_string(int status) {
         case INGOT_NONFINITE: return "non-finite values";
         case INGOT_DEVICE: return "device failure";
         case INGOT_UNSUPPORTED: return "unsupported format or shape";
+        case INGOT_RANGE: return "operands outside the split-f16 range: use INGOT_GEMM_FP32";
         default: return "unknown status";
     }
 }
@@ -522,6 +545,9 @@ int ingot_ctx_check_device_flags(ingot_ctx* ctx) {
     HIP_TRY(ctx, hipMemcpy(&flags, ctx->d_flags, 4, hipMemcpyDeviceToHost));
     HIP_TRY(ctx, hipMemcpy(ctx->d_flags, &zero, 4, hipMemcpyHostToDevice));
     if (flags & FLAG_NONFINITE) return fail(ctx, INGOT_NONFINITE, "non-finite router logits");
+    if (flags & FLAG_RANGE)
+        return fail(ctx, INGOT_RANGE,
+                    "prefill activations outside the range of the split-f16 GEMM: re-run with INGOT_GEMM_FP32");
     return INGOT_OK;
 }
 
@@ -855,19 +881,22 @@ int ingot_layer_reserve(ingot_layer* L, uint32_t T) {
 // dispatch + grouped MFMA GEMM (prefill) kernels.
 static const uint32_t GEMV_MAX_PAIRS = 64;
 
+// The f16 GEMM addresses its A operands (x split: T rows of H; act split: P + T
+// rows of F) and their group sums with 32-bit byte offsets.
+static bool f16_gemm_fits(uint64_t kdim, uint64_t rows) { return 2ull * kdim * rows < (1ull << 32); }
+
+// One forward on the workspace w (sized for at least T tokens).
 // d_a != NULL (ingot_layer_forward_add, norm layers only): the router adds
-// d_a to d_x, normalises the sum and stores it to L->resid, which is then the
+// d_a to d_x, normalises the sum and stores it to w.resid, which is then the
 // residual the down / combine kernels add.
-static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uint32_t T, float* d_out,
+static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const float* d_a, uint32_t T, float* d_out,
                          uint32_t* d_ids, float* d_weights) {
     ingot_ctx* ctx = L->ctx;
-    int st = reserve(L, T);
-    if (st != INGOT_OK) return st;
     hipStream_t s = ctx->stream;
     const uint32_t H = L->H, E = L->E, K = L->K, F = L->F, SF = L->SF, P = T * K;
-    const float* xin = L->has_norm ? L->xn : d_x;
-    const float* res = L->has_norm ? (d_a ? L->resid : d_x) : nullptr;
-    const float* sgl = L->has_sgvec ? L->sgl : nullptr;
+    const float* xin = L->has_norm ? w.xn : d_x;
+    const float* res = L->has_norm ? (d_a ? w.resid : d_x) : nullptr;
+    const float* sgl = L->has_sgvec ? w.sgl : nullptr;
     for (auto& f : L->stage) f = nullptr;
 
     const bool hs_ = L->has_shared;
@@ -876,46 +905,47 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
     const uint32_t nv_ = K * (F / 32) + (fuse_shared ? SF / 32 : 0);
     const bool decode = P <= GEMV_MAX_PAIRS && K <= 2 * GU_WAVES && (uint64_t)K * F + (hs_ ? SF : 0) <= DOWN_LDS_FLOATS &&
                         (nv_ + 63) / 64 <= 8 && (!hs_ || fuse_shared || (SF / 32 + 63) / 64 <= 2) && H <= 4096;
+    uint32_t* flags = ctx->d_flags;
+    float* xstat = w.xstat;
 
-    // 1. router (+ RMSNorm, + shared gate logit)
+    // 1. router (+ RMSNorm, + shared gate logit, + per-token input maximum)
     {
         const float *x = d_x, *a = d_a, *W = L->router, *sgv = L->sgvec, *g = L->gain;
-        float *lg = L->logits, *sl = L->sgl, *xn = L->xn, *rs = L->resid;
+        float *lg = w.logits, *sl = w.sgl, *xn = w.xn, *rs = w.resid;
         float eps = L->eps;
         bool has_sg = L->has_sgvec;
         uint32_t HB = H / 256;
         L->stage[ST_ROUTER] = [=](hipStream_t ss) {
-            launch_router(ss, HB, T, E, has_sg, x, a, W, sgv, g, eps, lg, sl, xn, rs);
+            launch_router(ss, HB, T, E, has_sg, x, a, W, sgv, g, eps, lg, sl, xn, rs, xstat);
         };
         L->stage_name[ST_ROUTER] = "k_router";
     }
     // 2. route (prefill)
     if (!decode) {
-        const float *lg = L->logits, *b = L->bias;
-        uint32_t* ids = L->ids;
-        float* w = L->wts;
+        const float *lg = w.logits, *b = L->bias;
+        uint32_t* ids = w.ids;
+        float* wt = w.wts;
         uint32_t mode = L->routing;
         float scale = L->scale;
-        uint32_t* flags = ctx->d_flags;
         L->stage[ST_ROUTE] = [=](hipStream_t ss) {
-            launch_route(ss, lg, b, T, E, K, mode, scale, ids, w, flags);
+            launch_route(ss, lg, b, T, E, K, mode, scale, ids, wt, flags);
         };
         L->stage_name[ST_ROUTE] = "k_route";
     }
+    L->last_prefill = !decode;
     if (decode) {
         // router -> routed gate/up (block routing) [+ shared gate/up] -> down + combine
         const DevMatrix gate = L->gate, up = L->up, down = L->down, sgate = L->sgate, sup = L->sup, sdown = L->sdown;
-        uint32_t* ids = L->ids;
-        float* wts = L->wts;
-        float *act = L->act, *sact = L->sact, limit = L->limit;
-        const float *lg = L->logits, *b = L->bias;
+        uint32_t* ids = w.ids;
+        float* wts = w.wts;
+        float *act = w.act, *sact = w.sact, limit = L->limit;
+        const float *lg = w.logits, *b = L->bias;
         const uint32_t mode = L->routing;
         const float scale = L->scale;
-        uint32_t* flags = ctx->d_flags;
         const bool hs = hs_;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
-            launch_dec_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, T, xin, lg, b, E, K, mode,
-                               scale, limit, ids, wts, flags, act);
+            launch_dec_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, T, xin, xstat, lg, b, E, K,
+                               mode, scale, limit, ids, wts, flags, act);
             if (hs)
                 launch_gemv_gate_up(ss, sgate.kind, sgate.d, sup.d, sgate.stride, sup.stride, SF, H, T, xin, nullptr, 1,
                                     limit, sact);
@@ -936,13 +966,13 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
         L->stage_name[ST_DOWN] = "k_dec_down";
     } else {
         const DevMatrix gate = L->gate, up = L->up, down = L->down, sgate = L->sgate, sup = L->sup, sdown = L->sdown;
-        const uint32_t *ids = L->ids;
-        uint32_t *counts = L->counts, *first = L->first, *tiles = L->tiles, *pairs = L->pairs, *inverse = L->inverse,
-                 *stiles = L->stiles;
+        const uint32_t *ids = w.ids;
+        uint32_t *counts = w.counts, *first = w.first, *tiles = w.tiles, *pairs = w.pairs, *inverse = w.inverse,
+                 *stiles = w.stiles, *rowmax = w.rowmax;
         const uint32_t cap = (P + TM - 1) / TM + E, scap = (T + TM - 1) / TM;
         // Shared-expert rows of Y follow this call's P routed rows.
-        float *act = L->act, *sact = L->sact, *Y = L->Y, *Ys = L->Y + (uint64_t)P * H, limit = L->limit;
-        const float* wts = L->wts;
+        float *act = w.act, *sact = w.sact, *Y = w.Y, *Ys = w.Y + (uint64_t)P * H, limit = L->limit;
+        const float* wts = w.wts;
         bool hs = L->has_shared;
         // The f16 GEMM runs when both projections' formats allow it; the shared
         // expert then joins the same launches (as tile expert E over rows
@@ -951,7 +981,9 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
         // format allows it (a Q4_K_M layer's Q6_K down), gate/up runs on the
         // f16 GEMM writing fp32 act and the down projection on the fp32 GEMM,
         // over the same 64-token tiles.
-        const bool f16gu = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(gate.kind, H, true);
+        const uint64_t PS = (uint64_t)P + (hs ? T : 0u);
+        const bool f16gu = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(gate.kind, H, true) &&
+                           f16_gemm_fits(H, T) && f16_gemm_fits(F, PS);
         const bool f16 = f16gu && f16_gemm_kind(down.kind, F, false);
         const bool merge = f16 && hs && SF == F && sgate.kind == gate.kind && sup.kind == up.kind &&
                            sdown.kind == down.kind && sgate.stride == gate.stride && sup.stride == up.stride &&
@@ -960,8 +992,15 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
         const bool mins = f16 && (down.kind == 12 || down.kind == 13);
         const uint32_t tm = f16gu ? TM16 : TM;
         const uint32_t S = merge ? T : 0u, capf = cap + (merge ? scap : 0u), e_sh = merge ? E : 0xffffffffu;
-        _Float16 *xh = L->xh, *xl = L->xl, *acth = L->acth, *actl = L->actl;
-        float *xs = L->xs, *acts = L->acts;
+        _Float16 *xh = w.xh, *xl = w.xl, *acth = w.acth, *actl = w.actl;
+        float *xs = w.xs, *acts = w.acts;
+        // rows whose maxima the f16 gate/up raises (act split in the f16 GEMM's units)
+        uint32_t* rmx = f16 ? rowmax : nullptr;
+        const uint32_t nrow = f16 ? P + S : 0u;
+        L->last_T = T;
+        L->last_P = P;
+        L->last_S = S;
+        L->last_cap = capf;
         // Dispatch stage: expert grouping, and for the f16 GEMM the split of x
         // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
@@ -969,7 +1008,8 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
             const uint64_t n = f16gu ? (uint64_t)T * H : 0ull;
             const uint32_t nsplit = (uint32_t)((n / 4 + 1023) / 1024);
             hipLaunchKernelGGL(k_dispatch, dim3(1 + nsplit), dim3(1024), 0, ss, ids, P, E, tm, capf, counts, first, tiles,
-                               pairs, inverse, S, K, xin, n, xh, xl, xs, (uint32_t)xord);
+                               pairs, inverse, S, K, xin, n, xh, xl, xs, (uint32_t)xord, (const float*)xstat, H, rmx,
+                               nrow);
             if (hs && !merge)
                 hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
         };
@@ -980,7 +1020,8 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
                                       merge ? sgate.d : nullptr, merge ? sup.d : nullptr, e_sh, gate.stride, up.stride,
                                       F, H, (const _Float16*)xh, (const _Float16*)xl, (const float*)xs,
                                       (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit,
-                                      f16 ? (float*)nullptr : act, acth, actl, mins ? acts : nullptr, F / 64, T);
+                                      f16 ? (float*)nullptr : act, acth, actl, mins ? acts : nullptr, F / 64, T,
+                                      (const float*)xstat, rmx, flags);
             } else {
                 launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
                                   pairs, K, tiles, F, limit, act);
@@ -997,7 +1038,7 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
                                        down.stride, 0ull, H, F, (const _Float16*)acth, (const _Float16*)actl,
                                        (const float*)acts, (const uint32_t*)nullptr, K, (const uint32_t*)tiles, H, 0.f,
                                        Y, (_Float16*)nullptr, (_Float16*)nullptr, (float*)nullptr, H / 128,
-                                       (uint32_t)(P + S));
+                                       (uint32_t)(P + S), (const float*)xstat, rmx, flags);
             else
                 launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act,
                                    nullptr, K, tiles, H, 0.f, Y);
@@ -1006,18 +1047,22 @@ static int layer_forward(ingot_layer* L, const float* d_x, const float* d_a, uin
                                    nullptr, 1, stiles, H, 0.f, Ys);
         };
         L->stage_name[ST_DOWN] = f16 ? "k_gemm_f16<down>" : "k_gemm<down>";
+        // The f16 down GEMM's rows of Y are in the act units of their token.
+        const float* yscale = f16 ? xstat : nullptr;
+        const uint32_t shared_scaled = merge ? 1u : 0u;
         L->stage[ST_COMBINE] = [=](hipStream_t ss) {
             hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, ss, Y, hs ? Ys : nullptr,
-                               inverse, wts, sgl, res, T, H, K, d_out);
+                               inverse, wts, sgl, res, T, H, K, d_out, yscale, shared_scaled);
         };
         L->stage_name[ST_COMBINE] = "k_combine";
     }
+    L->last = w;
     const int order[] = {ST_ROUTER, ST_ROUTE, ST_DISPATCH, ST_GATEUP, ST_DOWN, ST_COMBINE};
     for (int i : order)
         if (L->stage[i]) L->stage[i](s);
     LAUNCH_CHECK(ctx);
-    if (d_ids) HIP_TRY(ctx, hipMemcpyAsync(d_ids, L->ids, 4ull * P, hipMemcpyDeviceToDevice, s));
-    if (d_weights) HIP_TRY(ctx, hipMemcpyAsync(d_weights, L->wts, 4ull * P, hipMemcpyDeviceToDevice, s));
+    if (d_ids) HIP_TRY(ctx, hipMemcpyAsync(d_ids, w.ids, 4ull * P, hipMemcpyDeviceToDevice, s));
+    if (d_weights) HIP_TRY(ctx, hipMemcpyAsync(d_weights, w.wts, 4ull * P, hipMemcpyDeviceToDevice, s));
     return INGOT_OK;
 }
 
@@ -1025,7 +1070,9 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
     if (!L) return INGOT_INVALID;
     CHECK_CTX(L->ctx);
     if (!d_x || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
-    return layer_forward(L, d_x, nullptr, T, d_out, d_ids, d_weights);
+    const int st = reserve(L, T);
+    if (st != INGOT_OK) return st;
+    return layer_forward(L, L->w, d_x, nullptr, T, d_out, d_ids, d_weights);
 }
 
 int ingot_layer_forward_add(ingot_layer* L, const float* d_x, const float* d_a, uint32_t T, float* d_out,
@@ -1034,7 +1081,9 @@ int ingot_layer_forward_add(ingot_layer* L, const float* d_x, const float* d_a, 
     CHECK_CTX(L->ctx);
     if (!d_x || !d_a || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
     if (!L->has_norm) return fail(L->ctx, INGOT_INVALID, "the residual add needs the layer's RMSNorm gain");
-    return layer_forward(L, d_x, d_a, T, d_out, d_ids, d_weights);
+    const int st = reserve(L, T);
+    if (st != INGOT_OK) return st;
+    return layer_forward(L, L->w, d_x, d_a, T, d_out, d_ids, d_weights);
 }
 
 int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t stage, uint32_t reps, float* ms) {
@@ -1082,6 +1131,29 @@ int ingot_layer_time_stage(ingot_layer* L, uint32_t stage, uint32_t reps, float*
 const char* ingot_layer_stage_kernel(const ingot_layer* L, uint32_t stage) {
     if (!L || stage >= ST_N || !L->stage[stage]) return "";
     return L->stage_name[stage];
+}
+
+int ingot_layer_dispatch_debug(ingot_layer* L, uint32_t* counts, uint32_t* first, uint32_t* pairs,
+                               uint32_t* inverse, uint32_t* tiles, uint32_t tiles_cap, uint32_t* info) {
+    if (!L) return INGOT_INVALID;
+    ingot_ctx* ctx = L->ctx;
+    CHECK_CTX(ctx);
+    if (!L->last_prefill || !L->stage[ST_DISPATCH])
+        return fail(ctx, INGOT_INVALID, "the last forward did not run the prefill dispatch");
+    if (!counts || !first || !pairs || !inverse || !tiles || !info)
+        return fail(ctx, INGOT_INVALID, "null output buffer");
+    const Ws& w = L->last;
+    const uint32_t n = std::min(tiles_cap, L->last_cap);
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemcpy(counts, w.counts, 4ull * L->E, hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, hipMemcpy(first, w.first, 4ull * L->E, hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, hipMemcpy(pairs, w.pairs, 4ull * (L->last_P + L->last_S), hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, hipMemcpy(inverse, w.inverse, 4ull * L->last_P, hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, hipMemcpy(tiles, w.tiles, 16ull * n, hipMemcpyDeviceToHost));
+    info[0] = L->last_P;
+    info[1] = L->last_S;
+    info[2] = L->last_cap;
+    return INGOT_OK;
 }
 
 // ---- graphs ----

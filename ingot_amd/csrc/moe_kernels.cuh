@@ -30,6 +30,57 @@ namespace ingot {
 
 constexpr int WAVE = 64;
 constexpr uint32_t FLAG_NONFINITE = 1u;
+// An operand of the split-f16 arithmetic left the range in which it is exact
+// (see ACT_EXP_C); the outputs of the forwards since the last check are not
+// valid, and the fp32 GEMM must be used for these inputs.
+constexpr uint32_t FLAG_RANGE = 2u;
+
+// ------------------------------------------- f16-split operand scaling
+// Every operand that is split into f16 hi + lo (x for the f16 GEMM and the
+// v_dot2 decode formats, the prefill activations, the decode activations of
+// the v_dot2 formats) is first multiplied by an exact power of two, so that
+// neither half overflows and the lo half stays out of the f16 subnormals for
+// every value within 2^13 of the largest.
+//   * x: per token, max|x_t| 2^e_t in [2^10, 2^11) (x_exp of the token's
+//     maximum, which the router stores). Its 32-column sums are then below
+//     2^16 and enter the Q4_K mins MFMA divided by 32.
+//   * decode activations (k_dec_down): per token, the same rule on the
+//     block's maximum.
+//   * prefill activations: the gate/up epilogue unscales g and u by 2^-e_t
+//     before the SwiGLU and stores act 2^a_t, a_t = act_exp(xstat[t]) =
+//     2 n_t + ACT_EXP_C with n_t = x_exp(||x_t||_2). g and u are products of
+//     weight rows with x, of the order of |w| ||x_t||_2 whatever the shape of
+//     x (one large component or many small ones), and the SwiGLU of the two
+//     of the order of their product, so this puts a row's values near 2^5 for
+//     weights of the usual size (N(0, 0.02) at H = 2048) whatever the scale of
+//     x. Its validity is checked, not assumed: the epilogue keeps each row's
+//     max |act| (rowmax), and the down GEMM raises FLAG_RANGE unless it is
+//     zero or in [ACT_RANGE_LO, ACT_RANGE_HI) (below, products of the lo half
+//     lose bits; above, the group sums could overflow). The combine multiplies
+//     the routed sum by 2^-a_t.
+// xstat[t] = {max |x_t|, ||x_t 2^e_t||_2} (the router writes it).
+constexpr int ACT_EXP_C = -7;
+constexpr float ACT_RANGE_HI = 16384.f;  // 2^14
+constexpr float ACT_RANGE_LO = 0.125f;   // 2^-3
+
+// e with m 2^e in [2^10, 2^11) for finite m > 0; 0 for zero or non-finite m.
+__device__ __forceinline__ int x_exp(float m) {
+    if (!(m > 0.f) || !isfinite(m)) return 0;
+    int k;
+    (void)frexpf(m, &k);  // m = f 2^k, f in [0.5, 1)
+    return 11 - k;
+}
+// Units exponent of a token's prefill activations (above), from its xstat.
+__device__ __forceinline__ int act_exp(float2 st) { return 2 * (x_exp(st.y) + x_exp(st.x)) + ACT_EXP_C; }
+__device__ __forceinline__ float2 ld_xstat(const float* xstat, uint32_t t) {
+    return reinterpret_cast<const float2*>(xstat)[t];
+}
+__device__ __forceinline__ float4 ldexp4(float4 a, int e) {
+    return make_float4(ldexpf(a.x, e), ldexpf(a.y, e), ldexpf(a.z, e), ldexpf(a.w, e));
+}
+__device__ __forceinline__ float max_abs4(float4 a) {
+    return fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+}
 
 // The xor butterfly v_l <- v_l + v_(l xor m), m = 32, 16, ..., 1: the router's
 // fixed reduction tree (det_math.h). Each partner value is fetched by an exact
@@ -69,6 +120,18 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return (r0 + r1) + (r2 + r3);
+}
+// Wave maximum of non-negative values (same DPP pattern).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_mov<0xb1>(v));
+    v = fmaxf(v, dpp_mov<0x4e>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 __device__ __forceinline__ float swiglu(float g, float u, float limit) {
@@ -356,6 +419,26 @@ __device__ __forceinline__ void add_residual(float (&xr)[NT][HB * 4], const floa
     }
 }
 
+// xstat[t] = {max |x_t|, ||x_t 2^e_t||_2} (e_t = x_exp(max)) of one token held
+// by a wave as the router holds it (HB * 4 values per lane); lane 0 stores.
+template <int HB>
+__device__ __forceinline__ void token_stats(const float (&xr)[HB * 4], float* __restrict__ xstat, uint32_t t,
+                                            uint32_t T, uint32_t lane) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < HB * 4; ++j) m = fmaxf(m, fabsf(xr[j]));
+    m = wave_max(m);
+    const int e = x_exp(m);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < HB * 4; ++j) {
+        const float v = ldexpf(xr[j], e);
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = wave_sum_dpp(ss);
+    if (lane == 0 && t < T) reinterpret_cast<float2*>(xstat)[t] = make_float2(m, sqrtf(ss));
+}
+
 // One wave per (group of TOK tokens, group of experts). Lane l holds the
 // columns 4l + 256i + c (i < HB = H/256, c < 4) of each of its tokens, which
 // is the slot layout of the fixed reduction order (det_math.h): each logit is
@@ -366,13 +449,16 @@ __device__ __forceinline__ void add_residual(float (&xr)[NT][HB * 4], const floa
 // and writes the normalised rows (block (.., 0), wave 0 only). With an
 // addend a the rows are x + a first (add_residual), stored to xs.
 // Expert index E (when sgvec != NULL) is the shared-expert gate vector: its
-// product goes to sgl[t].
+// product goes to sgl[t]. xstat[t] receives {max |x_t|, ||x_t 2^e_t||_2} of the
+// expert input (after the residual add and the norm; e_t = x_exp(max)),
+// written by wave 0 of the by == 0 blocks: the scales of the f16 splits.
 template <int TOK, int HB>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, const float* __restrict__ addend,
                                                 const float* __restrict__ W, const float* __restrict__ sgvec,
                                                 const float* __restrict__ gain, float eps, uint32_t T, uint32_t E,
                                                 uint32_t epw, float* __restrict__ logits, float* __restrict__ sgl,
-                                                float* __restrict__ xn, float* __restrict__ xs) {
+                                                float* __restrict__ xn, float* __restrict__ xs,
+                                                float* __restrict__ xstat) {
     INGOT_NO_CONTRACT
     constexpr uint32_t H = 256u * HB;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -430,6 +516,10 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ x, con
                         make_float4(xr[t][4 * i], xr[t][4 * i + 1], xr[t][4 * i + 2], xr[t][4 * i + 3]);
             }
         }
+    }
+    if (xstat && blockIdx.y == 0 && wave == 0) {
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) token_stats<HB>(xr[t], xstat, t0 + t, T, lane);
     }
     for (uint32_t k = 0; k < epw; ++k) {
         uint32_t e = e0 + k;
@@ -517,13 +607,15 @@ __device__ __forceinline__ float transpose_sum64(float (&v)[64], uint32_t lane) 
 // The block's router rows pass through LDS in double-buffered chunks of 4.
 // The residual add (addend: s written to xs by the by == 0 blocks), RMSNorm
 // (gain: written to xn by the by == 0 blocks) and the shared-expert gate logit
-// (sgvec: by == 0 blocks, wave_sum) are computed as in k_router.
+// (sgvec: by == 0 blocks, wave_sum) and the per-token input statistics (xstat:
+// by == 0 blocks) are computed as in k_router.
 template <int HB, int EB>
 __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, const float* __restrict__ addend,
                                                   const float* __restrict__ W, const float* __restrict__ sgvec,
                                                   const float* __restrict__ gain, float eps, uint32_t T, uint32_t E,
                                                   float* __restrict__ logits, float* __restrict__ sgl,
-                                                  float* __restrict__ xn, float* __restrict__ xs) {
+                                                  float* __restrict__ xn, float* __restrict__ xs,
+                                                  float* __restrict__ xstat) {
     INGOT_NO_CONTRACT
     constexpr uint32_t H = 256u * HB, Q = H / 4u;  // Q float4 per row
     constexpr int CH = 4;                         // router rows per LDS chunk
@@ -582,6 +674,10 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             acc = wave_sum(acc);
             if (lane == 0 && t0 + t < T) sgl[t0 + t] = acc;
         }
+    }
+    if (xstat && blockIdx.y == 0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) token_stats<HB>(xr[t], xstat, t0 + t, T, lane);
     }
     // Router rows e0 .. e0 + EB - 1 in NC chunks of 4 through LDS.
     constexpr uint32_t PER = CH * Q / 256u;  // float4 per thread per chunk
@@ -722,13 +818,16 @@ __device__ __forceinline__ void load_xh_ilv(const float4* __restrict__ s, uint32
 // block 0 write the token's ids and weights for the down kernel. Wave w
 // computes rows [RPW*bx, +RPW) of the gate and up projections and stores
 // w_k * SwiGLU(g, u) (the routing weight folded in for the down kernel);
-// each lane keeps its input chunks in registers.
+// each lane keeps its input chunks in registers. The formats with f16 input
+// pairs (half_x) split x 2^e_t (x_exp of the max in the router's xstat[t]) and
+// take 2^-e_t out of the row sums.
 constexpr uint32_t GU_WAVES = 8;
 
 template <int KIND, int CPL, int RPW, int NP, int NE>
 __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
                                                       uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
-                                                      const float* __restrict__ x, const float* __restrict__ logits,
+                                                      const float* __restrict__ x, const float* __restrict__ xstat,
+                                                      const float* __restrict__ logits,
                                                       const float* __restrict__ bias, uint32_t E, uint32_t K,
                                                       uint32_t sigmoid_mode, float scale, float limit,
                                                       uint32_t* __restrict__ ids, float* __restrict__ wts,
@@ -754,6 +853,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         xa[m] = xok[m] ? *reinterpret_cast<const float4*>(xt + Fm::col(c, 4u * (ji & 7u)))
                        : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    const float xm = HX ? xstat[2u * t] : 0.f;
     // decoded only after the barrier that publishes s_x4
     if constexpr (HX) stage_half_tables<KIND>();
     else stage_codebooks<KIND>();
@@ -800,9 +900,10 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             if (blockIdx.x == 0) ids[(uint64_t)t * K + k] = eid[n];
         }
     }
+    const int xe = x_exp(xm);
 #pragma unroll
     for (int m = 0; m < 2; ++m)
-        if (xok[m]) s_x4[threadIdx.x + 512u * m] = HX ? split_h4(xa[m]) : xa[m];
+        if (xok[m]) s_x4[threadIdx.x + 512u * m] = HX ? split_h4(ldexp4(xa[m], xe)) : xa[m];
     __syncthreads();
     // Routing weights in selection order; block 0's wave 0 publishes them.
     const float w = wave_route_weight(lane < K ? s_sv[lane] : 0.f, K, sigmoid_mode, scale);
@@ -854,7 +955,11 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
 #pragma unroll
             for (int i = 0; i < RPW; ++i) {
-                const float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
+                float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
+                if constexpr (HX) {
+                    g = ldexpf(g, -xe);
+                    u = ldexpf(u, -xe);
+                }
                 if (k < K && lane == (uint32_t)i && r0 + i < F)
                     act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit) * wk[n];
             }
@@ -967,30 +1072,50 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     }
     __builtin_amdgcn_sched_barrier(0);
     // 4. stage the activations (shared expert's times its gate) and each
-    //    chunk's two 16-value sums (xs0, xs1 of the formats' dot products)
+    //    chunk's two 16-value sums (xs0, xs1 of the formats' dot products).
+    //    Chunks of the f16-pair formats are split after scaling by 2^ea, ea
+    //    from the block's maximum over them (x_exp), and their dot products
+    //    are scaled back.
     const float gate = KS >= 0 ? (sgl ? ingot_det_sigmoid(sgv) : 1.0f) : 1.0f;
+    constexpr bool ANYH = HD || HS;
+    float amax = 0.f;
 #pragma unroll
     for (int m = 0; m < (int)DOWN_ACT4; ++m) {
         const uint32_t u = tid + DOWN_THREADS * m, v = u >> 3;
-        float4 a = av[m];
         if (KS >= 0 && v >= K * nchF) {
-            a.x *= gate;
-            a.y *= gate;
-            a.z *= gate;
-            a.w *= gate;
+            av[m].x *= gate;
+            av[m].y *= gate;
+            av[m].z *= gate;
+            av[m].w *= gate;
         }
+        if (ANYH && v < nv && (v < KC ? HD : HS)) amax = fmaxf(amax, max_abs4(av[m]));
+    }
+    int ea = 0;
+    if constexpr (ANYH) {
+        __shared__ float s_amax[DOWN_WAVES];
+        amax = wave_max(amax);
+        if (lane == 0) s_amax[wave] = amax;
+        __syncthreads();
+#pragma unroll
+        for (uint32_t w = 0; w < DOWN_WAVES; ++w) amax = fmaxf(amax, s_amax[w]);
+        ea = x_exp(amax);
+    }
+#pragma unroll
+    for (int m = 0; m < (int)DOWN_ACT4; ++m) {
+        const uint32_t u = tid + DOWN_THREADS * m, v = u >> 3;
+        const float4 a = av[m];
         const bool half = v < KC ? HD : HS;
-        if (v < nv) s_act4[ilv_slot(v, u & 7u)] = half ? split_h4(a) : a;
+        if (v < nv) s_act4[ilv_slot(v, u & 7u)] = half ? split_h4(ldexp4(a, ea)) : a;
         float g = (a.x + a.y) + (a.z + a.w);
         g = dpp_add<0xb1>(g);  // quad_perm [1,0,3,2]
         g = dpp_add<0x4e>(g);  // quad_perm [2,3,0,1]
         if ((u & 3u) == 0 && v < nv) s_sum[2u * v + ((u >> 2) & 1u)] = g;
     }
     __syncthreads();
-    // 5. the dot products
-    float acc[RPW];
+    // 5. the dot products (f16-pair chunks into acch, in units of 2^ea)
+    float acc[RPW], acch[RPW];
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) acc[i] = 0.f;
+    for (int i = 0; i < RPW; ++i) acc[i] = acch[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         if (!has[j]) continue;
@@ -1001,11 +1126,11 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
             for (int i = 0; i < RPW; ++i) {
                 if constexpr (HS && !UNI) {
                     if (isS[j]) {
-                        acc[i] += Fs::dot_raw_h(rs[UNI ? 0 : i][UNI ? 0 : j], xh, xl);
+                        acch[i] += Fs::dot_raw_h(rs[UNI ? 0 : i][UNI ? 0 : j], xh, xl);
                         continue;
                     }
                 }
-                if constexpr (HD) acc[i] += Fd::dot_raw_h(rd[i][j], xh, xl);
+                if constexpr (HD) acch[i] += Fd::dot_raw_h(rd[i][j], xh, xl);
             }
         } else {
             float xv[32];
@@ -1021,7 +1146,8 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     }
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-        float sum = wave_sum_dpp(acc[i]);
+        float sum = ANYH ? acc[i] + ldexpf(acch[i], -ea) : acc[i];
+        sum = wave_sum_dpp(sum);
         const uint32_t r = r0 + i;
         if (lane == (uint32_t)i && r < H) {
             if (res) sum += resv;
@@ -1178,10 +1304,12 @@ __device__ inline uint32_t block_exclusive_scan_1024(uint32_t v, uint32_t* wsum,
 //   ballots over the bits of the expert id. A wave reads its ids DSP_BATCH
 //   per lane at a time, all loads issued before the first is used.
 // Blocks 1.. (when xh != NULL) split the token inputs into f16 hi + lo for
-// the f16 GEMM (split_f16_part), beside the dispatch.
+// the f16 GEMM (split_f16_part), beside the dispatch. Block 0 also clears the
+// per-row activation maxima (rowmax[0 .. nrow)) that the gate/up GEMM raises.
 constexpr uint32_t DSP_BATCH = 8;
 __device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
-                                      _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g);
+                                      _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g,
+                                      const float* __restrict__ xstat, uint32_t H);
 
 #ifndef INGOT_KIND_UNIT  // compiled in moe_hip.hip only
 __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ ids, uint32_t P, uint32_t E,
@@ -1190,11 +1318,15 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
                                                    uint32_t* __restrict__ pairs, uint32_t* __restrict__ inverse,
                                                    uint32_t S, uint32_t K, const float* __restrict__ x, uint64_t xn,
                                                    _Float16* __restrict__ xh, _Float16* __restrict__ xl,
-                                                   float* __restrict__ xs, uint32_t xorder) {
+                                                   float* __restrict__ xs, uint32_t xorder,
+                                                   const float* __restrict__ xstat, uint32_t H,
+                                                   uint32_t* __restrict__ rowmax, uint32_t nrow) {
     if (blockIdx.x > 0) {
-        split_f16_part(x, xn, xh, xl, xs, xorder, (uint64_t)(blockIdx.x - 1u) * blockDim.x + threadIdx.x);
+        split_f16_part(x, xn, xh, xl, xs, xorder, (uint64_t)(blockIdx.x - 1u) * blockDim.x + threadIdx.x, xstat, H);
         return;
     }
+    if (rowmax)
+        for (uint32_t i = threadIdx.x; i < nrow; i += 1024u) rowmax[i] = 0u;
     __shared__ uint32_t hist[16][1024];  // per wave, per expert; then each wave's running position
     __shared__ uint32_t wsum[32];
     __shared__ uint32_t tot[3];
@@ -1641,7 +1773,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     uint32_t kdim, const _Float16* __restrict__ ah, const _Float16* __restrict__ al, const float* __restrict__ gs,
     const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
-    uint32_t nblk, uint32_t a_rows) {
+    uint32_t nblk, uint32_t a_rows, const float* __restrict__ xstat, uint32_t* __restrict__ rowmax,
+    uint32_t* __restrict__ flags) {
     static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 22 || KIND == 23,
                   "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
@@ -1711,6 +1844,27 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         const uint32_t q = q0 + (am < n ? am : 0u);
         const uint32_t r = GATEUP ? (pairs ? pairs[q] / K : q) : q;
         soff = 4u * (r * ngroups + 4u * ahalf);
+    }
+    // GATEUP: the split exponent e_t of each tile row's token and the units
+    // exponent a_t of its activations, for the epilogue (published by the main
+    // loop's first barrier). Down: row block 0 of each tile checks that its
+    // activation rows were split in range.
+    __shared__ int2 s_rowe[TM16];
+    if constexpr (GATEUP) {
+        if (tid < TM16) {
+            const uint32_t q = q0 + (tid < n ? tid : 0u);
+            const float2 st = ld_xstat(xstat, pairs ? pairs[q] / K : q);
+            s_rowe[tid] = make_int2(x_exp(st.x), act_exp(st));
+        }
+    } else {
+        if (rowmax != nullptr && slot - ti * nblk == 0u) {
+            bool bad = false;
+            if (tid < n) {
+                const float m = __uint_as_float(rowmax[q0 + tid]);
+                bad = !(m == 0.f || (m >= ACT_RANGE_LO && m < ACT_RANGE_HI));  // NaN: bad
+            }
+            if (__any(bad) && lane == 0u) atomicOr(flags, FLAG_RANGE);
+        }
     }
     const bool sh_tile = e == e_shared;
     const uint8_t* const wb0 = sh_tile ? ws0 : w0 + (uint64_t)e * rows_per_expert * stride0;
@@ -1819,7 +1973,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             if constexpr (Q4K) {
                 q4k_sc_mn(nhdr[nb], st.sc[nb][0], st.sc[nb][1], st.mn[nb][0], st.mn[nb][1]);
                 if constexpr (Q5K) st.qh[nb] = nqh[nb];
-                st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 16777216.f;
+                // dmin 2^24, times 32: the group sums enter the MFMA divided by 32
+                st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 536870912.f;
                 if (half_bits_to_float(nhdr[nb].x) == 0.f) st.sc[nb][0] = st.sc[nb][1] = 0u;
             } else if constexpr (IQ2S) {
                 // gw: the lane's index words (0, 1) and sign words (2, 3);
@@ -1953,12 +2108,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     };
 
-    // Q4_K group sums of this thread's row, split hi/lo, into an S buffer.
+    // Q4_K group sums of this thread's row divided by 32 (exact; they reach
+    // 2^16 for x and 2^19 for act within range), split hi/lo, into an S buffer.
     auto store_s = [&](_Float16* sb_) {
         const float v[4] = {ps.x, ps.y, ps.z, ps.w};
         _Float16 h[4], l[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) split_f16(v[j], h[j], l[j]);
+        for (int j = 0; j < 4; ++j) split_f16(v[j] * 0.03125f, h[j], l[j]);
         *reinterpret_cast<uint2*>(&sb_[am * 16u + 4u * ahalf]) = make_uint2(pack_h2(h[0], h[1]), pack_h2(h[2], h[3]));
         *reinterpret_cast<uint2*>(&sb_[am * 16u + 8u + 4u * ahalf]) = make_uint2(pack_h2(l[0], l[1]), pack_h2(l[2], l[3]));
     };
@@ -2179,15 +2335,28 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 const uint32_t m = mb * 16u + 4u * kq + j;
                 const uint64_t q = q0 + m;
                 if (GATEUP && AORD == A_F32) {
-                    const float v0 = swiglu(acc[mb][0][j], acc[mb][2][j], limit);
-                    const float v1 = swiglu(acc[mb][1][j], acc[mb][3][j], limit);
+                    const int e = s_rowe[m].x;
+                    const float v0 = swiglu(ldexpf(acc[mb][0][j], -e), ldexpf(acc[mb][2][j], -e), limit);
+                    const float v1 = swiglu(ldexpf(acc[mb][1][j], -e), ldexpf(acc[mb][3][j], -e), limit);
                     if (m < n) {
                         out[q * ldo + row0 + 32u * wave + ln] = v0;
                         out[q * ldo + row0 + 32u * wave + 16u + ln] = v1;
                     }
                 } else if (GATEUP) {
-                    const float v0 = swiglu(acc[mb][0][j], acc[mb][2][j], limit);
-                    const float v1 = swiglu(acc[mb][1][j], acc[mb][3][j], limit);
+                    // g, u in true units, then act 2^a_t
+                    const int e = s_rowe[m].x, ea = s_rowe[m].y;
+                    const float v0 =
+                        ldexpf(swiglu(ldexpf(acc[mb][0][j], -e), ldexpf(acc[mb][2][j], -e), limit), ea);
+                    const float v1 =
+                        ldexpf(swiglu(ldexpf(acc[mb][1][j], -e), ldexpf(acc[mb][3][j], -e), limit), ea);
+                    // the row's max |act| over the 16 lanes of this row (bit patterns
+                    // as integers: NaN stays above infinity)
+                    uint32_t rm = max(__float_as_uint(fabsf(v0)), __float_as_uint(fabsf(v1)));
+                    rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0xb1, 0xf, 0xf, false));
+                    rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x4e, 0xf, 0xf, false));
+                    rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x141, 0xf, 0xf, false));
+                    rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x140, 0xf, 0xf, false));
+                    if (rowmax != nullptr && m < n && ln == 0u) atomicMax(rowmax + q, rm);
                     _Float16 h0, l0, h1, l1;
                     split_f16(v0, h0, l0);
                     split_f16(v1, h1, l1);
@@ -2230,19 +2399,20 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #undef INGOT_LOAD_S
 }
 
-// x [T][H] fp32 -> xh, xl [T][H] f16 with x = xh + xl (+ O(2^-22 |x|)),
-// stored in column order `order` (A_NATURAL; A_IQ3XXS, whose permutation
-// keeps runs of 4 columns together, H % 256 == 0; or A_IQ4NL, which spreads
-// them 2 apart within each 32-column block), and the
-// natural 32-column sums xs [T][H/32] used by the Q4_K mins term.
-// x -> f16 hi + lo in the order `order`, and the natural 32-column sums; item
-// g covers x[4g, 4g + 4) (8 consecutive items per 32-column group, so the
+// x [T][H] fp32 -> xh, xl [T][H] f16 with x 2^e_t = xh + xl (+ O(2^-22 |x|)),
+// e_t = x_exp(max |x_t|) per token (xstat), stored in column order `order` (A_NATURAL;
+// A_IQ3XXS, whose permutation keeps runs of 4 columns together, H % 256 == 0;
+// or A_IQ4NL, which spreads them 2 apart within each 32-column block), and the
+// natural 32-column sums of x 2^e_t, xs [T][H/32], used by the Q4_K mins term.
+// Item g covers x[4g, 4g + 4) (8 consecutive items per 32-column group, so the
 // threads of a wave cover whole groups; n is a multiple of 32).
 __device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _Float16* __restrict__ xh,
-                                      _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g) {
+                                      _Float16* __restrict__ xl, float* __restrict__ xs, uint32_t order, uint64_t g,
+                                      const float* __restrict__ xstat, uint32_t H) {
     const uint64_t i = g * 4u;
     const bool live = i < n;
-    const float4 v = live ? *reinterpret_cast<const float4*>(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 v = live ? ldexp4(*reinterpret_cast<const float4*>(x + i), x_exp(xstat[2u * (i / H)]))
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
     const float a[4] = {v.x, v.y, v.z, v.w};
     if (live) {
         if (order == A_IQ4NL) {  // the 4 columns land 2 apart
@@ -2285,14 +2455,18 @@ __global__ void k_dense_tiles(uint32_t T, uint32_t cap, uint32_t* __restrict__ t
 // ------------------------------------------------------- prefill: combine
 // out[t][i] = sum_k w[t,k] Y[inverse[t*K+k]][i] in route order (kernels/prefill.metal:39),
 // + sigmoid(sgl[t]) (or 1) * Ys[t][i] for a shared expert, + res[t][i].
+// xstat != NULL: the f16 GEMM's rows of Y (the routed ones, and Ys when
+// shared_scaled) are in units of 2^a_t (act_exp) and are scaled back.
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, const float* __restrict__ Ys,
                                                  const uint32_t* __restrict__ inverse, const float* __restrict__ wts,
                                                  const float* __restrict__ sgl, const float* __restrict__ res,
-                                                 uint32_t T, uint32_t H, uint32_t K, float* __restrict__ out) {
+                                                 uint32_t T, uint32_t H, uint32_t K, float* __restrict__ out,
+                                                 const float* __restrict__ xstat, uint32_t shared_scaled) {
     // grid (ceil(H / 1024), T): the token is uniform in the block, so its
     // packed positions and weights are scalar loads.
     const uint32_t t = blockIdx.y, c = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
     if (c >= H) return;
+    const int ue = xstat ? -act_exp(ld_xstat(xstat, t)) : 0;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t k = 0; k < K; ++k) {
         const uint32_t p = t * K + k;
@@ -2300,9 +2474,11 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
         const float4 y = *reinterpret_cast<const float4*>(Y + (uint64_t)inverse[p] * H + c);
         s.x += w * y.x; s.y += w * y.y; s.z += w * y.z; s.w += w * y.w;
     }
+    s = ldexp4(s, ue);
     if (Ys) {
         const float w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
-        const float4 y = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
+        float4 y = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
+        if (shared_scaled) y = ldexp4(y, ue);
         s.x += y.x * w; s.y += y.y * w; s.z += y.z * w; s.w += y.w * w;
     }
     if (res) {

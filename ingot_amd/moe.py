@@ -25,7 +25,7 @@ import numpy as np
 
 from . import _native as N
 
-OK, INVALID, NONFINITE, DEVICE, UNSUPPORTED = 0, 1, 2, 3, 4
+OK, INVALID, NONFINITE, DEVICE, UNSUPPORTED, RANGE = 0, 1, 2, 3, 4, 5
 ROUTE_SOFTMAX, ROUTE_SIGMOID = 0, 1
 
 # GGML type ids (src/gguf.rs:470-491)
@@ -55,10 +55,16 @@ class DeviceError(RuntimeError):
     """A HIP failure; the context refuses further work (src/metal.rs:1349-1353)."""
 
 
+class OutOfRange(RuntimeError):
+    """INGOT_RANGE: a prefill forward's activations left the range of the
+    split-f16 GEMM; its outputs must be recomputed on the fp32 GEMM."""
+
+
 def _raise(status: int, msg: str) -> None:
     if status == OK:
         return
-    cls = {INVALID: InvalidData, NONFINITE: NonFinite, UNSUPPORTED: Unsupported}.get(status, DeviceError)
+    cls = {INVALID: InvalidData, NONFINITE: NonFinite, UNSUPPORTED: Unsupported,
+           RANGE: OutOfRange}.get(status, DeviceError)
     raise cls(msg)
 
 
@@ -360,8 +366,9 @@ class MoeLayer:
         return int(self.gpu.lib.ingot_layer_weight_bytes(self.handle))
 
     def set_gemm_mode(self, mode: int) -> None:
-        """GEMM_AUTO: split-precision f16 MFMA for Q4_K prefill; GEMM_FP32: fp32 MFMA."""
+        """GEMM_AUTO: split-precision f16 MFMA prefill for the formats that have it; GEMM_FP32: fp32 MFMA."""
         self.gpu._check(self.gpu.lib.ingot_layer_set_gemm_mode(self.handle, mode))
+        self._gemm_mode = mode
 
     def reserve(self, T: int) -> None:
         self.gpu._check(self.gpu.lib.ingot_layer_reserve(self.handle, T))
@@ -380,7 +387,9 @@ class MoeLayer:
                                                              weights.ptr if weights else None))
 
     def __call__(self, x: np.ndarray):
-        """Host convenience: out [T, H], ids [T, K], weights [T, K]."""
+        """Host convenience: out [T, H], ids [T, K], weights [T, K]. A forward
+        that reports INGOT_RANGE (activations outside the split-f16 range) is
+        recomputed on the fp32 GEMM; `last_fallback` tells whether it was."""
         x = _f32(x).reshape(-1, self.spec.hidden)
         T, H, K = x.shape[0], self.spec.hidden, self.spec.top_k
         if not np.isfinite(x).all():
@@ -391,7 +400,19 @@ class MoeLayer:
         dw = self.gpu.buffer(4 * T * K)
         self.forward(dx, T, dout, dids, dw)
         self.gpu.synchronize()
-        self.gpu.check_device_flags()
+        self.last_fallback = False
+        try:
+            self.gpu.check_device_flags()
+        except OutOfRange:
+            mode = getattr(self, "_gemm_mode", GEMM_AUTO)
+            self.set_gemm_mode(GEMM_FP32)
+            try:
+                self.forward(dx, T, dout, dids, dw)
+                self.gpu.synchronize()
+                self.gpu.check_device_flags()
+            finally:
+                self.set_gemm_mode(mode)
+            self.last_fallback = True
         out = dout.download(np.float32, T * H).reshape(T, H)
         if not np.isfinite(out).all():
             raise NonFinite("output contains non-finite values")
@@ -404,6 +425,22 @@ class MoeLayer:
 
     def stage_kernel(self, stage: int) -> str:
         return self.gpu.lib.ingot_layer_stage_kernel(self.handle, stage).decode()
+
+    def dispatch_debug(self, T: int) -> dict:
+        """The last prefill forward's dispatch arrays (ingot_layer_dispatch_debug)."""
+        E, P = self.spec.experts, T * self.spec.top_k
+        cap = P // 64 + E + T // 64 + 2
+        counts, first = np.zeros(E, np.uint32), np.zeros(E, np.uint32)
+        pairs, inverse = np.zeros(P + T, np.uint32), np.zeros(P, np.uint32)
+        tiles = np.zeros((cap, 4), np.uint32)
+        info = np.zeros(3, np.uint32)
+        self.gpu._check(self.gpu.lib.ingot_layer_dispatch_debug(
+            self.handle, counts.ctypes.data, first.ctypes.data, pairs.ctypes.data, inverse.ctypes.data,
+            tiles.ctypes.data, cap, info.ctypes.data))
+        P_, S, n = (int(v) for v in info)
+        assert P_ == P
+        return {"counts": counts, "first": first, "pairs": pairs[:P + S], "inverse": inverse, "shared_rows": S,
+                "tiles": tiles[:min(cap, n)]}
 
 
 def time_stage(layers: Sequence[MoeLayer], stage: int, reps: int) -> float:

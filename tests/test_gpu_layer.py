@@ -64,21 +64,60 @@ def test_c3_prefill_full(gpu, oracle):
     layer.destroy()
 
 
-def test_c4_two_stacked_layers(gpu, oracle):
-    specs = [CF.c4_layer(l) for l in range(2)]
+def test_c4_48_stacked_layers_and_one_graph(gpu, oracle):
+    """configs[4] at full depth: 48 independent C0-shaped layers with RMSNorm and
+    the residual add, h <- h + MoE_l(RMSNorm_l(h)), at batch 1 and 8.
+      * every layer against the oracle on the GPU's own input (ids exact,
+        outputs to the bar);
+      * the whole stack against the oracle's own 48-layer chain;
+      * one HIP graph holding all 48 layers (the reference encodes one command
+        buffer per decode token across layers, src/generic.rs:700-724),
+        replayed three times with other work between, bit-equal to eager."""
+    L = 48
+    specs = [CF.c4_layer(l) for l in range(L)]
     layers = [MoeLayer(gpu, s) for s in specs]
+    print("C4: 48 layers resident", flush=True)
     for T in (1, 8):
-        h = CF.inputs(4, T, 2048)
-        h_ref = h.copy()
+        h0 = CF.inputs(4, T, 2048)
+        h, h_ref = h0, h0
         for l, (layer, spec) in enumerate(zip(layers, specs)):
             out, ids, w = layer(h)
-            st, ref, rids, _ = oracle.moe_forward(spec, h, oracle.F64)
-            assert st == 0 and np.array_equal(ids, rids)
+            st, ref, rids, rw = oracle.moe_forward(spec, h, oracle.F64)
+            assert st == 0 and np.array_equal(ids, rids), f"C4 layer {l} T={T}: ids"
+            assert np.array_equal(w, rw), f"C4 layer {l} T={T}: routing weights"
             assert_close(out, ref, f"C4 layer {l} T={T}")
-            # continue from the GPU output so each layer is checked on identical input
-            h = out
             st, h_ref, _, _ = oracle.moe_forward(spec, h_ref, oracle.F64)
-        assert_close(h, h_ref, f"C4 two-layer stack T={T}")
+            h = out
+        m = assert_close(h, h_ref, f"C4 48-layer stack T={T}")
+        print(f"C4 T={T}: 48 layers ids exact; stack vs oracle chain max-abs {m[0]:.2e} rel-L2 {m[1]:.2e}", flush=True)
+        # eager on device buffers, then the same chain captured in one graph
+        din = gpu.to_device(h0)
+        bufs = [gpu.buffer(4 * T * 2048), gpu.buffer(4 * T * 2048)]
+
+        def chain():
+            src = din
+            for l, layer in enumerate(layers):
+                layer.forward(src, T, bufs[l & 1])
+                src = bufs[l & 1]
+            return bufs[(L - 1) & 1]
+        res = chain()
+        gpu.synchronize()
+        gpu.check_device_flags()
+        eager = res.download(np.float32, T * 2048).reshape(T, 2048)
+        assert np.array_equal(eager, h), f"C4 T={T}: device chain differs from the per-layer calls"
+        gpu.graph_begin()
+        res = chain()
+        g = gpu.graph_end()
+        for rep in range(3):
+            gpu.to_device(np.zeros(T * 2048, np.float32)).free()
+            bufs[0].upload(np.full(T * 2048, 3.0, np.float32))
+            bufs[1].upload(np.full(T * 2048, 5.0, np.float32))
+            g.launch()
+            gpu.synchronize()
+            got = res.download(np.float32, T * 2048).reshape(T, 2048)
+            assert np.array_equal(got, eager), f"C4 T={T}: graph replay {rep} differs from eager"
+        g.destroy()
+        print(f"C4 T={T}: one-graph 48-layer replays bit-equal to eager", flush=True)
     for layer in layers:
         layer.destroy()
 
@@ -221,8 +260,13 @@ def test_f16_gemm_formats_shared_and_zero_scales(gpu, oracle, gk, dk, sf):
     for m in (spec.gate, spec.up, spec.down, *spec.shared):
         zero_scales(m)
     layer = MoeLayer(gpu, spec)
+    from ingot_amd.moe import STAGE_DOWN, STAGE_GATEUP
     for T in (70, 130):  # 2 and 3 shared-expert tiles, partial last tiles
         check_layer(layer, spec, CF.inputs(9, T, 2048, seed=T), oracle, f"f16 {gk}/{dk} shared {sf} T={T}")
+        # both projections ran on the f16 GEMM (not a silent fp32 fallback)
+        assert layer.stage_kernel(STAGE_GATEUP) == "k_gemm_f16<gate_up>"
+        assert layer.stage_kernel(STAGE_DOWN) == "k_gemm_f16<down>"
+        assert not layer.last_fallback
     layer.destroy()
 
 

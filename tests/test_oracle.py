@@ -242,49 +242,67 @@ def iq2xs_block(d, codes, scales):
     return struct.pack("<H", f16(d)) + struct.pack("<32H", *codes) + bytes(scales)
 
 
+def _table(name):
+    """A table of ingot_amd/csrc/codebooks.h (pinned by test_codebook_checksums_against_reference_text)."""
+    import re
+    src = open(os.path.join(os.path.dirname(HERE), "ingot_amd", "csrc", "codebooks.h")).read()
+    m = re.search(name + r"\[(\d+)\]\s*=\s*\{(.*?)\};", src, re.S)
+    return [int(v.rstrip("uUlL"), 0) for v in re.findall(r"-?0x[0-9a-fA-F]+[uUlL]*|-?\d+", m.group(2))]
+
+
+def _ksign(i):
+    return i | ((bin(i).count("1") & 1) << 7)
+
+
 def test_iq2_xs_layout_probes(oracle):
-    """Code l of group g drives values 32g+8l..+7; its sign index negates per the
-    even-parity sign table; scale nibble (l/2) of byte 66+g scales them
-    (kernels/iq3_mix.metal:25-30)."""
+    """IQ2_XS (kernels/iq3_mix.metal:25-30): the u16 code at 2 + 2 (4 g + l)
+    drives values 32 g + 8 l .. + 7; value v is byte v of iq2xs_grid[code & 511],
+    negated where bit v of the even-parity sign entry ksign(code >> 9) is set,
+    times d (0.5 + nibble l / 2 of byte 66 + g) / 4. One random code and scale
+    per probe, every other code 0 (grid entry 0, no signs): all 256 values are
+    checked exactly, so a wrong code position, grid entry, byte order within an
+    entry, sign bit or scale nibble fails."""
+    grid = _table("ingot_iq2xs_grid")
     rng = np.random.default_rng(3)
-    for trial in range(48):
+    for trial in range(64):
         g, l = int(rng.integers(0, 8)), int(rng.integers(0, 4))
         gi, si, s = int(rng.integers(0, 512)), int(rng.integers(0, 128)), int(rng.integers(0, 16))
         codes = [0] * 32
         codes[4 * g + l] = gi | (si << 9)
-        scales = [0] * 8
-        scales[g] = s << (4 * (l // 2))
-        blk = row_of(IQ2_XS, iq2xs_block(1.0, codes, scales))
+        scales = [int(b) for b in rng.integers(0, 256, 8)]
+        d = 0.75
+        blk = row_of(IQ2_XS, iq2xs_block(d, codes, scales))
         vals = np.array([oracle.dequant_value(blk, IQ2_XS, j) for j in range(256)])
-        sub = vals[32 * g + 8 * l:32 * g + 8 * l + 8]
-        signs = si | ((bin(si).count("1") & 1) << 7)
-        mags = np.abs(sub) / ((0.5 + s) * 0.25)
-        assert set(np.round(mags).astype(int)) <= {8, 25, 43}
-        for v in range(8):
-            assert (sub[v] < 0) == bool(signs >> v & 1)
-        assert (np.count_nonzero(sub < 0) % 2) == 0
+        for j in range(256):
+            gg, ll, v = j // 32, (j % 32) // 8, j % 8
+            code = codes[4 * gg + ll]
+            sc = (scales[gg] >> (4 * (ll // 2))) & 15
+            mag = (grid[code & 511] >> (8 * v)) & 255
+            sign = -1.0 if _ksign(code >> 9) >> v & 1 else 1.0
+            assert vals[j] == sign * d * (0.5 + sc) * 0.25 * mag, (trial, j)
 
 
 def test_iq3_xxs_layout_probes(oracle):
+    """IQ3_XXS (kernels/iq3_mix.metal:31-35): value v of sub-block l of group g is
+    byte v % 4 of iq3xxs_grid[b[2 + 8 g + 2 l + v / 4]], negated where bit v of
+    ksign((aux_g >> 7 l) & 127) is set, times d (0.5 + (aux_g >> 28)) / 2 with
+    aux_g the u32 at 66 + 4 g. Two random grid bytes, sign index and scale per
+    probe, every other grid byte 0: all 256 values are checked exactly."""
+    grid = _table("ingot_iq3xxs_grid")
     rng = np.random.default_rng(4)
-    for trial in range(48):
+    for trial in range(64):
         g, l = int(rng.integers(0, 8)), int(rng.integers(0, 4))
         qs = [0] * 64
-        b0, b1 = int(rng.integers(0, 256)), int(rng.integers(0, 256))
-        qs[8 * g + 2 * l], qs[8 * g + 2 * l + 1] = b0, b1
-        si, s = int(rng.integers(0, 128)), int(rng.integers(0, 16))
-        aux = [0] * 8
-        aux[g] = (si << (7 * l)) | (s << 28)
-        blk = row_of(IQ3_XXS, struct.pack("<H", f16(2.0)) + bytes(qs) + struct.pack("<8I", *aux))
+        qs[8 * g + 2 * l], qs[8 * g + 2 * l + 1] = int(rng.integers(0, 256)), int(rng.integers(0, 256))
+        aux = [int(a) for a in rng.integers(0, 2 ** 32, 8, dtype=np.uint64)]
+        d = 2.0
+        blk = row_of(IQ3_XXS, struct.pack("<H", f16(d)) + bytes(qs) + struct.pack("<8I", *aux))
         vals = np.array([oracle.dequant_value(blk, IQ3_XXS, j) for j in range(256)])
-        sub = vals[32 * g + 8 * l:32 * g + 8 * l + 8]
-        signs = si | ((bin(si).count("1") & 1) << 7)
-        mags = np.abs(sub) / (2.0 * (0.5 + s) * 0.5)
-        assert set(np.round(mags).astype(int)) <= {4, 12, 20, 28, 36, 44, 52, 62}
-        for v in range(8):
-            assert (sub[v] < 0) == bool(signs >> v & 1)
-        # the other sub-blocks of the group share the scale; their grid byte 0 entry decodes too
-        assert np.isfinite(vals).all()
+        for j in range(256):
+            gg, ll, v = j // 32, (j % 32) // 8, j % 8
+            mag = (grid[qs[8 * gg + 2 * ll + v // 4]] >> (8 * (v % 4))) & 255
+            sign = -1.0 if _ksign((aux[gg] >> (7 * ll)) & 127) >> v & 1 else 1.0
+            assert vals[j] == sign * d * (0.5 + (aux[gg] >> 28)) * 0.5 * mag, (trial, j)
 
 
 def test_codebook_checksums_against_reference_text():
