@@ -188,6 +188,21 @@ int ingot_layer_reserve(ingot_layer* layer, uint32_t T);
  * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL. */
 int ingot_layer_forward(ingot_layer* layer, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
                         float* d_weights);
+/* No counterpart in the reference: the same forward as ingot_layer_forward for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc or
+ * hipFree: its workspace is a static device array of 32 MiB (33554432 bytes)
+ * per GPU, held from the library's first context on that GPU until the
+ * process ends, and T is limited to what fits (ingot_layer_static_bytes; a
+ * larger T is INGOT_INVALID): every decode and MTP-verify batch of the
+ * configurations here, and prefill up to about 200 tokens of a
+ * Qwen3-30B-A3B-shaped layer. Every static forward on one GPU shares that
+ * array, so calls that overlap on one GPU (other streams, other threads, other
+ * contexts) race; the array keeps the last call's contents. */
+int ingot_layer_forward_static(ingot_layer* layer, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
+                               float* d_weights);
+/* Bytes of workspace a forward of T tokens of this layer uses. */
+uint64_t ingot_layer_static_bytes(const ingot_layer* layer, uint32_t T);
 /* out[T][H] = s + MoE(RMSNorm(s)) with s = x + a: the residual add before the
  * pre-FFN norm fused into the router, replacing add_rms (kernels/generic.metal:
  * 390-405, called as rms(x, Some(a), ffn_norm) at src/generic.rs:716-724)

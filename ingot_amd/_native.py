@@ -91,6 +91,8 @@ MOE_SYMBOLS = {
     "ingot_layer_reserve": (I32, [P, U32]),
     "ingot_layer_forward": (I32, [P, P, U32, P, P, P]),
     "ingot_layer_forward_add": (I32, [P, P, P, U32, P, P, P]),
+    "ingot_layer_forward_static": (I32, [P, P, U32, P, P, P]),
+    "ingot_layer_static_bytes": (U64, [P, U32]),
     "ingot_layer_weight_bytes": (U64, [P]),
     "ingot_layer_set_gemm_mode": (I32, [P, U32]),
     "ingot_graph_begin": (I32, [P]),

@@ -26,7 +26,17 @@ struct ingot_ctx {
     std::string err;
     std::string name;
     uint32_t* d_flags = nullptr;
+    void* scratch = nullptr;  // this device's copy of `scratch` (hipGetSymbolAddress)
 };
+
+// Workspace of the allocation-free forward (ingot_layer_forward_static): one
+// copy per device, held by every GPU the library runs on until the process
+// ends. Host code never passes the array's name to a kernel (in host code it is
+// a stand-in, not a device address): ingot_ctx_create looks up this device's
+// address once with hipGetSymbolAddress and keeps it in ctx->scratch. All
+// static forwards on one GPU share it, so calls that overlap on one GPU race.
+constexpr uint64_t STATIC_SCRATCH_BYTES = 32ull << 20;
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
 
 struct ingot_graph {
     hipGraph_t graph = nullptr;
@@ -508,6 +518,9 @@ int ingot_ctx_create(int device, ingot_ctx** out) {
     ctx->stream = ctx->own;
     if (bad(hipMalloc(&ctx->d_flags, 256))) return INGOT_DEVICE;
     if (bad(hipMemset(ctx->d_flags, 0, 256))) return INGOT_DEVICE;
+    void* sp = nullptr;
+    if (bad(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch))) || !sp) return INGOT_DEVICE;
+    ctx->scratch = sp;
     *out = ctx;
     return INGOT_OK;
 }
@@ -1073,6 +1086,25 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
     const int st = reserve(L, T);
     if (st != INGOT_OK) return st;
     return layer_forward(L, L->w, d_x, nullptr, T, d_out, d_ids, d_weights);
+}
+
+int ingot_layer_forward_static(ingot_layer* L, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
+                               float* d_weights) {
+    if (!L) return INGOT_INVALID;
+    CHECK_CTX(L->ctx);
+    if (!d_x || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
+    const uint64_t need = carve(L, T, nullptr, nullptr);
+    if (need > STATIC_SCRATCH_BYTES)
+        return fail(L->ctx, INGOT_INVALID,
+                    std::to_string(T) + " tokens need " + std::to_string(need) +
+                        " bytes of workspace; the static scratch holds " + std::to_string(STATIC_SCRATCH_BYTES));
+    Ws w;
+    carve(L, T, L->ctx->scratch, &w);
+    return layer_forward(L, w, d_x, nullptr, T, d_out, d_ids, d_weights);
+}
+
+uint64_t ingot_layer_static_bytes(const ingot_layer* L, uint32_t T) {
+    return L && T ? carve(L, T, nullptr, nullptr) : 0ull;
 }
 
 int ingot_layer_forward_add(ingot_layer* L, const float* d_x, const float* d_a, uint32_t T, float* d_out,

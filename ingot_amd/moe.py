@@ -379,6 +379,18 @@ class MoeLayer:
         self.gpu._check(self.gpu.lib.ingot_layer_forward(self.handle, x.ptr, T, out.ptr, ids.ptr if ids else None,
                                                          weights.ptr if weights else None))
 
+    def forward_static(self, x: DeviceBuffer, T: int, out: DeviceBuffer, ids: Optional[DeviceBuffer] = None,
+                       weights: Optional[DeviceBuffer] = None) -> None:
+        """forward() with the workspace in the library's static device array
+        (ingot_layer_forward_static): allocates nothing; T is limited by
+        static_bytes(T) <= 32 MiB; overlapping calls on one GPU race."""
+        self.gpu._check(self.gpu.lib.ingot_layer_forward_static(self.handle, x.ptr, T, out.ptr,
+                                                                ids.ptr if ids else None,
+                                                                weights.ptr if weights else None))
+
+    def static_bytes(self, T: int) -> int:
+        return int(self.gpu.lib.ingot_layer_static_bytes(self.handle, T))
+
     def forward_add(self, x: DeviceBuffer, a: DeviceBuffer, T: int, out: DeviceBuffer,
                     ids: Optional[DeviceBuffer] = None, weights: Optional[DeviceBuffer] = None) -> None:
         """out = s + MoE(RMSNorm(s)), s = x + a (norm layers): add_rms fused into the router."""
