@@ -13,7 +13,9 @@ import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 MOE_LIB = os.path.join(HERE, "libingot_moe.so")
-SYNTH_LIB = os.path.join(HERE, "libingot_synth.so")
+# INGOT_SYNTH_LIB: another build of synth.cpp (the host sanitizer build of
+# `make -C oracle sanitize`).
+SYNTH_LIB = os.environ.get("INGOT_SYNTH_LIB") or os.path.join(HERE, "libingot_synth.so")
 
 
 class NativeLibraryMissing(RuntimeError):

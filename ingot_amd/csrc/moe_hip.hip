@@ -136,9 +136,34 @@ struct DevMatrix {
     uint32_t kind = 0;
 };
 
+// Device allocations of one synchronous call, freed on every return path.
+struct DevScope {
+    std::vector<void*> p;
+    DevScope() = default;
+    DevScope(const DevScope&) = delete;
+    DevScope& operator=(const DevScope&) = delete;
+    ~DevScope() {
+        for (void* q : p) (void)hipFree(q);
+    }
+    template <typename T>
+    hipError_t alloc(T** d, uint64_t bytes) {
+        void* q = nullptr;
+        const hipError_t e = hipMalloc(&q, bytes);
+        if (e == hipSuccess) p.push_back(q);
+        *d = static_cast<T*>(q);
+        return e;
+    }
+};
+
 int upload_matrix(ingot_ctx* ctx, const ingot_matrix* m, DevMatrix* out) {
-    HIP_TRY(ctx, hipMalloc(&out->d, m->nbytes));
-    HIP_TRY(ctx, hipMemcpy(out->d, m->data, m->nbytes, hipMemcpyHostToDevice));
+    uint8_t* d = nullptr;
+    HIP_TRY(ctx, hipMalloc(&d, m->nbytes));
+    const hipError_t e = hipMemcpy(d, m->data, m->nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return fail(ctx, INGOT_DEVICE, std::string("hipMemcpy: ") + hipGetErrorString(e));
+    }
+    out->d = d;
     out->nbytes = m->nbytes;
     out->cols = m->cols;
     out->rows = m->rows;
@@ -148,10 +173,22 @@ int upload_matrix(ingot_ctx* ctx, const ingot_matrix* m, DevMatrix* out) {
     return INGOT_OK;
 }
 
+// An upload into a scope's allocation (freed with the scope).
+int upload_scoped(ingot_ctx* ctx, DevScope& sc, const ingot_matrix* m, DevMatrix* out) {
+    const int st = upload_matrix(ctx, m, out);
+    if (st == INGOT_OK) sc.p.push_back(out->d);
+    return st;
+}
+
 template <typename T>
 int upload(ingot_ctx* ctx, const T* h, uint64_t n, T** d) {
     HIP_TRY(ctx, hipMalloc(reinterpret_cast<void**>(d), sizeof(T) * n));
-    HIP_TRY(ctx, hipMemcpy(*d, h, sizeof(T) * n, hipMemcpyHostToDevice));
+    const hipError_t e = hipMemcpy(*d, h, sizeof(T) * n, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(*d);
+        *d = nullptr;
+        return fail(ctx, INGOT_DEVICE, std::string("hipMemcpy: ") + hipGetErrorString(e));
+    }
     return INGOT_OK;
 }
 
@@ -507,6 +544,8 @@ int ingot_ctx_create(int device, ingot_ctx** out) {
     ctx->device = device;
     auto bad = [&](hipError_t e) {
         if (e == hipSuccess) return false;
+        if (ctx->d_flags) (void)hipFree(ctx->d_flags);
+        if (ctx->own) (void)hipStreamDestroy(ctx->own);
         delete ctx;
         return true;
     };
@@ -643,19 +682,18 @@ int ingot_project(ingot_ctx* ctx, const ingot_matrix* m, const float* x, float* 
     if (!x || !y || m->count != 1 || !all_finite(x, m->cols)) return fail(ctx, INGOT_INVALID, "projection shape mismatch");
     CHECK_CTX(ctx);
     if (!supported(m->kind)) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+    DevScope sc;
     DevMatrix dm;
     float* d = nullptr;
-    int st = upload_matrix(ctx, m, &dm);
+    int st = upload_scoped(ctx, sc, m, &dm);
     if (st != INGOT_OK) return st;
-    HIP_TRY(ctx, hipMalloc(&d, 4ull * (m->cols + m->rows)));
+    HIP_TRY(ctx, sc.alloc(&d, 4ull * (m->cols + m->rows)));
     HIP_TRY(ctx, hipMemcpy(d, x, 4ull * m->cols, hipMemcpyHostToDevice));
     hipLaunchKernelGGL(k_project_generic, dim3((uint32_t)((m->rows + 3) / 4), 1), dim3(256), 0, ctx->stream, dm.d,
                        m->stride, m->kind, (uint32_t)m->cols, (uint32_t)m->rows, d, 0ull, d + m->cols);
     LAUNCH_CHECK(ctx);
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     HIP_TRY(ctx, hipMemcpy(y, d + m->cols, 4ull * m->rows, hipMemcpyDeviceToHost));
-    (void)hipFree(d);
-    (void)hipFree(dm.d);
     if (!all_finite(y, m->rows)) return fail(ctx, INGOT_NONFINITE, "output contains non-finite values");
     return INGOT_OK;
 }
@@ -664,19 +702,18 @@ int ingot_dequant(ingot_ctx* ctx, const ingot_matrix* m, float* out) {
     if (validate(m) != INGOT_OK || !out) return fail(ctx, INGOT_INVALID, "invalid quantized matrix layout");
     CHECK_CTX(ctx);
     if (!supported(m->kind)) return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
+    DevScope sc;
     DevMatrix dm;
-    int st = upload_matrix(ctx, m, &dm);
+    int st = upload_scoped(ctx, sc, m, &dm);
     if (st != INGOT_OK) return st;
     const uint64_t nrows = m->rows * m->count, n = nrows * m->cols;
     float* d = nullptr;
-    HIP_TRY(ctx, hipMalloc(&d, 4ull * n));
+    HIP_TRY(ctx, sc.alloc(&d, 4ull * n));
     hipLaunchKernelGGL(k_dequant_generic, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, ctx->stream, dm.d,
                        m->stride, m->kind, (uint32_t)m->cols, nrows, d);
     LAUNCH_CHECK(ctx);
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     HIP_TRY(ctx, hipMemcpy(out, d, 4ull * n, hipMemcpyDeviceToHost));
-    (void)hipFree(d);
-    (void)hipFree(dm.d);
     if (!all_finite(out, n)) return fail(ctx, INGOT_NONFINITE, "output contains non-finite values");
     return INGOT_OK;
 }
@@ -709,16 +746,17 @@ int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* 
             (has_shared && !supported(shared_gate->kind)))
             return fail(ctx, INGOT_UNSUPPORTED, "GGML type has no kernel here");
     const uint32_t F = (uint32_t)routed[0].rows, SF = has_shared ? (uint32_t)shared[0].rows : 0;
+    DevScope sc;
     DevMatrix dr[3], ds[3], dg;
     int st = INGOT_OK;
-    for (int i = 0; i < 3 && st == INGOT_OK; ++i) st = upload_matrix(ctx, &routed[i], &dr[i]);
-    for (int i = 0; i < 3 && st == INGOT_OK && has_shared; ++i) st = upload_matrix(ctx, &shared[i], &ds[i]);
-    if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, shared_gate, &dg);
+    for (int i = 0; i < 3 && st == INGOT_OK; ++i) st = upload_scoped(ctx, sc, &routed[i], &dr[i]);
+    for (int i = 0; i < 3 && st == INGOT_OK && has_shared; ++i) st = upload_scoped(ctx, sc, &shared[i], &ds[i]);
+    if (st == INGOT_OK && has_shared) st = upload_scoped(ctx, sc, shared_gate, &dg);
     if (st != INGOT_OK) return st;
     // scratch: x[H] w[K] g,u,a [K F] y [K H] sg,su,sa [SF] sy [H] slogit [1] out [H]
     const uint64_t n = H + K + 3ull * K * F + (uint64_t)K * H + 3ull * SF + H + 1 + H;
     float* d = nullptr;
-    HIP_TRY(ctx, hipMalloc(&d, 4 * n));
+    HIP_TRY(ctx, sc.alloc(&d, 4 * n));
     float *dx = d, *dw = dx + H, *g = dw + K, *u = g + (uint64_t)K * F, *a = u + (uint64_t)K * F,
           *y = a + (uint64_t)K * F, *sg = y + (uint64_t)K * H, *su = sg + SF, *sa = su + SF, *sy = sa + SF,
           *sl = sy + H, *dout = sl + 1;
@@ -745,12 +783,6 @@ int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* 
     LAUNCH_CHECK(ctx);
     HIP_TRY(ctx, hipStreamSynchronize(s));
     HIP_TRY(ctx, hipMemcpy(out, dout, 4 * H, hipMemcpyDeviceToHost));
-    (void)hipFree(d);
-    for (int i = 0; i < 3; ++i) {
-        (void)hipFree(dr[i].d);
-        if (ds[i].d) (void)hipFree(ds[i].d);
-    }
-    if (dg.d) (void)hipFree(dg.d);
     if (!all_finite(out, H)) return fail(ctx, INGOT_NONFINITE, "output contains non-finite values");
     return INGOT_OK;
 }

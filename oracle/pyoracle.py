@@ -12,7 +12,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "liboracle.so")
+# INGOT_ORACLE_LIB: another build of the same sources (the sanitizer build of
+# `make -C oracle sanitize`).
+LIB = os.environ.get("INGOT_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 OK, INVALID, NONFINITE = 0, 1, 2
 F64, F32 = 64, 32
