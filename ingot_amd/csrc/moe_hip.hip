@@ -317,38 +317,56 @@ int a_order(uint32_t kind) {
     return (kind == 20 || kind == 23) ? A_IQ4NL : (kind == 17 || kind == 18 || kind == 22) ? A_IQ3XXS : A_NATURAL;
 }
 
+// Formats with a 128-token-tile instantiation of the f16 GEMM (tt128):
+// Q4_K and Q5_K, whose B operands need no LDS tables.
+bool f16_tt128_kind(uint32_t kind) { return kind == 12 || kind == 13; }
+
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
-// projection's a_order).
+// projection's a_order); tt128: tiles of up to 128 tokens (f16_tt128_kind).
 template <bool GATEUP, typename... Args>
-bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, dim3 grid, Args... args) {
-#define F16(KV, AO) hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO>), grid, dim3(128), 0, s, args...)
-#define F16_GU(KV)                                          \
-    switch (aord) {                                         \
-        case A_IQ4NL: F16(KV, A_IQ4NL); return true;        \
-        case A_IQ3XXS: F16(KV, A_IQ3XXS); return true;      \
-        case A_F32: F16(KV, A_F32); return true;            \
-        default: F16(KV, A_NATURAL); return true;           \
+bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 grid, Args... args) {
+#define F16(KV, AO, TT) hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT>), grid, dim3(2 * TT), 0, s, args...)
+#define F16_GU(KV, TT)                                          \
+    switch (aord) {                                             \
+        case A_IQ4NL: F16(KV, A_IQ4NL, TT); return true;        \
+        case A_IQ3XXS: F16(KV, A_IQ3XXS, TT); return true;      \
+        case A_F32: F16(KV, A_F32, TT); return true;            \
+        default: F16(KV, A_NATURAL, TT); return true;           \
     }
     if constexpr (GATEUP) {
+        if (tt128) {
+            switch (kind) {
+                case 12: F16_GU(12, 128)
+                case 13: F16_GU(13, 128)
+                default: return false;
+            }
+        }
         switch (kind) {
-            case 12: F16_GU(12)
-            case 13: F16_GU(13)
-            case 17: F16_GU(17)
-            case 18: F16_GU(18)
-            case 20: F16_GU(20)
-            case 22: F16_GU(22)
-            case 23: F16_GU(23)
+            case 12: F16_GU(12, 64)
+            case 13: F16_GU(13, 64)
+            case 17: F16_GU(17, 64)
+            case 18: F16_GU(18, 64)
+            case 20: F16_GU(20, 64)
+            case 22: F16_GU(22, 64)
+            case 23: F16_GU(23, 64)
             default: return false;
         }
     } else {
+        if (tt128) {
+            switch (kind) {
+                case 12: F16(12, A_NATURAL, 128); return true;
+                case 13: F16(13, A_NATURAL, 128); return true;
+                default: return false;
+            }
+        }
         switch (kind) {
-            case 12: F16(12, A_NATURAL); return true;
-            case 13: F16(13, A_NATURAL); return true;
-            case 17: F16(17, A_NATURAL); return true;
-            case 18: F16(18, A_NATURAL); return true;
-            case 20: F16(20, A_NATURAL); return true;
-            case 22: F16(22, A_NATURAL); return true;
-            case 23: F16(23, A_NATURAL); return true;
+            case 12: F16(12, A_NATURAL, 64); return true;
+            case 13: F16(13, A_NATURAL, 64); return true;
+            case 17: F16(17, A_NATURAL, 64); return true;
+            case 18: F16(18, A_NATURAL, 64); return true;
+            case 20: F16(20, A_NATURAL, 64); return true;
+            case 22: F16(22, A_NATURAL, 64); return true;
+            case 23: F16(23, A_NATURAL, 64); return true;
             default: return false;
         }
     }
@@ -446,7 +464,7 @@ struct ingot_layer {
     std::function<void(hipStream_t)> stage[ST_N];
     const char* stage_name[ST_N] = {};
     // the dispatch buffers of the last prefill forward (ingot_layer_dispatch_debug)
-    uint32_t last_T = 0, last_P = 0, last_S = 0, last_cap = 0;
+    uint32_t last_T = 0, last_P = 0, last_S = 0, last_cap = 0, last_tm = 0;
     bool last_prefill = false;
     Ws last;
 };
@@ -1035,7 +1053,10 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
                            sdown.stride == down.stride;
         const int aord = f16 ? a_order(down.kind) : A_F32, xord = a_order(gate.kind);
         const bool mins = f16 && (down.kind == 12 || down.kind == 13);
-        const uint32_t tm = f16gu ? TM16 : TM;
+        // 128-token tiles when an expert can take more than 64 pairs (each takes at
+        // most one per token) and both projections have the TT 128 kernel.
+        const bool tt128 = f16 && T > TM && f16_tt128_kind(gate.kind) && f16_tt128_kind(down.kind);
+        const uint32_t tm = tt128 ? 2u * TM : TM;
         const uint32_t S = merge ? T : 0u, capf = cap + (merge ? scap : 0u), e_sh = merge ? E : 0xffffffffu;
         _Float16 *xh = w.xh, *xl = w.xl, *acth = w.acth, *actl = w.actl;
         float *xs = w.xs, *acts = w.acts;
@@ -1046,6 +1067,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         L->last_P = P;
         L->last_S = S;
         L->last_cap = capf;
+        L->last_tm = tm;
         // Dispatch stage: expert grouping, and for the f16 GEMM the split of x
         // into f16 hi/lo with its 32-column sums.
         L->stage[ST_DISPATCH] = [=](hipStream_t ss) {
@@ -1061,7 +1083,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         L->stage_name[ST_DISPATCH] = "k_dispatch";
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             if (f16gu) {
-                launch_gemm_f16<true>(ss, gate.kind, aord, dim3(8 * (F / 64) * ((capf + 7) / 8)), gate.d, up.d,
+                launch_gemm_f16<true>(ss, gate.kind, aord, tt128, dim3(8 * (F / 64) * ((capf + 7) / 8)), gate.d, up.d,
                                       merge ? sgate.d : nullptr, merge ? sup.d : nullptr, e_sh, gate.stride, up.stride,
                                       F, H, (const _Float16*)xh, (const _Float16*)xl, (const float*)xs,
                                       (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit,
@@ -1078,7 +1100,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         L->stage_name[ST_GATEUP] = f16gu ? "k_gemm_f16<gate_up>" : "k_gemm<gate_up>";
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
             if (f16)
-                launch_gemm_f16<false>(ss, down.kind, A_NATURAL, dim3(8 * (H / 128) * ((capf + 7) / 8)), down.d,
+                launch_gemm_f16<false>(ss, down.kind, A_NATURAL, tt128, dim3(8 * (H / 128) * ((capf + 7) / 8)), down.d,
                                        (const uint8_t*)nullptr, merge ? sdown.d : nullptr, (const uint8_t*)nullptr, e_sh,
                                        down.stride, 0ull, H, F, (const _Float16*)acth, (const _Float16*)actl,
                                        (const float*)acts, (const uint32_t*)nullptr, K, (const uint32_t*)tiles, H, 0.f,
@@ -1217,6 +1239,7 @@ int ingot_layer_dispatch_debug(ingot_layer* L, uint32_t* counts, uint32_t* first
     info[0] = L->last_P;
     info[1] = L->last_S;
     info[2] = L->last_cap;
+    info[3] = L->last_tm;
     return INGOT_OK;
 }
 

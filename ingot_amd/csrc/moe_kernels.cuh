@@ -1766,8 +1766,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // wait for this wave's A(s + 1) only (vector-memory loads complete in issue
 // order, so vmcnt counts the B loads issued after it), which the next barrier
 // publishes. Every A DMA has landed before the block exits.
-template <int KIND, bool GATEUP, int AORD>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
+//   TT (tile tokens) 64: 2 waves; wave w owns B rows (gate/up: gate and up rows
+// 32 w .. + 31 of the block's 64; down: rows 64 w .. + 63 of its 128) for all
+// 64 tokens, as 4 x 4 MFMA tiles. TT 128 (tiles of up to 128 pairs, for
+// batches in which an expert can take more than 64): 4 waves; wave w owns
+// gate and up rows 16 w .. + 15 (down: rows 32 w .. + 31) for all 128 tokens,
+// as 8 x 2 MFMA tiles. Each decoded B fragment then feeds 16 MFMAs instead of
+// 8 and each weight byte is fetched once per 128 tokens instead of 64; the A
+// slab (128 rows) is shared by the 4 waves through LDS.
+template <int KIND, bool GATEUP, int AORD, int TT>
+__global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ ws0,
     const uint8_t* __restrict__ ws1, uint32_t e_shared, uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
     uint32_t kdim, const _Float16* __restrict__ ah, const _Float16* __restrict__ al, const float* __restrict__ gs,
@@ -1778,7 +1786,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 22 || KIND == 23,
                   "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
-    constexpr int NB = 4;
+    static_assert(TT == 64 || TT == 128, "tiles of 64 or 128 tokens");
+    // NB: 16-row B blocks per wave (gate/up: HB = NB / 2 gate, HB up); NW waves.
+    constexpr int NB = TT == 128 ? 2 : 4;
+    constexpr uint32_t NW = TT / 32u, HB = NB / 2;
     // Q5_K is Q4_K with a fifth bit per value (b[16 + k % 32] bit k / 32 of its
     // superblock, kernels/iq3_mix.metal:19-23): the same header, scales, mins
     // and operand build, nibbles 32 bytes later in a 176-byte superblock, and
@@ -1809,8 +1820,8 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // reads (16 rows at one chunk) touch every bank once. Separate objects, so
     // that the compiler sees that a DMA into one never aliases reads of the
     // other. S tiles (Q4_K group sums) by superblock parity.
-    __shared__ _Float16 Ah0[TM16 * 64], Ah1[TM16 * 64], Al0[TM16 * 64], Al1[TM16 * 64];
-    __shared__ _Float16 Ss[2][TM16 * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
+    __shared__ _Float16 Ah0[TT * 64], Ah1[TT * 64], Al0[TT * 64], Al1[TT * 64];
+    __shared__ _Float16 Ss[2][TT * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
     const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk;
     const uint32_t t = ti * 8u + (blockIdx.x & 7u);
     if (t >= nt) return;
@@ -1827,13 +1838,13 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     const uint32_t row0 = (slot - ti * nblk) * (GATEUP ? 64u : 128u);
     const uint32_t ngroups = kdim / 32u;
 
-    // A DMA: instruction i of wave w fills tile rows 8 (2 i + w) .. + 7; lane l
-    // writes row r = 8 (2 i + w) + l / 8 at LDS slot l % 8, which holds chunk
+    // A DMA: instruction i of wave w fills tile rows 8 (NW i + w) .. + 7; lane l
+    // writes row r = 8 (NW i + w) + l / 8 at LDS slot l % 8, which holds chunk
     // (l % 8) ^ ((r >> 1) & 7) of the row (the swizzle of the fragment reads).
     uint32_t avo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t r = 8u * (2u * i + wave) + (lane >> 3);
+        const uint32_t r = 8u * (NW * i + wave) + (lane >> 3);
         const uint32_t q = q0 + (r < n ? r : 0u);
         const uint32_t arow = GATEUP ? (pairs ? pairs[q] / K : q) : q;
         avo[i] = 2u * (arow * kdim + 8u * ((lane & 7u) ^ ((r >> 1) & 7u)));
@@ -1849,9 +1860,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
     // exponent a_t of its activations, for the epilogue (published by the main
     // loop's first barrier). Down: row block 0 of each tile checks that its
     // activation rows were split in range.
-    __shared__ int2 s_rowe[TM16];
+    __shared__ int2 s_rowe[TT];
+    // TT 128 gate/up: each wave's 16-column halves of the act group sums
+    __shared__ float gpart[GATEUP && TT == 128 ? 4 : 1][TT];
     if constexpr (GATEUP) {
-        if (tid < TM16) {
+        if (tid < TT) {
             const uint32_t q = q0 + (tid < n ? tid : 0u);
             const float2 st = ld_xstat(xstat, pairs ? pairs[q] / K : q);
             s_rowe[tid] = make_int2(x_exp(st.x), act_exp(st));
@@ -1878,11 +1891,11 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         if (GATEUP) {
-            const uint32_t st = (uint32_t)(nb < 2 ? stride0 : stride1);
-            bsoff[nb] = (row0 + 32u * wave + 16u * (nb & 1)) * st;
+            const uint32_t st = (uint32_t)(nb < (int)HB ? stride0 : stride1);
+            bsoff[nb] = (row0 + 16u * HB * wave + 16u * (nb % HB)) * st;
             boff[nb] = ln * st;
         } else {
-            bsoff[nb] = (row0 + 64u * wave + 16u * nb) * (uint32_t)stride0;
+            bsoff[nb] = (row0 + 16u * NB * wave + 16u * nb) * (uint32_t)stride0;
             boff[nb] = ln * (uint32_t)stride0;
         }
     }
@@ -1898,7 +1911,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         sb = sb < sbs ? sb : sbs - 1u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
+            const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= (int)HB ? rw1 : rw0;
             if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
             if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
             if constexpr (IQ2S) {
@@ -1929,7 +1942,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         s = s < slabs ? s : slabs - 1u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= 2 ? rw1 : rw0;
+            const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= (int)HB ? rw1 : rw0;
             if constexpr (Q4K) {
                 const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * SBB + QOFF + 32u * (s & 3u));
                 nq[rs][nb].x = v.x;
@@ -2126,14 +2139,16 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
         constexpr int MBE = decltype(mbe_tag)::value;
         constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;
         // Two operand sets let the decode of slab s + 1 interleave with slab s's
-        // MFMAs; with 3-4 row blocks the registers hold one set (IQ4_NL: two),
-        // and the decode follows the MFMAs in program order.
-        constexpr uint32_t NFB = (IQN || MBE <= 2) ? 2u : 1u;
+        // MFMAs; with 3-4 row blocks of 4 B blocks the registers hold one set
+        // (IQ4_NL: two), and the decode follows the MFMAs in program order.
+        constexpr uint32_t NFB = (IQN || MBE <= 2 || NB == 2) ? 2u : 1u;
         typedef __attribute__((address_space(3))) void lds_void;
         auto dma_a = [&](uint32_t buf, uint32_t s) {
 #pragma unroll
-            for (int i = 0; i < MBE; ++i) {
-                const uint32_t roff = 8u * (2u * i + wave) * 64u;
+            // Row groups past the tile's 16 MBE rows (odd MBE at TT 128) are
+            // loaded too, from clamped rows into LDS rows nobody reads: no branch.
+            for (int i = 0; i < (2 * MBE + (int)NW - 1) / (int)NW; ++i) {
+                const uint32_t roff = 8u * (NW * i + wave) * 64u;
                 _Float16* const dh = (buf ? Ah1 : Ah0) + roff;
                 _Float16* const dl = (buf ? Al1 : Al0) + roff;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_h, (lds_void*)dh, 16, avo[i], 128u * s, 0, 0);
@@ -2141,7 +2156,9 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         };
         floatx4 acc[MBE][NB];
-        float dlast[NB] = {1.f, 1.f, 1.f, 1.f};
+        float dlast[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) dlast[j] = 1.f;
 #pragma unroll
         for (int i = 0; i < MBE; ++i)
 #pragma unroll
@@ -2212,11 +2229,14 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (!IQN) {
-                    if (sq == 3 && more) take_hdr(nxt, sb + 1u);
+                    // past the last superblock: the clamped header, never used
+                    if (sq == 3) take_hdr(nxt, sb + 1u);
                 }
                 // Decode B(s + 1) while this slab's MFMAs issue.
                 const uint32_t cb = NFB == 2u ? (sq & 1u) : 0u, nb_ = NFB == 2u ? cb ^ 1u : 0u;
-                if (NFB == 2u && more) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[nb_], dgs[nb_]);
+                // (after the last slab: a decode of clamped bytes that nothing reads;
+                // kept unconditional so that the decode shares a block with the MFMAs)
+                if (NFB == 2u) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[nb_], dgs[nb_]);
                 const _Float16* const bh = (sq & 1u) ? Ah1 : Ah0;
                 const _Float16* const bl = (sq & 1u) ? Al1 : Al0;
                 if constexpr (!IQN) {
@@ -2234,6 +2254,20 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                                 for (int nb = 0; nb < NB; ++nb)
                                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[cb][nb][gi], acc[mb][nb], 0, 0, 0);
                             }
+                    {
+                        // Issue order within the slab: PF A-fragment reads ahead, then
+                        // per fragment its NB MFMAs, the read PF fragments on and (with
+                        // two operand sets) a share of the next slab's B decode (VALU),
+                        // so that LDS latency and the decode hide behind the MFMAs.
+                        constexpr int NF = 4 * MBE, PF = 4, VPF = NFB == 2u ? (NB == 2 ? 2 : 4) : 0;
+                        __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+                        for (int f = 0; f < NF; ++f) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+                            if (f + PF < NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                            if (VPF > 0) __builtin_amdgcn_sched_group_barrier(0x002, VPF, 0);
+                        }
+                    }
                 } else {
 #pragma unroll
                     for (int gi = 0; gi < 2; ++gi) {
@@ -2259,7 +2293,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                             }
                     }
                 }
-                if (NFB == 1u && more) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[0], dgs[0]);
+                if (NFB == 1u) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[0], dgs[0]);
                 if constexpr (Q4K) {
                     if (sq == 3) {
                         half8 fm[NB];
@@ -2295,7 +2329,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                         cur = nxt;
                         // S of the next superblock into the other buffer (last read
                         // at the previous superblock's end, two barriers ago).
-                        if (more) store_s(Ss[(sb + 1u) & 1u]);
+                        store_s(Ss[(sb + 1u) & 1u]);  // past the last superblock: clamped, unread
                     }
                 } else if constexpr (IQG) {
                     if (sq == 3) {
@@ -2336,65 +2370,92 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2))) void k
                 const uint64_t q = q0 + m;
                 if (GATEUP && AORD == A_F32) {
                     const int e = s_rowe[m].x;
-                    const float v0 = swiglu(ldexpf(acc[mb][0][j], -e), ldexpf(acc[mb][2][j], -e), limit);
-                    const float v1 = swiglu(ldexpf(acc[mb][1][j], -e), ldexpf(acc[mb][3][j], -e), limit);
-                    if (m < n) {
-                        out[q * ldo + row0 + 32u * wave + ln] = v0;
-                        out[q * ldo + row0 + 32u * wave + 16u + ln] = v1;
+#pragma unroll
+                    for (int h = 0; h < (int)HB; ++h) {
+                        const float v = swiglu(ldexpf(acc[mb][h][j], -e), ldexpf(acc[mb][HB + h][j], -e), limit);
+                        if (m < n) out[q * ldo + row0 + 16u * HB * wave + 16u * h + ln] = v;
                     }
                 } else if (GATEUP) {
-                    // g, u in true units, then act 2^a_t
+                    // g, u in true units, then act 2^a_t; act column row0 + 16 HB w + 16 h + ln
                     const int e = s_rowe[m].x, ea = s_rowe[m].y;
-                    const float v0 =
-                        ldexpf(swiglu(ldexpf(acc[mb][0][j], -e), ldexpf(acc[mb][2][j], -e), limit), ea);
-                    const float v1 =
-                        ldexpf(swiglu(ldexpf(acc[mb][1][j], -e), ldexpf(acc[mb][3][j], -e), limit), ea);
+                    float v[HB];
+#pragma unroll
+                    for (int h = 0; h < (int)HB; ++h)
+                        v[h] = ldexpf(swiglu(ldexpf(acc[mb][h][j], -e), ldexpf(acc[mb][HB + h][j], -e), limit), ea);
                     // the row's max |act| over the 16 lanes of this row (bit patterns
                     // as integers: NaN stays above infinity)
-                    uint32_t rm = max(__float_as_uint(fabsf(v0)), __float_as_uint(fabsf(v1)));
+                    uint32_t rm = __float_as_uint(fabsf(v[0]));
+#pragma unroll
+                    for (int h = 1; h < (int)HB; ++h) rm = max(rm, __float_as_uint(fabsf(v[h])));
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0xb1, 0xf, 0xf, false));
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x4e, 0xf, 0xf, false));
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x141, 0xf, 0xf, false));
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x140, 0xf, 0xf, false));
                     if (rowmax != nullptr && m < n && ln == 0u) atomicMax(rowmax + q, rm);
-                    _Float16 h0, l0, h1, l1;
-                    split_f16(v0, h0, l0);
-                    split_f16(v1, h1, l1);
+                    _Float16 hh[HB], ll[HB];
+#pragma unroll
+                    for (int h = 0; h < (int)HB; ++h) split_f16(v[h], hh[h], ll[h]);
                     if (m < n) {
-                        if (AORD == A_IQ4NL) {
+                        if (AORD == A_IQ4NL && HB == 2) {
+                            // columns c and c + 16 of a 32-column block are neighbours
                             const uint64_t o = q * ldo + row0 + 32u * wave + 8u * (ln >> 2) + 2u * (ln & 3u);
-                            *reinterpret_cast<uint32_t*>(out_h + o) = pack_h2(h0, h1);
-                            *reinterpret_cast<uint32_t*>(out_l + o) = pack_h2(l0, l1);
+                            *reinterpret_cast<uint32_t*>(out_h + o) = pack_h2(hh[0], hh[HB - 1]);
+                            *reinterpret_cast<uint32_t*>(out_l + o) = pack_h2(ll[0], ll[HB - 1]);
                         } else {
-                            const uint64_t o0 = q * ldo + a_pos<AORD>(row0 + 32u * wave + ln);
-                            const uint64_t o1 = q * ldo + a_pos<AORD>(row0 + 32u * wave + 16u + ln);
-                            out_h[o0] = h0;
-                            out_l[o0] = l0;
-                            out_h[o1] = h1;
-                            out_l[o1] = l1;
+#pragma unroll
+                            for (int h = 0; h < (int)HB; ++h) {
+                                const uint64_t o = q * ldo + a_pos<AORD>(row0 + 16u * HB * wave + 16u * h + ln);
+                                out_h[o] = hh[h];
+                                out_l[o] = ll[h];
+                            }
                         }
                     }
                     if (out_gs != nullptr) {
-                        float gsum = v0 + v1;
+                        float gsum = v[0];
+#pragma unroll
+                        for (int h = 1; h < (int)HB; ++h) gsum += v[h];
                         gsum += dpp_mov<0xb1>(gsum);
                         gsum += dpp_mov<0x4e>(gsum);
                         gsum += dpp_mov<0x141>(gsum);
                         gsum += dpp_mov<0x140>(gsum);
-                        if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
+                        if constexpr (HB == 2) {
+                            if (m < n && ln == 0) out_gs[q * (ldo / 32u) + (row0 + 32u * wave) / 32u] = gsum;
+                        } else {
+                            if (ln == 0) gpart[wave][m] = gsum;  // half of a 32-column group
+                        }
                     }
                 } else {
                     if (m < n) {
 #pragma unroll
-                        for (int nb = 0; nb < NB; ++nb) out[q * ldo + row0 + 64u * wave + 16u * nb + ln] = acc[mb][nb][j];
+                        for (int nb = 0; nb < NB; ++nb)
+                            out[q * ldo + row0 + 16u * NB * wave + 16u * nb + ln] = acc[mb][nb][j];
                     }
                 }
             }
+        if constexpr (GATEUP && HB == 1 && AORD != A_F32) {
+            // 32-column group g of the block's 64 act columns = waves 2 g, 2 g + 1
+            if (out_gs != nullptr) {
+                __syncthreads();
+                const uint32_t g = tid / TT, m = tid % TT;
+                if (m < n) out_gs[(q0 + m) * (ldo / 32u) + row0 / 32u + g] = gpart[2u * g][m] + gpart[2u * g + 1u][m];
+            }
+        }
     };
     switch ((n + 15u) >> 4) {
         case 1: run(std::integral_constant<int, 1>{}); break;
         case 2: run(std::integral_constant<int, 2>{}); break;
         case 3: run(std::integral_constant<int, 3>{}); break;
-        default: run(std::integral_constant<int, 4>{}); break;
+        case 4: run(std::integral_constant<int, 4>{}); break;
+        default:
+            if constexpr (TT == 128) {
+                switch ((n + 15u) >> 4) {
+                    case 5: run(std::integral_constant<int, 5>{}); break;
+                    case 6: run(std::integral_constant<int, 6>{}); break;
+                    case 7: run(std::integral_constant<int, 7>{}); break;
+                    default: run(std::integral_constant<int, 8>{}); break;
+                }
+            }
+            break;
     }
 #undef INGOT_LOAD_S
 }

@@ -445,14 +445,14 @@ class MoeLayer:
         counts, first = np.zeros(E, np.uint32), np.zeros(E, np.uint32)
         pairs, inverse = np.zeros(P + T, np.uint32), np.zeros(P, np.uint32)
         tiles = np.zeros((cap, 4), np.uint32)
-        info = np.zeros(3, np.uint32)
+        info = np.zeros(4, np.uint32)
         self.gpu._check(self.gpu.lib.ingot_layer_dispatch_debug(
             self.handle, counts.ctypes.data, first.ctypes.data, pairs.ctypes.data, inverse.ctypes.data,
             tiles.ctypes.data, cap, info.ctypes.data))
-        P_, S, n = (int(v) for v in info)
+        P_, S, n, tile = (int(v) for v in info)
         assert P_ == P
         return {"counts": counts, "first": first, "pairs": pairs[:P + S], "inverse": inverse, "shared_rows": S,
-                "tiles": tiles[:min(cap, n)]}
+                "tiles": tiles[:min(cap, n)], "tile": tile}
 
 
 def time_stage(layers: Sequence[MoeLayer], stage: int, reps: int) -> float:

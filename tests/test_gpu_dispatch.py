@@ -6,26 +6,27 @@ the reference's expert_layout / expert_pairs contract (kernels/prefill.metal:
 tests/test_oracle.py). Index work must match exactly, not merely produce the
 right layer outputs: a wrong but self-consistent permutation would pass every
 end-to-end test. The GPU tile list holds the same {expert, first, n} tiles (64
-pairs each) in its own order: the shared expert's tiles first, then every full
-tile, then the partial tiles by decreasing n; its fourth word is the number of
-non-empty tiles.
+pairs each, or 128 when an expert can take more than 64 pairs and both
+projections are Q4_K or Q5_K on the f16 GEMM) in its own order: the shared
+expert's tiles first, then every full tile, then the partial tiles by
+decreasing n; its fourth word is the number of non-empty tiles.
 """
 import numpy as np
 import pytest
 
 from ingot_amd import configs as CF
-from ingot_amd.moe import IQ4_NL, Q4_K, Q8_0, MoeLayer
+from ingot_amd.moe import GEMM_FP32, IQ4_NL, Q4_K, Q8_0, MoeLayer
 
 pytestmark = pytest.mark.gpu
 
-TILE = 64
 
-
-def check_dispatch(layer, spec, x, oracle, label):
+def check_dispatch(layer, spec, x, oracle, label, tile=64):
     out, ids, _ = layer(x)
     T, K, E = x.shape[0], spec.top_k, spec.experts
     P = T * K
     d = layer.dispatch_debug(T)
+    TILE = d["tile"]
+    assert TILE == tile, f"{label}: {TILE}-pair tiles, expected {tile}"
     cap = P // TILE + E + 1
     used, counts, first, pairs, inverse, otiles = oracle.dispatch(ids.ravel(), E, TILE, cap)
     assert np.array_equal(d["counts"], counts), f"{label}: counts"
@@ -67,7 +68,8 @@ def test_dispatch_c1_zipf(gpu, oracle, T, seed):
     """C1's Zipf-biased routing: a hot expert with every token, empty experts."""
     spec = CF.c1_layer()
     layer = MoeLayer(gpu, spec)
-    ids = check_dispatch(layer, spec, CF.inputs(1, T, 2048, seed=seed), oracle, f"C1 T={T}")
+    ids = check_dispatch(layer, spec, CF.inputs(1, T, 2048, seed=seed), oracle, f"C1 T={T}",
+                         tile=128 if T > 64 else 64)
     if T == 512:
         counts = np.bincount(ids.ravel(), minlength=128)
         assert counts.max() == 512 and (counts == 0).any()
@@ -89,7 +91,9 @@ def test_dispatch_tile_tails(gpu, oracle):
     x[:, :E] = 0.0
     x[np.arange(T), order] = 4.0
     layer = MoeLayer(gpu, spec)
-    check_dispatch(layer, spec, x, oracle, "tails")
+    check_dispatch(layer, spec, x, oracle, "tails", tile=128)
+    layer.set_gemm_mode(GEMM_FP32)
+    check_dispatch(layer, spec, x, oracle, "tails, fp32 GEMM", tile=64)
     layer.destroy()
 
 

@@ -320,6 +320,37 @@ def test_dispatch_tile_tails_and_empty_experts(gpu, oracle):
     layer.destroy()
 
 
+@pytest.mark.parametrize("kind", [Q4_K, Q5_K])
+def test_f16_gemm_128_token_tiles(gpu, oracle, kind):
+    """Batches in which an expert can take more than 64 pairs run the f16 GEMM on
+    128-pair tiles: expert loads ending a tile at every 16-row block (1, 17, ...,
+    113, 127), full tiles (128, 256) and tails past them (129, 200, 300), with a
+    shared expert of the routed formats in the same launches."""
+    from ingot_amd.moe import STAGE_DOWN, STAGE_GATEUP
+    E, K, H, F = 16, 1, 1024, 512
+    loads = [1, 17, 33, 49, 65, 81, 97, 113, 127, 128, 129, 200, 256, 300, 0, 0]
+    T = sum(loads)
+    spec = CF.make_layer(15, 0, H, E, K, F, kind, kind, shared_ffn=F)
+    spec.router = np.zeros((E, H), np.float32)
+    spec.router[np.arange(E), np.arange(E)] = 1.0
+    x = CF.inputs(15, T, H) * 0.05
+    order = np.repeat(np.arange(E), loads)
+    np.random.default_rng(7).shuffle(order)
+    x[:, :E] = 0.0
+    x[np.arange(T), order] = 4.0
+    layer = MoeLayer(gpu, spec)
+    check_layer(layer, spec, x, oracle, f"128-token tiles kind {kind}")
+    assert layer.stage_kernel(STAGE_GATEUP) == "k_gemm_f16<gate_up>"
+    assert layer.stage_kernel(STAGE_DOWN) == "k_gemm_f16<down>"
+    d = layer.dispatch_debug(T)
+    assert d["tile"] == 128 and d["shared_rows"] == T
+    want = sorted([128] * (l // 128) + [l % 128] * (l % 128 > 0) for l in loads + [T])
+    want = sorted(v for w in want for v in w)
+    got = sorted(int(v) for v in d["tiles"][:, 2] if v)
+    assert got == want, "128-pair tiles: one per 128 pairs of an expert, then its tail"
+    layer.destroy()
+
+
 def test_route_ties_across_lanes_top8(gpu, oracle):
     E, K, H = 128, 8, 1024
     spec = identity_router_layer(E, K, H)
