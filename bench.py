@@ -55,6 +55,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, the datatype the f16 grouped GEMM issues
 PROFILES = os.path.join(ROOT, "profiles")
+from ingot_amd.profile_summary import WORKLOADS as PROFILE_WORKLOADS  # noqa: E402
 
 
 def log(*a):
@@ -141,15 +142,14 @@ def work(spec, ids, T):
 
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` on `workload` from a committed rocprofv3
-    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated against the plain copy
-    kernel), or (None, None)."""
+    PMC summary in profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated against the
+    plain copy kernel; lines `traffic_bytes_per_launch[<kernel>] @ <workload>: N`
+    written by ingot_amd.profile_summary), or (None, None)."""
+    key = f"traffic_bytes_per_launch[{kernel}] @ {workload}:"
     for path in sorted(glob.glob(os.path.join(PROFILES, "*_pmc.md"))):
-        text = open(path).read()
-        if f"kernel: {kernel}" not in text or f"workload: {workload}" not in text:
-            continue
-        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
-        if m:
-            return int(m.group(1)), os.path.relpath(path, ROOT)
+        for line in open(path):
+            if line.startswith(key):
+                return int(line[len(key):].strip()), os.path.relpath(path, ROOT)
     return None, None
 
 
@@ -167,7 +167,8 @@ def kernel_roofline(bound, stage, stages, w, workload):
         unit, algo = "TFLOP/s", {"algorithmic_flops": w[stage]["flops"]}
     traffic, src = measured_traffic(kernel, workload)
     r = {"bound": bound, "kernel": kernel, "stage": stage, "achieved": achieved, "peak": peak, "unit": unit,
-         "frac": achieved / peak, "traffic": traffic, "traffic_source": src, "kernel_us": us, **algo}
+         "frac": achieved / peak, "traffic": traffic, "traffic_source": src,
+         "traffic_over_algorithmic_bytes": traffic / w[stage]["bytes"] if traffic else None, "kernel_us": us, **algo}
     if bound == "mfma" and kernel.startswith("k_gemm_f16"):
         r["issued_f16_frac"] = 2.0 * achieved / MFMA_F16_PEAK_TFLOPS
         r["frac_vs_fp32_mfma_peak"] = achieved / MFMA_F32_PEAK_TFLOPS
@@ -314,48 +315,47 @@ def extra_configs(gpu, args):
 
 
 def profile_workload(args):
-    """A short eager workload for rocprofv3 (--kernel-trace or --pmc), then one
-    256 MiB device copy by the plain copy kernel (the counter calibration).
-    --profile c01: configs[1] prefill forwards over 8 weight copies and
-    configs[0] decode forwards over 32; c2: configs[2] at b=1 and b=4 over 32
-    copies; c3: configs[3] over 2 copies; c4: the 48-layer stack at b=1 and b=8."""
+    """A short eager workload for rocprofv3 (--kernel-trace or --pmc), one
+    configuration and batch per run (ingot_amd.profile_summary.WORKLOADS), then two 256 MiB
+    device copies by the plain copy kernel (the counter calibration)."""
     from ingot_amd import configs as CF
     from ingot_amd.moe import Gpu, MoeLayer
     gpu = Gpu(0)
 
-    def run(spec, Ts, copies, cfg, H, bf16=False):
+    def run(spec, T, copies, cfg, H, bf16=False):
         base = MoeLayer(gpu, spec)
         layers = [base] + [base.clone() for _ in range(copies - 1)]
-        for T in Ts:
-            dx = gpu.to_device(CF.inputs(cfg, T, H, bf16=bf16))
-            dout = gpu.buffer(4 * T * H)
-            for rep in range(2):
-                for l in layers:
-                    l.forward(dx, T, dout)
-            gpu.synchronize()
-            log(f"profile: configs[{cfg}] T={T} done")
+        dx = gpu.to_device(CF.inputs(cfg, T, H, bf16=bf16))
+        dout = gpu.buffer(4 * T * H)
+        for rep in range(2):
+            for l in layers:
+                l.forward(dx, T, dout)
+        gpu.synchronize()
+        log(f"profile: configs[{cfg}] T={T} done")
         for l in layers:
             l.destroy()
 
-    if args.profile == "c01":
-        run(CF.c1_layer(), (512,), args.copies, 1, 2048)
-        run(CF.c0_layer(), (1,), 32, 0, 2048)
-    elif args.profile == "c2":
-        run(CF.c2_layer(), (1, 4), 32, 2, 2048)
-    elif args.profile == "c3":
-        run(CF.c3_layer(), (64,), 2, 3, 4096, bf16=True)
-    elif args.profile == "c4":
+    w = args.profile
+    if w == "c1":
+        run(CF.c1_layer(), 512, args.copies, 1, 2048)
+    elif w == "c0":
+        run(CF.c0_layer(), 1, 32, 0, 2048)
+    elif w in ("c2b1", "c2b4"):
+        run(CF.c2_layer(), 1 if w == "c2b1" else 4, 32, 2, 2048)
+    elif w == "c3":
+        run(CF.c3_layer(), 64, 2, 3, 4096, bf16=True)
+    elif w in ("c4b1", "c4b8"):
+        T = 1 if w == "c4b1" else 8
         layers = [MoeLayer(gpu, CF.c4_layer(l)) for l in range(48)]
-        for T in (1, 8):
-            da = gpu.to_device(CF.inputs(4, T, 2048))
-            bufs = [gpu.buffer(4 * T * 2048), gpu.buffer(4 * T * 2048)]
-            for rep in range(2):
-                s_ = da
-                for j, l in enumerate(layers):
-                    l.forward(s_, T, bufs[j & 1])
-                    s_ = bufs[j & 1]
-            gpu.synchronize()
-            log(f"profile: configs[4] T={T} done")
+        da = gpu.to_device(CF.inputs(4, T, 2048))
+        bufs = [gpu.buffer(4 * T * 2048), gpu.buffer(4 * T * 2048)]
+        for rep in range(2):
+            s_ = da
+            for j, l in enumerate(layers):
+                l.forward(s_, T, bufs[j & 1])
+                s_ = bufs[j & 1]
+        gpu.synchronize()
+        log(f"profile: configs[4] T={T} done")
     n = 256 << 20
     a, b = gpu.buffer(n), gpu.buffer(n)
     a.upload(np.zeros(n // 4, np.float32))
@@ -396,7 +396,7 @@ def main():
     ap.add_argument("--only-headline", action="store_true", help="configs[0] and configs[1] only")
     ap.add_argument("--extra", action="store_true", help="also the real-file format mixes ('extra_configs')")
     ap.add_argument("--extra-steps", type=int, default=100)
-    ap.add_argument("--profile", choices=["c01", "c2", "c3", "c4"],
+    ap.add_argument("--profile", choices=sorted(PROFILE_WORKLOADS),  # ingot_amd.profile_summary.WORKLOADS
                     help="run only a short eager workload for rocprofv3 and exit (no JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -1,0 +1,217 @@
+"""Summaries of rocprofv3 counter and kernel-trace runs for profiles/.
+
+    python -m ingot_amd.profile_summary ROOT OUT
+
+ROOT holds one rocprofv3 output directory per (workload, pass), made by
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d ROOT/<w>_fetch -o run -- python3 bench.py --profile <w>
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d ROOT/<w>_write -o run -- python3 bench.py --profile <w>
+    rocprofv3 --pmc <SQ_PASS> --output-format csv -d ROOT/<w>_sq -o run -- python3 bench.py --profile <w>
+    rocprofv3 --kernel-trace --stats --output-format csv -d ROOT/<w>_trace -o run -- python3 bench.py --profile <w>
+
+for each workload <w> of WORKLOADS. For each workload present, OUT/<label>_pmc.md
+gets a per-kernel table (HBM bytes from FETCH_SIZE / WRITE_SIZE calibrated
+against the plain copy kernel k_copy16 of the same run, MFMA busy fraction,
+instruction mix, and the trace's mean duration) and one line per kernel
+`traffic_bytes_per_launch[<kernel>] @ <label>: <bytes>`, which bench.py reads
+into its roofline objects.
+"""
+from __future__ import annotations
+
+import csv
+import os
+import re
+import shutil
+import subprocess
+import sys
+from collections import defaultdict
+
+# --profile name -> (the workload label bench.py files its figures under, what runs)
+WORKLOADS = {
+    "c1": ("c1 prefill512", "configs[1] prefill 512: 2 eager forwards over each of 8 resident weight copies"),
+    "c0": ("c0 b=1", "configs[0] decode b=1: 2 eager forwards over each of 32 copies"),
+    "c2b1": ("c2 b=1", "configs[2] decode b=1: 2 eager forwards over each of 32 copies"),
+    "c2b4": ("c2 b=4", "configs[2] batch 4: 2 eager forwards over each of 32 copies"),
+    "c3": ("c3 T=64", "configs[3] 64 tokens: 2 eager forwards over each of 2 copies"),
+    "c4b1": ("c4 b=1", "configs[4] 48-layer stack at b=1: 2 eager passes"),
+    "c4b8": ("c4 b=8", "configs[4] 48-layer stack at b=8: 2 eager passes"),
+}
+SQ_PASS = ("SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_WAVES "
+           "SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_INSTS_SALU GRBM_GUI_ACTIVE")
+COPY_BYTES = 256 << 20  # k_copy16 reads and writes this many bytes per launch
+SIMDS, XCDS = 1024, 8   # MI355X: 256 CUs x 4 SIMDs; GRBM_GUI_ACTIVE is summed over the 8 XCDs
+
+
+def _short_mangled(n: str) -> str:
+    """ingot::name<int and bool arguments> of a mangled ingot kernel name, for
+    the names c++filt leaves alone (binutils' c++filt does not know _Float16's
+    DF16_)."""
+    m = re.match(r"_ZN5ingot(\d+)", n)
+    if not m:
+        return n
+    i = m.end()
+    name = n[i:i + int(m.group(1))]
+    rest = n[i + int(m.group(1)):]
+    if rest.startswith("I"):
+        args = []
+        for kind, v in re.findall(r"L([ib])(\d+)E", rest[:rest.index("EE") + 2] if "EE" in rest else rest):
+            args.append(("true" if v == "1" else "false") if kind == "b" else v)
+        return f"ingot::{name}<{', '.join(args)}>"
+    return f"ingot::{name}"
+
+
+def _demangle(names):
+    mangled = [n for n in names if n.startswith("_Z")]
+    out = {n: n for n in names}
+    if mangled and shutil.which("c++filt"):
+        r = subprocess.run(["c++filt"], input="\n".join(mangled), capture_output=True, text=True)
+        for m, d in zip(mangled, r.stdout.splitlines()):
+            out[m] = d
+    for m in mangled:
+        if out[m].startswith("_Z"):
+            out[m] = _short_mangled(m)
+    return out
+
+
+def stage_kernel(name: str) -> str:
+    """The name bench.py and ingot_layer_stage_kernel use for a launched kernel:
+    k_gemm_f16<gate_up> / k_gemm_f16<down> (and k_gemm<...>) by their GATEUP
+    argument, k_router for both router kernels, otherwise the bare name."""
+    m = re.search(r"(k_\w+?)(?:<([^>]*)>|I|E|\(|$)", name)
+    if not m:
+        return name
+    base = m.group(1)
+    args = [a.strip() for a in (m.group(2) or "").split(",")]
+    if base in ("k_gemm_f16", "k_gemm"):
+        if len(args) > 1:
+            gu = args[1] == "true"
+        else:  # still mangled: ...ILi<kind>ELb<0|1>E...
+            mm = re.search(r"Lb([01])E", name)
+            gu = bool(mm and mm.group(1) == "1")
+        return f"{base}<{'gate_up' if gu else 'down'}>"
+    if base == "k_router_t":
+        return "k_router"
+    return base
+
+
+def read_counters(path):
+    """{kernel: {counter: [value per dispatch]}} from run_counter_collection.csv."""
+    rows = list(csv.DictReader(open(path)))
+    dm = _demangle({r["Kernel_Name"] for r in rows})
+    out = defaultdict(lambda: defaultdict(list))
+    for r in rows:
+        out[stage_kernel(dm[r["Kernel_Name"]])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return out
+
+
+def read_trace(path):
+    """{kernel: (calls, mean us)} from run_kernel_stats.csv (launches merged by stage name)."""
+    rows = list(csv.DictReader(open(path)))
+    dm = _demangle({r["Name"] for r in rows})
+    acc = defaultdict(lambda: [0, 0.0])
+    for r in rows:
+        k = stage_kernel(dm[r["Name"]])
+        acc[k][0] += int(r["Calls"])
+        acc[k][1] += float(r["TotalDurationNs"])
+    return {k: (c, t / c / 1000.0) for k, (c, t) in acc.items()}
+
+
+def mean(v):
+    return sum(v) / len(v) if v else float("nan")
+
+
+def summarize(root: str, w: str):
+    label, desc = WORKLOADS[w]
+    p = lambda s: os.path.join(root, f"{w}_{s}", "run_counter_collection.csv")  # noqa: E731
+    fetch, write = read_counters(p("fetch")), read_counters(p("write"))
+    sq = read_counters(p("sq")) if os.path.exists(p("sq")) else {}
+    tpath = os.path.join(root, f"{w}_trace", "run_kernel_stats.csv")
+    trace = read_trace(tpath) if os.path.exists(tpath) else {}
+    fr = COPY_BYTES / (mean(fetch["k_copy16"]["FETCH_SIZE"]) * 1024)
+    fw = COPY_BYTES / (mean(write["k_copy16"]["WRITE_SIZE"]) * 1024)
+    cmds = [f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof/{w}_fetch -o run -- python3 bench.py --profile {w}",
+            f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof/{w}_write -o run -- python3 bench.py --profile {w}",
+            f"rocprofv3 --pmc {SQ_PASS} --output-format csv -d gpurun_out/prof/{w}_sq -o run -- python3 bench.py --profile {w}",
+            f"rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof/{w}_trace -o run -- python3 bench.py --profile {w}",
+            "python -m ingot_amd.profile_summary gpurun_out/prof profiles"]
+    L = [f"# rocprofv3 counters and kernel trace: {desc}", "",
+         f"workload: {label}", "",
+         "Commands (repository root, one MI355X; each pass is its own run):", "", "```", *cmds, "```", "",
+         f"**Calibration.** The plain copy kernel `k_copy16` reads and writes {COPY_BYTES:,} B per launch; in "
+         f"these runs FETCH_SIZE reads {mean(fetch['k_copy16']['FETCH_SIZE']):,.1f} KiB and WRITE_SIZE "
+         f"{mean(write['k_copy16']['WRITE_SIZE']):,.1f} KiB for it, so HBM bytes = FETCH_SIZE x 1024 x {fr:.3f} "
+         f"+ WRITE_SIZE x 1024 x {fw:.3f}.", "",
+         "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8 XCDs), the fraction of the "
+         "kernel's SIMD cycles in which the matrix core was busy; f16 MFMA rate = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 "
+         "FLOP over the same cycles at the trace's duration. Counter runs serialize kernels; durations are the "
+         "kernel trace's means.", "",
+         "| kernel | dispatches | trace mean us | FETCH KiB | WRITE KiB | HBM read MB | HBM write MB | MFMA busy | "
+         "f16 MFMA TFLOP/s issued | VALU per MFMA |",
+         "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    lines = []
+    kernels = [k for k in fetch if k != "k_copy16" and k.startswith("k_")]
+    order = sorted(kernels, key=lambda k: -(trace.get(k, (0, 0))[0] * trace.get(k, (0, 0))[1]))
+    for k in order:
+        fk, wk = mean(fetch[k]["FETCH_SIZE"]), mean(write[k]["WRITE_SIZE"]) if k in write else 0.0
+        rb, wb = fk * 1024 * fr, wk * 1024 * fw
+        s = sq.get(k, {})
+        cyc = mean(s.get("GRBM_GUI_ACTIVE", [])) / XCDS
+        busy = mean(s.get("SQ_VALU_MFMA_BUSY_CYCLES", [])) / (SIMDS * cyc) if s else float("nan")
+        nm = mean(s.get("SQ_INSTS_MFMA", []))
+        vpm = (mean(s.get("SQ_INSTS_VALU", [])) - nm) / nm if s and nm > 0 else float("nan")
+        calls, us = trace.get(k, (len(fetch[k]["FETCH_SIZE"]), float("nan")))
+        mops = mean(s.get("SQ_INSTS_VALU_MFMA_MOPS_F16", [])) if s else 0.0
+        tf = mops * 512 / (us * 1e-6) / 1e12 if mops and us == us else float("nan")
+        f = lambda v, d=1: "-" if v != v else f"{v:,.{d}f}"  # noqa: E731
+        L.append(f"| `{k}` | {len(fetch[k]['FETCH_SIZE'])} | {f(us, 2)} | {f(fk)} | {f(wk)} | {f(rb / 1e6)} | "
+                 f"{f(wb / 1e6)} | {('-' if busy != busy or nm == 0 else f'{100 * busy:.1f} %')} | "
+                 f"{('-' if tf != tf else f'{tf:.1f}')} | {('-' if vpm != vpm else f'{vpm:.2f}')} |")
+        lines.append(f"traffic_bytes_per_launch[{k}] @ {label}: {int(round(rb + wb))}")
+    L += ["", "Per-launch HBM traffic (FETCH + WRITE, calibrated), read by bench.py:", "", "```", *lines, "```", ""]
+    return label, "\n".join(L)
+
+
+BENCH_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof/bench_trace -o run -- "
+                   "python3 bench.py --only-headline --steps 50 --decode-steps 200 --no-cpu")
+
+
+def bench_trace(root: str):
+    """Per-kernel mean durations of the headline bench command under the kernel trace."""
+    rows = list(csv.DictReader(open(os.path.join(root, "bench_trace", "run_kernel_stats.csv"))))
+    dm = _demangle({r["Name"] for r in rows})
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    L = ["# Kernel trace: the headline bench command (configs[1] prefill 512 and configs[0] decode b=1)", "",
+         "Command (repository root, one MI355X):", "", "```", BENCH_TRACE_CMD,
+         "python -m ingot_amd.profile_summary gpurun_out/prof profiles", "```", "",
+         "Every launch of the run: eager warm-ups, the graph-captured timed steps and the per-stage graph "
+         "replays behind `stages_us`. Tracing adds a gap per graph node, so whole-step times printed by the "
+         "traced run are not the benchmark result; per-kernel durations are unaffected.", "",
+         "| kernel | stage name | calls | mean us | min us | max us | share of kernel time |",
+         "|---|---|---:|---:|---:|---:|---:|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:14]:
+        d = dm[r["Name"]]
+        short = re.sub(r"\(.*", "", d).replace("void ", "")
+        L.append(f"| `{short}` | `{stage_kernel(d)}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                 f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                 f"{100 * float(r['TotalDurationNs']) / total:.1f} % |")
+    return "\n".join(L) + "\n"
+
+
+def main(argv):
+    root, out = argv[1], argv[2]
+    os.makedirs(out, exist_ok=True)
+    if os.path.exists(os.path.join(root, "bench_trace", "run_kernel_stats.csv")):
+        path = os.path.join(out, "bench_headline_kernel_trace.md")
+        open(path, "w").write(bench_trace(root))
+        print("wrote", path)
+    for w in WORKLOADS:
+        if not os.path.exists(os.path.join(root, f"{w}_fetch", "run_counter_collection.csv")):
+            continue
+        label, text = summarize(root, w)
+        path = os.path.join(out, re.sub(r"[^A-Za-z0-9]+", "_", label).strip("_") + "_pmc.md")
+        open(path, "w").write(text)
+        print("wrote", path)
+
+
+if __name__ == "__main__":
+    main(sys.argv)
