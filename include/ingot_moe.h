@@ -32,6 +32,11 @@
  *                            gain is given
  *   ingot_layer_forward_add  the same with the attention output's residual add
  *                            (add_rms, kernels/generic.metal:390-405) fused in
+ *   ingot_layer_create_cached
+ *                            bounded-memory experts: ExpertWeights::Cached +
+ *                            ExpertCache (src/weights.rs:46-95), forwarded as in
+ *                            the cached branch of Qwen::ffn (src/qwen.rs:1171-1253)
+ *   ingot_expert_cache_*     ExpertCache::hit / ExpertCache::slot (src/weights.rs:59-95)
  *
  * Errors follow the reference: an invalid argument, shape or format is
  * INGOT_INVALID (io::ErrorKind::InvalidData via invalid(), src/lib.rs:39-41);
@@ -178,8 +183,42 @@ typedef struct ingot_layer_desc {
 
 /* Copies the layer to device memory (every expert resident). */
 int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* desc, ingot_layer** out);
-/* A second resident copy of the same weights at new device addresses. */
+/* A second resident copy of the same weights at new device addresses (not for
+ * cached layers). */
 int ingot_layer_clone(const ingot_layer* src, ingot_layer** out);
+/* A layer whose routed experts stay in the caller's host memory (desc's gate,
+ * up and down bytes, which must stay valid and unchanged while the layer
+ * lives) and are copied on demand into `slots` device expert slots, 1 <= slots
+ * <= E (router, vectors and the shared expert are resident). ingot_layer_forward
+ * on it routes on the device, reads the routing back to the host, then runs
+ * the routed experts in order of first use in passes of at most `slots`
+ * experts: each expert of a pass takes a hit slot or the least recently used
+ * slot that the pass has not claimed (an empty slot first, ties to the lower
+ * slot), a miss copies the expert's bytes into it, and the pass's grouped
+ * products run on those slots. The forward synchronizes the context stream,
+ * cannot be captured into a graph (INGOT_INVALID), and has no allocation-free
+ * variant. Outputs equal a resident layer's bit for bit. */
+int ingot_layer_create_cached(ingot_ctx* ctx, const ingot_layer_desc* desc, uint32_t slots, ingot_layer** out);
+/* Counters of a cached layer since creation: hits, misses and bytes copied
+ * into slots. */
+int ingot_layer_cache_stats(const ingot_layer* layer, uint64_t* hits, uint64_t* misses, uint64_t* bytes);
+
+/* The cache policy alone, on the host (no device): for tests of it.
+ * hit: the slot holding expert `id`, its age refreshed, or -1.
+ * claim: the slot for `id` before a read: a hit (*load = 0), or the least
+ *   recently used slot not among pinned[npinned], emptied (*load = 1: read the
+ *   expert, then commit); -1 when every slot is pinned ("no reusable expert
+ *   slot"), leaving the slots unchanged. A read that fails is simply not
+ *   committed: the slot stays empty.
+ * state: ids[slots] (-1: empty), hits and misses (a miss counts at commit). */
+typedef struct ingot_expert_cache ingot_expert_cache;
+ingot_expert_cache* ingot_expert_cache_create(uint32_t slots);
+void ingot_expert_cache_destroy(ingot_expert_cache* cache);
+int ingot_expert_cache_hit(ingot_expert_cache* cache, uint32_t id);
+int ingot_expert_cache_claim(ingot_expert_cache* cache, uint32_t id, const uint32_t* pinned, uint32_t npinned,
+                             int* load);
+int ingot_expert_cache_commit(ingot_expert_cache* cache, uint32_t slot, uint32_t id);
+int ingot_expert_cache_state(const ingot_expert_cache* cache, int64_t* ids, uint64_t* hits, uint64_t* misses);
 void ingot_layer_destroy(ingot_layer* layer);
 /* Reserve workspace for up to T tokens (done implicitly by forward; call it
  * before graph capture, which must not allocate). */

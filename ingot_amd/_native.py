@@ -89,6 +89,14 @@ MOE_SYMBOLS = {
     "ingot_ctx_check_device_flags": (I32, [P]),
     "ingot_layer_create": (I32, [P, C.POINTER(LayerDesc_t), C.POINTER(P)]),
     "ingot_layer_clone": (I32, [P, C.POINTER(P)]),
+    "ingot_layer_create_cached": (I32, [P, C.POINTER(LayerDesc_t), U32, C.POINTER(P)]),
+    "ingot_layer_cache_stats": (I32, [P, C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
+    "ingot_expert_cache_create": (P, [U32]),
+    "ingot_expert_cache_destroy": (None, [P]),
+    "ingot_expert_cache_hit": (I32, [P, U32]),
+    "ingot_expert_cache_claim": (I32, [P, U32, P, U32, C.POINTER(I32)]),
+    "ingot_expert_cache_commit": (I32, [P, U32, U32]),
+    "ingot_expert_cache_state": (I32, [P, P, C.POINTER(U64), C.POINTER(U64)]),
     "ingot_layer_destroy": (None, [P]),
     "ingot_layer_reserve": (I32, [P, U32]),
     "ingot_layer_forward": (I32, [P, P, U32, P, P, P]),

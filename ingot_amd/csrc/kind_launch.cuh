@@ -41,7 +41,7 @@ bool launch_shared_add_k(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* 
 template <int KIND, bool GATEUP>
 bool launch_gemm_k(hipStream_t s, dim3 grid, const GemmArgs& a) {
     hipLaunchKernelGGL((k_gemm<KIND, GATEUP>), grid, dim3(256), 0, s, a.w0, a.w1, a.s0, a.s1, a.rows, a.kdim, a.a,
-                       a.pairs, a.K, a.tiles, a.ldo, a.limit, a.out);
+                       a.pairs, a.K, a.tiles, a.ldo, a.limit, a.out, a.slot_of);
     return true;
 }
 

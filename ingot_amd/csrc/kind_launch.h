@@ -72,6 +72,7 @@ struct GemmArgs {
     uint32_t ldo;
     float limit;
     float* out;
+    const uint32_t* slot_of;  // cached experts: expert -> device slot (NO_SLOT: skip), or NULL
 };
 
 // k_gemv_gate_up: act = SwiGLU(G x, U x) for `pairs` (grid.y) pairs, cpl chunks

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -288,8 +289,8 @@ bool launch_shared_down_add(hipStream_t s, uint32_t ks, const uint8_t* sd, uint6
 template <bool GATEUP>
 bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, const uint8_t* w1, uint64_t s0,
                  uint64_t s1, uint32_t rows, uint32_t kdim, const float* a, const uint32_t* pairs, uint32_t K,
-                 const uint32_t* tiles, uint32_t ldo, float limit, float* out) {
-    const GemmArgs g{w0, w1, s0, s1, rows, kdim, a, pairs, K, tiles, ldo, limit, out};
+                 const uint32_t* tiles, uint32_t ldo, float limit, float* out, const uint32_t* slot_of = nullptr) {
+    const GemmArgs g{w0, w1, s0, s1, rows, kdim, a, pairs, K, tiles, ldo, limit, out, slot_of};
     switch (kind) {
 #define K_(KV) case KV: return launch_gemm_k<KV, GATEUP>(s, grid, g);
         INGOT_KINDS(K_)
@@ -446,7 +447,61 @@ struct Ws {
     float* resid = nullptr;                 // x + a of ingot_layer_forward_add (the new residual stream)
     float* xstat = nullptr;                 // per token {max |x|, ||x 2^e||}: scales of the f16 splits
     uint32_t* rowmax = nullptr;             // per-row max |act| of the f16 GEMM (range check)
+    uint32_t* slot_of = nullptr;            // cached layers: expert -> slot of the current pass (E + 1 entries)
     uint32_t tile_cap = 0, stile_cap = 0;
+};
+
+// The reference's expert cache policy (ExpertCache, src/weights.rs:46-95): slot
+// i holds expert id[i] (-1: empty) last used at age[i]; a hit refreshes the age;
+// a miss takes the least recently used slot that is not pinned (an empty slot
+// counts as age 0; ties to the lower slot), empties it for the read, and the
+// read's success fills it (commit) with the age of the claim. A failed read
+// leaves the slot empty.
+struct ExpertCache {
+    std::vector<int64_t> id;
+    std::vector<uint64_t> age, claim_age;
+    uint64_t clock = 0, hits = 0, misses = 0, bytes = 0;
+    explicit ExpertCache(uint32_t n) : id(n, -1), age(n, 0), claim_age(n, 0) {}
+    uint32_t slots() const { return (uint32_t)id.size(); }
+    int hit(uint32_t e) {
+        for (uint32_t i = 0; i < slots(); ++i)
+            if (id[i] == (int64_t)e) {
+                age[i] = ++clock;
+                ++hits;
+                return (int)i;
+            }
+        return -1;
+    }
+    // The slot for expert e: a hit (*load = 0), or a slot emptied for the read
+    // (*load = 1); -1 when every slot is pinned ("no reusable expert slot").
+    int claim(uint32_t e, const uint32_t* pinned, uint32_t np, int* load) {
+        *load = 0;
+        const int h = hit(e);
+        if (h >= 0) return h;
+        ++clock;
+        int best = -1;
+        uint64_t best_age = 0;
+        for (uint32_t i = 0; i < slots(); ++i) {
+            bool pin = false;
+            for (uint32_t j = 0; j < np; ++j) pin = pin || pinned[j] == i;
+            if (pin) continue;
+            const uint64_t a = id[i] < 0 ? 0 : age[i];
+            if (best < 0 || a < best_age) {
+                best = (int)i;
+                best_age = a;
+            }
+        }
+        if (best < 0) return -1;
+        id[best] = -1;
+        claim_age[best] = clock;
+        *load = 1;
+        return best;
+    }
+    void commit(uint32_t slot, uint32_t e) {
+        id[slot] = e;
+        age[slot] = claim_age[slot];
+        ++misses;
+    }
 };
 
 struct ingot_layer {
@@ -463,6 +518,17 @@ struct ingot_layer {
     Ws w;
     std::function<void(hipStream_t)> stage[ST_N];
     const char* stage_name[ST_N] = {};
+    // Cached layer (ingot_layer_create_cached): gate/up/down hold `cache` slots;
+    // the experts stay in host memory at hgate/hup/hdown (the caller's bytes,
+    // expert e at e * rows * stride). pass: the expert -> slot table and whether
+    // the shared expert runs, read by the GEMM stages of the current pass.
+    bool cached = false;
+    std::unique_ptr<ExpertCache> cache;
+    const uint8_t *hgate = nullptr, *hup = nullptr, *hdown = nullptr;
+    struct Pass {
+        const uint32_t* slot_of = nullptr;
+        bool first = true;
+    } pass;
     // the dispatch buffers of the last prefill forward (ingot_layer_dispatch_debug)
     uint32_t last_T = 0, last_P = 0, last_S = 0, last_cap = 0, last_tm = 0;
     bool last_prefill = false;
@@ -505,6 +571,7 @@ static uint64_t carve(const ingot_layer* L, uint32_t T, void* base, Ws* out) {
         {(void**)&w.xs, 4ull * T * (L->H / 32)}, {(void**)&w.acts, 4ull * PS * (L->F / 32)},
         {(void**)&w.resid, L->has_norm ? 4ull * T * L->H : 0ull},
         {(void**)&w.xstat, 8ull * T},            {(void**)&w.rowmax, 4ull * PS},
+        {(void**)&w.slot_of, L->cached ? 4ull * (L->E + 1) : 0ull},
     };
     uint64_t off = 0;
     for (const Part& p : parts) {
@@ -806,7 +873,9 @@ int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* 
 }
 
 // ---- resident layer ----
-int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* d, ingot_layer** out) {
+// slots == 0: every expert resident; else a cached layer with `slots` device
+// expert slots (ingot_layer_create_cached).
+static int create_layer(ingot_ctx* ctx, const ingot_layer_desc* d, uint32_t slots, ingot_layer** out) {
     if (!d || !out) return fail(ctx, INGOT_INVALID, "null layer description");
     *out = nullptr;
     const uint32_t H = d->hidden, E = d->experts, K = d->top_k;
@@ -861,9 +930,35 @@ int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* d, ingot_layer** 
     if (st == INGOT_OK && L->has_bias) st = upload(ctx, d->router_bias, E, &L->bias);
     if (st == INGOT_OK && L->has_sgvec) st = upload(ctx, d->shared_gate_vec, H, &L->sgvec);
     if (st == INGOT_OK && L->has_norm) st = upload(ctx, d->norm_gain, H, &L->gain);
-    if (st == INGOT_OK) st = upload_matrix(ctx, &d->gate, &L->gate);
-    if (st == INGOT_OK) st = upload_matrix(ctx, &d->up, &L->up);
-    if (st == INGOT_OK) st = upload_matrix(ctx, &d->down, &L->down);
+    if (slots == 0) {
+        if (st == INGOT_OK) st = upload_matrix(ctx, &d->gate, &L->gate);
+        if (st == INGOT_OK) st = upload_matrix(ctx, &d->up, &L->up);
+        if (st == INGOT_OK) st = upload_matrix(ctx, &d->down, &L->down);
+    } else {
+        // Device slots for `slots` experts of each matrix; the experts stay in
+        // the caller's host bytes.
+        L->cached = true;
+        L->cache = std::make_unique<ExpertCache>(slots);
+        L->hgate = d->gate.data;
+        L->hup = d->up.data;
+        L->hdown = d->down.data;
+        for (auto [m, dm] : {std::pair{&d->gate, &L->gate}, std::pair{&d->up, &L->up}, std::pair{&d->down, &L->down}}) {
+            if (st != INGOT_OK) break;
+            const uint64_t bytes = (uint64_t)slots * m->rows * m->stride;
+            const hipError_t e = hipMalloc(reinterpret_cast<void**>(&dm->d), bytes);
+            if (e != hipSuccess) {
+                dm->d = nullptr;
+                st = fail(ctx, INGOT_DEVICE, std::string("hipMalloc: ") + hipGetErrorString(e));
+                break;
+            }
+            dm->nbytes = bytes;
+            dm->cols = m->cols;
+            dm->rows = m->rows;
+            dm->count = slots;
+            dm->stride = m->stride;
+            dm->kind = m->kind;
+        }
+    }
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_gate, &L->sgate);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_up, &L->sup);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_down, &L->sdown);
@@ -876,10 +971,56 @@ int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* d, ingot_layer** 
     return INGOT_OK;
 }
 
+int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* d, ingot_layer** out) {
+    return create_layer(ctx, d, 0, out);
+}
+
+int ingot_layer_create_cached(ingot_ctx* ctx, const ingot_layer_desc* d, uint32_t slots, ingot_layer** out) {
+    if (slots == 0) return fail(ctx, INGOT_INVALID, "a cached layer needs at least one expert slot");
+    if (d && slots > d->experts) return fail(ctx, INGOT_INVALID, "more expert slots than experts");
+    return create_layer(ctx, d, slots, out);
+}
+
+int ingot_layer_cache_stats(const ingot_layer* L, uint64_t* hits, uint64_t* misses, uint64_t* bytes) {
+    if (!L || !hits || !misses || !bytes) return INGOT_INVALID;
+    if (!L->cached) return fail(L->ctx, INGOT_INVALID, "the layer's experts are resident, not cached");
+    *hits = L->cache->hits;
+    *misses = L->cache->misses;
+    *bytes = L->cache->bytes;
+    return INGOT_OK;
+}
+
+// Host-only mirror of the cache policy (no device), for tests of it.
+struct ingot_expert_cache {
+    ExpertCache c;
+    explicit ingot_expert_cache(uint32_t n) : c(n) {}
+};
+
+ingot_expert_cache* ingot_expert_cache_create(uint32_t slots) { return slots ? new ingot_expert_cache(slots) : nullptr; }
+void ingot_expert_cache_destroy(ingot_expert_cache* c) { delete c; }
+int ingot_expert_cache_hit(ingot_expert_cache* c, uint32_t id) { return c ? c->c.hit(id) : -1; }
+int ingot_expert_cache_claim(ingot_expert_cache* c, uint32_t id, const uint32_t* pinned, uint32_t npinned, int* load) {
+    if (!c || !load || (npinned && !pinned)) return -1;
+    return c->c.claim(id, pinned, npinned, load);
+}
+int ingot_expert_cache_commit(ingot_expert_cache* c, uint32_t slot, uint32_t id) {
+    if (!c || slot >= c->c.slots()) return INGOT_INVALID;
+    c->c.commit(slot, id);
+    return INGOT_OK;
+}
+int ingot_expert_cache_state(const ingot_expert_cache* c, int64_t* ids, uint64_t* hits, uint64_t* misses) {
+    if (!c || !ids || !hits || !misses) return INGOT_INVALID;
+    for (uint32_t i = 0; i < c->c.slots(); ++i) ids[i] = c->c.id[i];
+    *hits = c->c.hits;
+    *misses = c->c.misses;
+    return INGOT_OK;
+}
+
 int ingot_layer_clone(const ingot_layer* src, ingot_layer** out) {
     if (!src || !out) return INGOT_INVALID;
     ingot_ctx* ctx = src->ctx;
     CHECK_CTX(ctx);
+    if (src->cached) return fail(ctx, INGOT_INVALID, "a cached layer cannot be cloned");
     ingot_layer* L = new ingot_layer();
     L->ctx = ctx;
     L->H = src->H; L->E = src->E; L->K = src->K; L->F = src->F; L->SF = src->SF; L->routing = src->routing;
@@ -948,6 +1089,76 @@ static const uint32_t GEMV_MAX_PAIRS = 64;
 // rows of F) and their group sums with 32-bit byte offsets.
 static bool f16_gemm_fits(uint64_t kdim, uint64_t rows) { return 2ull * kdim * rows < (1ull << 32); }
 
+// The stages of a cached layer's forward (src/qwen.rs:1171-1253): routing and
+// dispatch, then the routing is read back to the host; the routed experts, in
+// order of first use, go through the cache in passes of at most `slots`
+// experts (the slots of a pass are pinned while it claims the next ones; a miss
+// copies the expert's gate, up and down bytes into its slot); each pass runs
+// the grouped GEMMs on the tiles of its experts (slot_of maps expert -> slot,
+// NO_SLOT skips a tile; the shared expert runs in the first pass); the combine
+// follows the last pass. Every copy and launch is ordered on the context's
+// stream, so a slot is refilled only after the pass that read it; the call
+// returns after the stream drains (the host tables and the routing it read).
+static int cached_expert_passes(ingot_layer* L, const Ws& w, uint32_t T) {
+    ingot_ctx* ctx = L->ctx;
+    hipStream_t s = ctx->stream;
+    const uint32_t E = L->E, P = T * L->K;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(ctx, hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(ctx, INGOT_INVALID, "a cached layer reads its routing on the host and cannot be graph-captured");
+    for (int i : {ST_ROUTER, ST_ROUTE, ST_DISPATCH}) L->stage[i](s);
+    std::vector<uint32_t> ids(P);
+    HIP_TRY(ctx, hipMemcpyAsync(ids.data(), w.ids, 4ull * P, hipMemcpyDeviceToHost, s));
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    std::vector<uint32_t> order;
+    std::vector<char> seen(E, 0);
+    for (uint32_t e : ids) {
+        if (e >= E) return fail(ctx, INGOT_NONFINITE, "routing failed: non-finite router logits");
+        if (!seen[e]) {
+            seen[e] = 1;
+            order.push_back(e);
+        }
+    }
+    const DevMatrix* dev[3] = {&L->gate, &L->up, &L->down};
+    const uint8_t* host[3] = {L->hgate, L->hup, L->hdown};
+    std::vector<std::vector<uint32_t>> tables;  // kept until the stream drains
+    ExpertCache& c = *L->cache;
+    size_t i = 0;
+    for (bool first = true; first || i < order.size(); first = false) {
+        std::vector<uint32_t> pinned;
+        tables.emplace_back(E + 1, NO_SLOT);
+        std::vector<uint32_t>& slot_of = tables.back();
+        while (i < order.size() && pinned.size() < c.slots()) {
+            const uint32_t e = order[i];
+            int load = 0;
+            const int slot = c.claim(e, pinned.data(), (uint32_t)pinned.size(), &load);
+            if (slot < 0) return fail(ctx, INGOT_INVALID, "no reusable expert slot");
+            if (load) {
+                for (int m = 0; m < 3; ++m) {
+                    const uint64_t bytes = dev[m]->rows * dev[m]->stride;
+                    HIP_TRY(ctx, hipMemcpyAsync(dev[m]->d + (uint64_t)slot * bytes, host[m] + (uint64_t)e * bytes, bytes,
+                                                hipMemcpyHostToDevice, s));
+                    c.bytes += bytes;
+                }
+                c.commit((uint32_t)slot, e);
+            }
+            slot_of[e] = (uint32_t)slot;
+            pinned.push_back((uint32_t)slot);
+            ++i;
+        }
+        slot_of[E] = first ? 0u : NO_SLOT;
+        HIP_TRY(ctx, hipMemcpyAsync(w.slot_of, slot_of.data(), 4ull * (E + 1), hipMemcpyHostToDevice, s));
+        L->pass = {w.slot_of, first};
+        L->stage[ST_GATEUP](s);
+        L->stage[ST_DOWN](s);
+    }
+    L->pass = {};
+    L->stage[ST_COMBINE](s);
+    HIP_TRY(ctx, hipStreamSynchronize(s));
+    return INGOT_OK;
+}
+
 // One forward on the workspace w (sized for at least T tokens).
 // d_a != NULL (ingot_layer_forward_add, norm layers only): the router adds
 // d_a to d_x, normalises the sum and stores it to w.resid, which is then the
@@ -966,7 +1177,9 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
     const int ks_ = hs_ ? (int)L->sdown.kind : -1;
     const bool fuse_shared = hs_ && can_fuse_shared(L->down.kind, ks_);
     const uint32_t nv_ = K * (F / 32) + (fuse_shared ? SF / 32 : 0);
-    const bool decode = P <= GEMV_MAX_PAIRS && K <= 2 * GU_WAVES && (uint64_t)K * F + (hs_ ? SF : 0) <= DOWN_LDS_FLOATS &&
+    // A cached layer reads the routing back to the host before its expert
+    // products, so it always takes the route / dispatch / grouped GEMM path.
+    const bool decode = !L->cached && P <= GEMV_MAX_PAIRS && K <= 2 * GU_WAVES && (uint64_t)K * F + (hs_ ? SF : 0) <= DOWN_LDS_FLOATS &&
                         (nv_ + 63) / 64 <= 8 && (!hs_ || fuse_shared || (SF / 32 + 63) / 64 <= 2) && H <= 4096;
     uint32_t* flags = ctx->d_flags;
     float* xstat = w.xstat;
@@ -1081,35 +1294,38 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
                 hipLaunchKernelGGL(k_dense_tiles, dim3((scap + 63) / 64), dim3(64), 0, ss, T, scap, stiles);
         };
         L->stage_name[ST_DISPATCH] = "k_dispatch";
+        ingot_layer* const LL = L;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
+            const uint32_t* so = LL->pass.slot_of;
             if (f16gu) {
                 launch_gemm_f16<true>(ss, gate.kind, aord, tt128, dim3(8 * (F / 64) * ((capf + 7) / 8)), gate.d, up.d,
                                       merge ? sgate.d : nullptr, merge ? sup.d : nullptr, e_sh, gate.stride, up.stride,
                                       F, H, (const _Float16*)xh, (const _Float16*)xl, (const float*)xs,
                                       (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit,
                                       f16 ? (float*)nullptr : act, acth, actl, mins ? acts : nullptr, F / 64, T,
-                                      (const float*)xstat, rmx, flags);
+                                      (const float*)xstat, rmx, flags, so);
             } else {
                 launch_gemm<true>(ss, gate.kind, dim3(F / 64, cap), gate.d, up.d, gate.stride, up.stride, F, H, xin,
-                                  pairs, K, tiles, F, limit, act);
+                                  pairs, K, tiles, F, limit, act, so);
             }
-            if (hs && !merge)
+            if (hs && !merge && LL->pass.first)
                 launch_gemm<true>(ss, sgate.kind, dim3(SF / 64, scap), sgate.d, sup.d, sgate.stride, sup.stride, SF, H,
                                   xin, nullptr, 1, stiles, SF, limit, sact);
         };
         L->stage_name[ST_GATEUP] = f16gu ? "k_gemm_f16<gate_up>" : "k_gemm<gate_up>";
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
+            const uint32_t* so = LL->pass.slot_of;
             if (f16)
                 launch_gemm_f16<false>(ss, down.kind, A_NATURAL, tt128, dim3(8 * (H / 128) * ((capf + 7) / 8)), down.d,
                                        (const uint8_t*)nullptr, merge ? sdown.d : nullptr, (const uint8_t*)nullptr, e_sh,
                                        down.stride, 0ull, H, F, (const _Float16*)acth, (const _Float16*)actl,
                                        (const float*)acts, (const uint32_t*)nullptr, K, (const uint32_t*)tiles, H, 0.f,
                                        Y, (_Float16*)nullptr, (_Float16*)nullptr, (float*)nullptr, H / 128,
-                                       (uint32_t)(P + S), (const float*)xstat, rmx, flags);
+                                       (uint32_t)(P + S), (const float*)xstat, rmx, flags, so);
             else
                 launch_gemm<false>(ss, down.kind, dim3(H / 128, cap), down.d, nullptr, down.stride, 0, H, F, act,
-                                   nullptr, K, tiles, H, 0.f, Y);
-            if (hs && !merge)
+                                   nullptr, K, tiles, H, 0.f, Y, so);
+            if (hs && !merge && LL->pass.first)
                 launch_gemm<false>(ss, sdown.kind, dim3(H / 128, scap), sdown.d, nullptr, sdown.stride, 0, H, SF, sact,
                                    nullptr, 1, stiles, H, 0.f, Ys);
         };
@@ -1124,9 +1340,14 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         L->stage_name[ST_COMBINE] = "k_combine";
     }
     L->last = w;
-    const int order[] = {ST_ROUTER, ST_ROUTE, ST_DISPATCH, ST_GATEUP, ST_DOWN, ST_COMBINE};
-    for (int i : order)
-        if (L->stage[i]) L->stage[i](s);
+    if (L->cached) {
+        const int st = cached_expert_passes(L, w, T);
+        if (st != INGOT_OK) return st;
+    } else {
+        const int order[] = {ST_ROUTER, ST_ROUTE, ST_DISPATCH, ST_GATEUP, ST_DOWN, ST_COMBINE};
+        for (int i : order)
+            if (L->stage[i]) L->stage[i](s);
+    }
     LAUNCH_CHECK(ctx);
     if (d_ids) HIP_TRY(ctx, hipMemcpyAsync(d_ids, w.ids, 4ull * P, hipMemcpyDeviceToDevice, s));
     if (d_weights) HIP_TRY(ctx, hipMemcpyAsync(d_weights, w.wts, 4ull * P, hipMemcpyDeviceToDevice, s));
@@ -1146,6 +1367,7 @@ int ingot_layer_forward_static(ingot_layer* L, const float* d_x, uint32_t T, flo
                                float* d_weights) {
     if (!L) return INGOT_INVALID;
     CHECK_CTX(L->ctx);
+    if (L->cached) return fail(L->ctx, INGOT_INVALID, "a cached layer copies experts into its slots: not allocation-free");
     if (!d_x || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
     const uint64_t need = carve(L, T, nullptr, nullptr);
     if (need > STATIC_SCRATCH_BYTES)

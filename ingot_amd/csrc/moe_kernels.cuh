@@ -1466,6 +1466,8 @@ __global__ __launch_bounds__(1024) void k_dispatch(const uint32_t* __restrict__ 
 // 4*(i/16)+ks inside a 16-column group, so each lane fetches 4 consecutive
 // columns of A and B with one 128-bit LDS read.
 constexpr uint32_t TM = 64, LDS_STRIDE = 68;
+// slot_of entry of an expert that is not in the device slots for this pass.
+constexpr uint32_t NO_SLOT = 0xffffffffu;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -1475,13 +1477,17 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
                                               uint32_t kdim, const float* __restrict__ a_src,
                                               const uint32_t* __restrict__ pairs, uint32_t K,
                                               const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
-                                              float* __restrict__ out) {
+                                              float* __restrict__ out, const uint32_t* __restrict__ slot_of) {
     using Fm = Fmt<KIND>;
     __shared__ float As[TM * LDS_STRIDE];
     __shared__ float Bs[128 * LDS_STRIDE];
     const uint32_t* tile = tiles + 4u * blockIdx.y;
     const uint32_t n = tile[2];
     if (n == 0) return;
+    // Cached experts (slot_of != NULL): the tile's expert lives in slot
+    // slot_of[e] of the weight arrays, or is not resident in this pass (NO_SLOT).
+    const uint32_t ew = slot_of ? slot_of[tile[0]] : tile[0];
+    if (ew == NO_SLOT) return;
     if constexpr (has_codebook<KIND>()) {
         stage_codebooks<KIND>();
         __syncthreads();
@@ -1511,9 +1517,9 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
         const uint8_t* base = brow < 64 ? w0 : w1;
         uint64_t st = brow < 64 ? stride0 : stride1;
         uint32_t r = row0 + (brow & 63u);
-        bptr = base + ((uint64_t)e * rows_per_expert + r) * st;
+        bptr = base + ((uint64_t)ew * rows_per_expert + r) * st;
     } else {
-        bptr = w0 + ((uint64_t)e * rows_per_expert + row0 + brow) * stride0;
+        bptr = w0 + ((uint64_t)ew * rows_per_expert + row0 + brow) * stride0;
     }
 
     // Only the first ceil(n / 16) 16-row blocks of the tile issue MFMAs.
@@ -1782,7 +1788,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     const uint32_t* __restrict__ pairs, uint32_t K, const uint32_t* __restrict__ tiles, uint32_t ldo, float limit,
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows, const float* __restrict__ xstat, uint32_t* __restrict__ rowmax,
-    uint32_t* __restrict__ flags) {
+    uint32_t* __restrict__ flags, const uint32_t* __restrict__ slot_of) {
     static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 22 || KIND == 23,
                   "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
@@ -1828,6 +1834,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     const uint32_t* tile = tiles + 4u * t;
     const uint32_t n = tile[2];
     if (n == 0) return;
+    // Cached experts (slot_of != NULL, entry E for the shared expert's tiles):
+    // the expert's weights are in slot slot_of[e], or it is not resident in this
+    // pass (NO_SLOT) and the tile waits for a later one.
+    const uint32_t ew = slot_of ? slot_of[tile[0]] : tile[0];
+    if (ew == NO_SLOT) return;
     if constexpr (!Q4K) {
         stage_f16_tables<KIND>();
         __syncthreads();
@@ -1880,8 +1891,8 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
     }
     const bool sh_tile = e == e_shared;
-    const uint8_t* const wb0 = sh_tile ? ws0 : w0 + (uint64_t)e * rows_per_expert * stride0;
-    const uint8_t* const wb1 = GATEUP ? (sh_tile ? ws1 : w1 + (uint64_t)e * rows_per_expert * stride1) : wb0;
+    const uint8_t* const wb0 = sh_tile ? ws0 : w0 + (uint64_t)ew * rows_per_expert * stride0;
+    const uint8_t* const wb1 = GATEUP ? (sh_tile ? ws1 : w1 + (uint64_t)ew * rows_per_expert * stride1) : wb0;
     const __amdgpu_buffer_rsrc_t ra_h = make_rsrc(ah, (uint32_t)(kdim * 2u) * a_rows);
     const __amdgpu_buffer_rsrc_t ra_l = make_rsrc(al, (uint32_t)(kdim * 2u) * a_rows);
     const __amdgpu_buffer_rsrc_t rgs = make_rsrc(gs, ngroups * 4u * a_rows);

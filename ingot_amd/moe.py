@@ -332,19 +332,34 @@ class LayerSpec:
 
 
 class MoeLayer:
-    """A resident MoE layer on one GPU (every expert in HBM)."""
+    """A MoE layer on one GPU: every expert resident in HBM, or, with
+    cache_slots, the routed experts kept in the spec's host bytes and copied on
+    demand into that many device slots (ingot_layer_create_cached; the
+    reference's ExpertWeights::Cached, src/weights.rs:46-95)."""
 
-    def __init__(self, gpu: Gpu, spec: Optional[LayerSpec], _handle=None):
+    def __init__(self, gpu: Gpu, spec: Optional[LayerSpec], _handle=None, cache_slots: Optional[int] = None):
         self.gpu = gpu
         self.spec = spec
+        self.cache_slots = cache_slots
         if _handle is not None:
             self.handle = _handle
             return
         d, keep = spec.c()
         h = C.c_void_p()
-        gpu._check(gpu.lib.ingot_layer_create(gpu.ctx, C.byref(d), C.byref(h)))
+        if cache_slots is None:
+            gpu._check(gpu.lib.ingot_layer_create(gpu.ctx, C.byref(d), C.byref(h)))
+        else:
+            gpu._check(gpu.lib.ingot_layer_create_cached(gpu.ctx, C.byref(d), cache_slots, C.byref(h)))
+            # the library reads the experts from these host bytes for the layer's lifetime
+            self._host_experts = (keep, spec.gate.data, spec.up.data, spec.down.data)
         del keep
         self.handle = h.value
+
+    def cache_stats(self) -> dict:
+        """Cached layer: {"hits", "misses", "bytes"} since creation."""
+        v = [C.c_uint64() for _ in range(3)]
+        self.gpu._check(self.gpu.lib.ingot_layer_cache_stats(self.handle, *(C.byref(x) for x in v)))
+        return {"hits": v[0].value, "misses": v[1].value, "bytes": v[2].value}
 
     def clone(self) -> "MoeLayer":
         h = C.c_void_p()
