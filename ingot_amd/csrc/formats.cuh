@@ -238,6 +238,9 @@ __device__ inline void stage_f16_tables() {
     if constexpr (KIND == 22) {
         for (uint32_t i = threadIdx.x; i < 1024u; i += blockDim.x) lds_iq2s_grid()[i] = ingot_iq2s_grid[i];
         for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_sign8mask()[i] = sign_mask8(i);
+    } else if constexpr (KIND == 21) {
+        for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq3s_grid()[i] = ingot_iq3s_grid[i];
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_sign8mask()[i] = sign_mask8(i);
     } else if constexpr (KIND == 17) {
         for (uint32_t i = threadIdx.x; i < 512u; i += blockDim.x) lds_iq2xs_grid()[i] = ingot_iq2xs_grid[i];
         for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {

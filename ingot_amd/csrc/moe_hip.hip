@@ -300,13 +300,13 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
 }
 
 // Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K;
-// IQ2_XS, IQ2_S and IQ3_XXS when their rows are a whole number of dwords (kdim % 512
+// IQ2_XS, IQ2_S, IQ3_XXS and IQ3_S when their rows are a whole number of dwords (kdim % 512
 // == 0; their loads assume 4-byte aligned rows); IQ4_NL and IQ4_XS (A read permuted:
 // x as split by the dispatch, act as stored by the gate/up kernel).
 bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
     switch (kind) {
         case 12: case 13: return kdim % 256 == 0;
-        case 17: case 18: case 22: return kdim % 512 == 0;
+        case 17: case 18: case 21: case 22: return kdim % 512 == 0;
         case 20: return kdim % 64 == 0;
         case 23: return kdim % 256 == 0;
         default: return false;
@@ -315,7 +315,9 @@ bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
 
 // Column order of A that an f16 GEMM over weights of `kind` reads.
 int a_order(uint32_t kind) {
-    return (kind == 20 || kind == 23) ? A_IQ4NL : (kind == 17 || kind == 18 || kind == 22) ? A_IQ3XXS : A_NATURAL;
+    return (kind == 20 || kind == 23) ? A_IQ4NL
+           : (kind == 17 || kind == 18 || kind == 21 || kind == 22) ? A_IQ3XXS
+                                                                    : A_NATURAL;
 }
 
 // Formats with a 128-token-tile instantiation of the f16 GEMM (tt128):
@@ -348,6 +350,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 gr
             case 17: F16_GU(17, 64)
             case 18: F16_GU(18, 64)
             case 20: F16_GU(20, 64)
+            case 21: F16_GU(21, 64)
             case 22: F16_GU(22, 64)
             case 23: F16_GU(23, 64)
             default: return false;
@@ -366,6 +369,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 gr
             case 17: F16(17, A_NATURAL, 64); return true;
             case 18: F16(18, A_NATURAL, 64); return true;
             case 20: F16(20, A_NATURAL, 64); return true;
+            case 21: F16(21, A_NATURAL, 64); return true;
             case 22: F16(22, A_NATURAL, 64); return true;
             case 23: F16(23, A_NATURAL, 64); return true;
             default: return false;

@@ -1789,8 +1789,9 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows, const float* __restrict__ xstat, uint32_t* __restrict__ rowmax,
     uint32_t* __restrict__ flags, const uint32_t* __restrict__ slot_of) {
-    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 22 || KIND == 23,
-                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ4_NL, IQ4_XS");
+    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 21 || KIND == 22 ||
+                      KIND == 23,
+                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
     static_assert(TT == 64 || TT == 128, "tiles of 64 or 128 tokens");
     // NB: 16-row B blocks per wave (gate/up: HB = NB / 2 gate, HB up); NW waves.
@@ -1812,13 +1813,18 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // and 8 sign bytes at 34 + 8 kq, the index high bits (66) and scales (74)
     // of its two 32-value groups among the 16 bytes at 66; B = (1 + 2 s) *
     // grid * sign <= 31 * 43 and the unit d * 2^21, as for IQ2_XS.
-    constexpr bool IQ2 = KIND == 17, IQ2S = KIND == 22, IQG = IQ2 || IQ2S || IQ3;
+    // IQ3_S too (110-byte superblocks, kernels/moe.metal:65-75): lane kq's 16
+    // grid-index bytes at 2 + 16 kq (as IQ3_XXS's grid bytes; 4-value entries
+    // of the 512-entry grid), the ninth index bit from qh[2 kq], qh[2 kq + 1]
+    // (66), its 8 sign bytes at 74 + 8 kq, the scale byte 106 + kq (a nibble per
+    // 32-value group). B = (1 + 2 s) * grid * sign <= 31 * 15, unit d * 2^24.
+    constexpr bool IQ2 = KIND == 17, IQ2S = KIND == 22, IQ3S = KIND == 21, IQG = IQ2 || IQ2S || IQ3 || IQ3S;
     // IQ4_XS takes IQ4_NL's path (B = the codebook value, a unit per 32-column
     // block): its blocks' 16 quant bytes sit at 8 + 16 g of a 136-byte
     // superblock (dword aligned), and a block's unit is d * (scale - 32), the
     // 6-bit scale from the 8-byte superblock header read with each slab.
     constexpr bool IQ4X = KIND == 23, IQN = IQ4 || IQ4X;
-    constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : 98u;
+    constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : IQ3S ? 110u : 98u;
     constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
     constexpr uint32_t UNR = 4u;
     // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
@@ -1918,6 +1924,8 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     uint2 nqh[Q5K ? NB : 1];
     uint32_t n5[NB], n_d[NB];
     uint3 n3[NB], ns3[IQ2S ? NB : 1];
+    uint4 nqh3[IQ3S ? NB : 1];  // IQ3_S: bytes 64 .. 79 (qh) and 104 .. 111 (scales) of the superblock's dword window
+    uint2 nsc3[IQ3S ? NB : 1];
     auto load_hdr = [&](uint32_t sb) {
         sb = sb < sbs ? sb : sbs - 1u;
 #pragma unroll
@@ -1933,6 +1941,15 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 n3[nb] = make_uint3(q.x, q.y, buf_load4(rw, boff[nb] + 8u * kq, u + 8u));
                 const uint2 g = buf_load8(rw, boff[nb] + 8u * kq, u + 32u);
                 ns3[nb] = make_uint3(g.x, g.y, buf_load4(rw, boff[nb] + 8u * kq, u + 40u));
+                n_d[nb] = buf_load4(rw, boff[nb], u);
+            } else if constexpr (IQ3S) {
+                const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
+                nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);  // grid-index bytes
+                n5[nb] = buf_load4(rw, boff[nb] + 16u * kq, u + 16u);
+                const uint2 g = buf_load8(rw, boff[nb] + 8u * kq, u + 72u);  // sign bytes
+                n3[nb] = make_uint3(g.x, g.y, buf_load4(rw, boff[nb] + 8u * kq, u + 80u));
+                nqh3[nb] = buf_load16(rw, boff[nb], u + 64u);
+                nsc3[nb] = buf_load8(rw, boff[nb], u + 104u);
                 n_d[nb] = buf_load4(rw, boff[nb], u);
             } else if constexpr (IQG) {
                 const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
@@ -2019,6 +2036,21 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint32_t sc16 = ((kq < 2u ? h[2] : h[3]) >> sh) & 0xffffu;
                 st.aw[nb][0] = qh16 | (sc16 << 16);
                 st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
+            } else if constexpr (IQ3S) {
+                // gw: the lane's 16 grid-index bytes; aw: its 8 sign bytes; mn[0]:
+                // qh[2 kq], qh[2 kq + 1] in bits 0..15 and the scale byte in 16..23.
+                const bool odd = (sb & 1u) != 0u;
+                auto al = [&](uint32_t hi, uint32_t lo) { return odd ? hi : __builtin_amdgcn_alignbit(hi, lo, 16u); };
+                const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) st.gw[nb][i] = al(w[i + 1], w[i]);
+                st.aw[nb][0] = al(n3[nb].y, n3[nb].x);
+                st.aw[nb][1] = al(n3[nb].z, n3[nb].y);
+                const uint32_t h0 = al(nqh3[nb].y, nqh3[nb].x), h1 = al(nqh3[nb].z, nqh3[nb].y);
+                const uint32_t qh16 = ((kq < 2u ? h0 : h1) >> (16u * (kq & 1u))) & 0xffffu;
+                const uint32_t sc8 = (al(nsc3[nb].y, nsc3[nb].x) >> (8u * kq)) & 255u;
+                st.mn[nb][0] = qh16 | (sc8 << 16);
+                st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
             } else if constexpr (IQG) {
                 const bool odd = (sb & 1u) != 0u;
                 const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
@@ -2071,6 +2103,24 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                     fb[nb][gi] = __builtin_bit_cast(
                         half8, make_uint4(mad_u16x2(bytes01(lo), f2, m.x), mad_u16x2(bytes23(lo), f2, m.y),
                                           mad_u16x2(bytes01(hi), f2, m.z), mad_u16x2(bytes23(hi), f2, m.w)));
+                }
+            } else if constexpr (IQ3S) {
+                // group 2 kq + sq / 2 of the superblock, its 8-value pieces l = 2 (sq & 1) + gi
+                const uint32_t gq = sq >> 1, x = st.mn[nb][0];
+                const uint32_t qh8 = (x >> (8u * gq)) & 255u;
+                const uint32_t f = st.sc[nb][0] * (2u * ((x >> (16u + 4u * gq)) & 15u) + 1u);
+                const uint32_t f2 = f | (f << 16);
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    const uint32_t l = 2u * (sq & 1u) + (uint32_t)gi;
+                    const uint32_t wq = st.gw[nb][2u * gq + (l >> 1)] >> (16u * (l & 1u));
+                    const uint32_t i0 = (wq & 255u) | (((qh8 >> (2u * l)) & 1u) << 8);
+                    const uint32_t i1 = ((wq >> 8) & 255u) | (((qh8 >> (2u * l + 1u)) & 1u) << 8);
+                    const uint32_t e0 = lds_iq3s_grid()[i0], e1 = lds_iq3s_grid()[i1];
+                    const uint4 m = lds_sign8mask()[(st.aw[nb][gq] >> (8u * l)) & 255u];
+                    fb[nb][gi] = __builtin_bit_cast(
+                        half8, make_uint4(mad_u16x2(bytes01(e0), f2, m.x), mad_u16x2(bytes23(e0), f2, m.y),
+                                          mad_u16x2(bytes01(e1), f2, m.z), mad_u16x2(bytes23(e1), f2, m.w)));
                 }
             } else if constexpr (IQ2) {
                 const uint32_t g = st.gw[nb][sq];  // codes 8 kq + 2 sq (low half) and + 1
@@ -2145,7 +2195,8 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
     constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : IQ4X ? 3u * NB : 0u;
-    constexpr uint32_t B_PER_SB = Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : IQ2S ? 7u * NB : IQG ? 5u * NB : 0u;
+    constexpr uint32_t B_PER_SB =
+        Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : (IQ2S || IQ3S) ? 7u * NB : IQG ? 5u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
         constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;

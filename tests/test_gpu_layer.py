@@ -232,7 +232,8 @@ def test_shared_expert_gated_and_ungated(gpu, oracle):
         layer.destroy()
 
 
-BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ4_NL: 18, IQ4_XS: 136}  # f16 d first
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110, IQ4_NL: 18,
+               IQ4_XS: 136}  # f16 d first
 
 
 def zero_scales(m, every=7, phase=3):
@@ -251,7 +252,8 @@ def zero_scales(m, every=7, phase=3):
                                       (IQ2_XS, IQ4_NL, 512), (Q4_K, IQ2_XS, 256), (IQ4_NL, IQ4_NL, 512),
                                       (IQ4_NL, Q4_K, 256), (IQ4_XS, IQ4_XS, 512), (Q4_K, IQ4_XS, 512),
                                       (IQ4_XS, IQ2_XS, 256), (IQ2_S, IQ2_S, 512), (IQ2_S, IQ4_XS, 512),
-                                      (Q4_K, IQ2_S, 256)])
+                                      (Q4_K, IQ2_S, 256), (IQ3_S, IQ3_S, 512), (IQ2_S, IQ3_S, 256),
+                                      (IQ3_S, IQ4_NL, 512)])
 def test_f16_gemm_formats_shared_and_zero_scales(gpu, oracle, gk, dk, sf):
     """Every format pair the f16 grouped GEMM takes, with a shared expert that joins its launches
     (same formats and width, sf == 512) or runs on the fp32 GEMM beside them (sf == 256), and
