@@ -299,13 +299,14 @@ bool launch_gemm(hipStream_t s, uint32_t kind, dim3 grid, const uint8_t* w0, con
     }
 }
 
-// Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K;
-// IQ2_XS, IQ2_S, IQ3_XXS and IQ3_S when their rows are a whole number of dwords (kdim % 512
-// == 0; their loads assume 4-byte aligned rows); IQ4_NL and IQ4_XS (A read permuted:
-// x as split by the dispatch, act as stored by the gate/up kernel).
+// Formats the f16 grouped GEMM decodes, for a matrix of kdim columns: Q4_K, Q5_K,
+// Q6_K; IQ2_XS, IQ2_S, IQ3_XXS and IQ3_S when their rows are a whole number of dwords
+// (kdim % 512 == 0; their loads assume 4-byte aligned rows); IQ4_NL and IQ4_XS (A read
+// permuted: x as split by the dispatch, act as stored by the gate/up kernel).
 bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
     switch (kind) {
         case 12: case 13: return kdim % 256 == 0;
+        case 14: return kdim % 256 == 0;
         case 17: case 18: case 21: case 22: return kdim % 512 == 0;
         case 20: return kdim % 64 == 0;
         case 23: return kdim % 256 == 0;
@@ -317,12 +318,14 @@ bool f16_gemm_kind(uint32_t kind, uint32_t kdim, bool gateup) {
 int a_order(uint32_t kind) {
     return (kind == 20 || kind == 23) ? A_IQ4NL
            : (kind == 17 || kind == 18 || kind == 21 || kind == 22) ? A_IQ3XXS
+           : kind == 14                                             ? A_Q6K
                                                                     : A_NATURAL;
 }
 
 // Formats with a 128-token-tile instantiation of the f16 GEMM (tt128):
-// Q4_K and Q5_K, whose B operands need no LDS tables.
-bool f16_tt128_kind(uint32_t kind) { return kind == 12 || kind == 13; }
+// Q4_K, Q5_K and Q6_K, whose B operands need no LDS tables. Q6_K has only
+// that one (it also runs the 64-token tiles of a batch without tt128).
+bool f16_tt128_kind(uint32_t kind) { return kind == 12 || kind == 13 || kind == 14; }
 
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
 // projection's a_order); tt128: tiles of up to 128 tokens (f16_tt128_kind).
@@ -333,6 +336,7 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 gr
     switch (aord) {                                             \
         case A_IQ4NL: F16(KV, A_IQ4NL, TT); return true;        \
         case A_IQ3XXS: F16(KV, A_IQ3XXS, TT); return true;      \
+        case A_Q6K: F16(KV, A_Q6K, TT); return true;            \
         case A_F32: F16(KV, A_F32, TT); return true;            \
         default: F16(KV, A_NATURAL, TT); return true;           \
     }
@@ -341,12 +345,14 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 gr
             switch (kind) {
                 case 12: F16_GU(12, 128)
                 case 13: F16_GU(13, 128)
+                case 14: F16_GU(14, 128)
                 default: return false;
             }
         }
         switch (kind) {
             case 12: F16_GU(12, 64)
             case 13: F16_GU(13, 64)
+            case 14: F16_GU(14, 128)
             case 17: F16_GU(17, 64)
             case 18: F16_GU(18, 64)
             case 20: F16_GU(20, 64)
@@ -360,12 +366,14 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 gr
             switch (kind) {
                 case 12: F16(12, A_NATURAL, 128); return true;
                 case 13: F16(13, A_NATURAL, 128); return true;
+                case 14: F16(14, A_NATURAL, 128); return true;
                 default: return false;
             }
         }
         switch (kind) {
             case 12: F16(12, A_NATURAL, 64); return true;
             case 13: F16(13, A_NATURAL, 64); return true;
+            case 14: F16(14, A_NATURAL, 128); return true;
             case 17: F16(17, A_NATURAL, 64); return true;
             case 18: F16(18, A_NATURAL, 64); return true;
             case 20: F16(20, A_NATURAL, 64); return true;

@@ -1667,6 +1667,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ w0, co
 //   writes fp32 Y [P][ldo].
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef short short2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // Column orders of an A operand (x split, act) in HBM; a_pos maps a column to
 // its stored position.
@@ -1678,7 +1679,10 @@ typedef short short2v __attribute__((ext_vector_type(2)));
 //     4 of them (16 columns) in slab sq, so slab sq's A is one contiguous run.
 //   A_F32: act in natural order as fp32 (out), for a down projection that
 //     runs on the fp32 GEMM (a format without an f16 path).
-enum : int { A_NATURAL = 0, A_IQ4NL = 1, A_IQ3XXS = 2, A_F32 = 3 };
+//   A_Q6K: bits 5 and 6 of the column index swapped, column 128 n + 64 g +
+//     32 p + c -> 128 n + 64 p + 32 g + c (c < 32): slab 2 n + p of a Q6_K
+//     superblock holds the low-nibble and high-nibble columns of its ql bytes.
+enum : int { A_NATURAL = 0, A_IQ4NL = 1, A_IQ3XXS = 2, A_F32 = 3, A_Q6K = 4 };
 template <int ORD>
 __device__ __forceinline__ uint32_t a_pos(uint32_t c) {
     if constexpr (ORD == A_IQ4NL) {
@@ -1686,6 +1690,8 @@ __device__ __forceinline__ uint32_t a_pos(uint32_t c) {
         return (c & ~31u) | (8u * ((k & 15u) >> 2) + 2u * (k & 3u) + (k >> 4));
     } else if constexpr (ORD == A_IQ3XXS) {
         return (c & ~255u) | (((c >> 4) & 3u) << 6) | (((c >> 6) & 3u) << 4) | (c & 15u);
+    } else if constexpr (ORD == A_Q6K) {
+        return (c & ~96u) | (((c >> 5) & 1u) << 6) | (((c >> 6) & 1u) << 5);
     }
     return c;
 }
@@ -1789,9 +1795,9 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     float* __restrict__ out, _Float16* __restrict__ out_h, _Float16* __restrict__ out_l, float* __restrict__ out_gs,
     uint32_t nblk, uint32_t a_rows, const float* __restrict__ xstat, uint32_t* __restrict__ rowmax,
     uint32_t* __restrict__ flags, const uint32_t* __restrict__ slot_of) {
-    static_assert(KIND == 12 || KIND == 13 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 21 || KIND == 22 ||
-                      KIND == 23,
-                  "f16 GEMM formats: Q4_K, Q5_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS");
+    static_assert(KIND == 12 || KIND == 13 || KIND == 14 || KIND == 17 || KIND == 18 || KIND == 20 || KIND == 21 ||
+                      KIND == 22 || KIND == 23,
+                  "f16 GEMM formats: Q4_K, Q5_K, Q6_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ4_NL, IQ4_XS");
     static_assert(AORD == A_NATURAL || GATEUP, "the permuted act layout is written by the gate/up kernel");
     static_assert(TT == 64 || TT == 128, "tiles of 64 or 128 tokens");
     // NB: 16-row B blocks per wave (gate/up: HB = NB / 2 gate, HB up); NW waves.
@@ -1824,7 +1830,26 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // superblock (dword aligned), and a block's unit is d * (scale - 32), the
     // 6-bit scale from the 8-byte superblock header read with each slab.
     constexpr bool IQ4X = KIND == 23, IQN = IQ4 || IQ4X;
-    constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : IQ3S ? 110u : 98u;
+    // Q6_K (210-byte superblocks, kernels/moe.metal:22-28): w = d sc (q - 32),
+    // q = 4 bits of ql | 2 bits of qh, sc an int8 per 16 columns; |sc (q - 32)|
+    // reaches 4096, past the 2048 that f16 holds exactly, so B enters twice:
+    // B_r = sc (q - 32) rounded to f16 (an integer, exact up to 2048, even
+    // above) and B_e = sc (q - 32) - B_r in {-1, 0, 1} (one f16 fma, exact),
+    // with MFMAs A hi x B_r, A hi x B_e, A lo x B_r (A lo x B_e is below 2^-22
+    // of the product). B is integer-valued (no 2^-24 unit): D = d. Slab sq of a
+    // superblock is half n = sq / 2, p = sq % 2; lane kq reads ql bytes
+    // 64 n + 32 p + 8 kq .. + 7 (low nibbles: columns 128 n + 32 p + l, MFMA 0;
+    // high: + 64, MFMA 1; l = 8 kq + j) and the qh bytes 32 n + 8 kq .. + 7 of
+    // its half (once per half), so A is stored with bits 5 and 6 of each column
+    // index swapped (A_Q6K). A lane's superblock may start 2 bytes off a dword
+    // (210-byte superblocks, rows of any multiple of 256 columns): its loads
+    // take the dword-aligned window and shift by 16 bits where it does (no
+    // byte it uses sits in a dword past its superblock), and d comes from a
+    // 16-bit load.
+    constexpr bool Q6K = KIND == 14;
+    // (two operand sets per fragment: TT 128's 2 row blocks per wave fit the registers, 4 do not)
+    static_assert(!Q6K || TT == 128, "Q6_K runs on 128-token tiles (which also take tiles of 64)");
+    constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : IQ3S ? 110u : Q6K ? 210u : 98u;
     constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
     constexpr uint32_t UNR = 4u;
     // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
@@ -1845,7 +1870,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // pass (NO_SLOT) and the tile waits for a later one.
     const uint32_t ew = slot_of ? slot_of[tile[0]] : tile[0];
     if (ew == NO_SLOT) return;
-    if constexpr (!Q4K) {
+    if constexpr (!Q4K && !Q6K) {
         stage_f16_tables<KIND>();
         __syncthreads();
     }
@@ -1917,6 +1942,12 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
     }
     const uint32_t slabs = kdim / 64u, sbs = kdim / 256u;
+    // Q6_K: each lane's row start (bytes from the expert's base)
+    uint32_t q6r[Q6K ? NB : 1];
+    if constexpr (Q6K) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) q6r[nb] = bsoff[nb] + boff[nb];
+    }
 
     float4 ps;
 #define INGOT_LOAD_S(SB) ps = __builtin_bit_cast(float4, buf_load16(rgs, soff, 32u * ((SB) < sbs ? (SB) : sbs - 1u)))
@@ -1960,18 +1991,37 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint2 a = buf_load8(rw, ao, u + 64u);
                 n3[nb] = make_uint3(a.x, a.y, buf_load4(rw, ao, u + 72u));
                 n_d[nb] = buf_load4(rw, boff[nb], u);
+            } else if constexpr (Q6K) {
+                // the 16 scale bytes (192) in a 20-byte window, d (208)
+                const uint32_t b = q6r[nb] + sb * IQB, a = b & ~3u;
+                nhdr[nb] = buf_load16(rw, a, 192u);
+                n5[nb] = buf_load4(rw, a, 208u);
+                n_d[nb] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)b, 208, 0);
             }
         }
     };
     uint4 nq[4][NB];
     uint32_t n1[4][NB];
     uint2 nd[4][NB];
-    auto load_slab = [&](uint32_t rs, uint32_t s) {
+    // Q6_K: ev (the slab is the first of its half, a compile-time constant at
+    // each call) also loads the half's qh window.
+    auto load_slab = [&](uint32_t rs, uint32_t s, bool ev = false) {
         s = s < slabs ? s : slabs - 1u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= (int)HB ? rw1 : rw0;
-            if constexpr (Q4K) {
+            if constexpr (Q6K) {
+                const uint32_t a = (q6r[nb] + 8u * kq + (s >> 2) * IQB) & ~3u, hn = (s >> 1) & 1u;
+                const auto l = __builtin_amdgcn_raw_buffer_load_b96(rw, (int)a, (int)(64u * hn + 32u * (s & 1u)), 0);
+                nq[rs][nb].x = l[0];
+                nq[rs][nb].y = l[1];
+                nq[rs][nb].z = l[2];
+                if (ev) {
+                    const auto h = __builtin_amdgcn_raw_buffer_load_b96(rw, (int)a, (int)(128u + 32u * hn), 0);
+                    nq[rs][nb].w = h[0];
+                    nd[rs][nb] = make_uint2(h[1], h[2]);
+                }
+            } else if constexpr (Q4K) {
                 const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * SBB + QOFF + 32u * (s & 3u));
                 nq[rs][nb].x = v.x;
                 nq[rs][nb].y = v.y;
@@ -1992,11 +2042,12 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     };
     auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
         if constexpr (IQG) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
+        if constexpr (Q6K) return n_d[nb];
         return nhdr[nb].x;
     };
     auto unit = [](uint32_t bits) {
         const float d = half_bits_to_float(bits);
-        return d != 0.f ? d * ((IQ2 || IQ2S) ? 2097152.f : IQ3 ? 4194304.f : 16777216.f) : 1.f;
+        return d != 0.f ? d * ((IQ2 || IQ2S) ? 2097152.f : IQ3 ? 4194304.f : Q6K ? 1.f : 16777216.f) : 1.f;
     };
     // Superblock state for the decode (and, at the superblock's end, the mins
     // and the unit change).
@@ -2005,6 +2056,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
         uint2 qh[Q5K ? NB : 1];
         uint32_t gw[NB][4], aw[NB][2];
         float dsc[NB], dmn[NB];
+        uint32_t sh[Q6K ? NB : 1];  // Q6_K: the lane's superblock misalignment in bits (0 or 16)
     };
     auto take_hdr = [&](SbState& st, uint32_t sb) {
 #pragma unroll
@@ -2060,16 +2112,64 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
                 for (int i = 0; i < 2; ++i) st.aw[nb][i] = odd ? v[i + 1] : __builtin_amdgcn_alignbit(v[i + 1], v[i], 16u);
                 st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
+            } else if constexpr (Q6K) {
+                // gw: the 16 int8 scales (zero with d, which zeroes B)
+                st.sh[nb] = ((q6r[nb] + sb * IQB) & 2u) << 3;
+                const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
+                const bool z = half_bits_to_float(db) == 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) st.gw[nb][i] = z ? 0u : __builtin_amdgcn_alignbit(w[i + 1], w[i], st.sh[nb]);
             }
         }
     };
-    // Decode of slab position sq (within its superblock) into fb; IQ4_NL also
-    // yields the units of its two blocks and whether a d is zero.
+    // Q6_K: the qh words of the half being decoded (set at its first slab), and
+    // the perm selector of the lane's two scale bytes (byte kq / 2 of scale
+    // words 2 n, 2 n + 1; + 2 in a half's second slab).
+    uint2 qhc[Q6K ? NB : 1];
+    const uint32_t q6sel = 0x0c040c00u + (kq >> 1) * 0x00010001u;
+    // Decode of slab position sq (within its superblock) into fb (Q6_K: B_r
+    // into fb, B_e into fe); IQ4_NL also yields the units of its two blocks and
+    // whether a d is zero.
     auto decode = [&](const SbState& st, uint32_t sq, const uint4* qv, const uint2* dv, half8 (*fb)[2],
-                      float (*dg)[2]) {
+                      float (*dg)[2], half8 (*fe)[2]) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            if constexpr (Q4K) {
+            if constexpr (Q6K) {
+                const uint32_t p = sq & 1u, hn = sq >> 1;
+                if (p == 0u)
+                    qhc[nb] = make_uint2(__builtin_amdgcn_alignbit(dv[nb].x, qv[nb].w, st.sh[nb]),
+                                         __builtin_amdgcn_alignbit(dv[nb].y, dv[nb].x, st.sh[nb]));
+                const uint32_t L[2] = {__builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, st.sh[nb]),
+                                       __builtin_amdgcn_alignbit(qv[nb].z, qv[nb].y, st.sh[nb])};
+                const uint32_t H[2] = {qhc[nb].x, qhc[nb].y};
+                // int8 scale b -> f16 bits 0x6400 | (b ^ 0x80) = 1152 + sc
+                const uint32_t scw = __builtin_amdgcn_perm(st.gw[nb][2u * hn + 1u], st.gw[nb][2u * hn],
+                                                           q6sel + 0x00020002u * p) ^ 0x64806480u;
+                const half2v sc = __builtin_bit_cast(half2v, scw) - half2v{(_Float16)1152.f, (_Float16)1152.f};
+#pragma unroll
+                for (int gi = 0; gi < 2; ++gi) {
+                    const half2v s = gi ? __builtin_shufflevector(sc, sc, 1, 1) : __builtin_shufflevector(sc, sc, 0, 0);
+                    uint32_t r[4], e[4];
+#pragma unroll
+                    for (int w = 0; w < 2; ++w) {
+                        // 6-bit q of the 4 values: nibble gi of the ql bytes, qh bits 2 (p + 2 gi) + 0, 1
+                        const uint32_t q = gi ? ((L[w] >> 4) & 0x0f0f0f0fu) | ((H[w] >> (2u * p)) & 0x30303030u)
+                                              : (L[w] & 0x0f0f0f0fu) | ((H[w] << (4u - 2u * p)) & 0x30303030u);
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            // f16 bits 0x6400 | q = 1024 + q, minus 1056: q - 32
+                            const uint32_t x = __builtin_amdgcn_perm(0x64646464u, q, hh ? 0x04030402u : 0x04010400u);
+                            const half2v v = __builtin_bit_cast(half2v, x) - half2v{(_Float16)1056.f, (_Float16)1056.f};
+                            const half2v br = v * s;
+                            const half2v be = __builtin_elementwise_fma(v, s, -br);
+                            r[2 * w + hh] = __builtin_bit_cast(uint32_t, br);
+                            e[2 * w + hh] = __builtin_bit_cast(uint32_t, be);
+                        }
+                    }
+                    fb[nb][gi] = __builtin_bit_cast(half8, make_uint4(r[0], r[1], r[2], r[3]));
+                    fe[nb][gi] = __builtin_bit_cast(half8, make_uint4(e[0], e[1], e[2], e[3]));
+                }
+            } else if constexpr (Q4K) {
                 const uint32_t scw = st.sc[nb][sq >> 1] >> (16u * (sq & 1u));
                 const uint32_t s0_ = __builtin_amdgcn_perm(0u, scw, 0x0c000c00u);
                 const uint32_t s1_ = __builtin_amdgcn_perm(0u, scw, 0x0c010c01u);
@@ -2196,10 +2296,10 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // superblock's first slab its header (and Q4_K group sums).
     constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : IQ4X ? 3u * NB : 0u;
     constexpr uint32_t B_PER_SB =
-        Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : (IQ2S || IQ3S) ? 7u * NB : IQG ? 5u * NB : 0u;
+        Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : (IQ2S || IQ3S) ? 7u * NB : IQG ? 5u * NB : Q6K ? 3u * NB : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
-        constexpr uint32_t DEPTH = (!Q4K && MBE <= 2) ? 4u : 2u;
+        constexpr uint32_t DEPTH = (!Q4K && !Q6K && MBE <= 2) ? 4u : 2u;
         // Two operand sets let the decode of slab s + 1 interleave with slab s's
         // MFMAs; with 3-4 row blocks of 4 B blocks the registers hold one set
         // (IQ4_NL: two), and the decode follows the MFMAs in program order.
@@ -2233,10 +2333,10 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
             store_s(Ss[0]);
         }
 #pragma unroll
-        for (uint32_t d = 0; d < DEPTH; ++d) load_slab(d, d);
+        for (uint32_t d = 0; d < DEPTH; ++d) load_slab(d, d, (d & 1u) == 0u);
         SbState cur, nxt;
         if constexpr (!IQN) take_hdr(cur, 0u);
-        half8 fb[NFB][NB][2];
+        half8 fb[NFB][NB][2], fe[Q6K ? NFB : 1][NB][2];
         float dgs[NFB][NB][2];
         {
             uint4 qv[NB];
@@ -2244,13 +2344,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 qv[nb] = nq[0][nb];
-                if constexpr (IQN) {
-                    qv[nb].z = n1[0][nb];
-                    dv[nb] = nd[0][nb];
-                }
+                if constexpr (IQN) qv[nb].z = n1[0][nb];
+                if constexpr (IQN || Q6K) dv[nb] = nd[0][nb];
             }
-            load_slab(0, DEPTH);
-            decode(cur, 0u, qv, dv, fb[0], dgs[0]);
+            load_slab(0, DEPTH, true);
+            decode(cur, 0u, qv, dv, fb[0], dgs[0], fe[0]);
         }
         for (uint32_t s0 = 0; s0 < slabs; s0 += UNR) {
             const uint32_t sb = s0 >> 2;
@@ -2277,12 +2375,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     qv[nb] = nq[rs][nb];
-                    if constexpr (IQN) {
-                        qv[nb].z = n1[rs][nb];
-                        dv[nb] = nd[rs][nb];
-                    }
+                    if constexpr (IQN) qv[nb].z = n1[rs][nb];
+                    if constexpr (IQN || Q6K) dv[nb] = nd[rs][nb];
                 }
-                load_slab(rs, s + 1u + DEPTH);
+                // (s is a multiple of UNR plus sq: slab s + 1 + DEPTH opens a half when sq is odd)
+                load_slab(rs, s + 1u + DEPTH, (sq & 1u) != 0u);
                 if constexpr (!IQN) {
                     if (sq == 0) {
                         load_hdr(sb + 1);
@@ -2298,7 +2395,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint32_t cb = NFB == 2u ? (sq & 1u) : 0u, nb_ = NFB == 2u ? cb ^ 1u : 0u;
                 // (after the last slab: a decode of clamped bytes that nothing reads;
                 // kept unconditional so that the decode shares a block with the MFMAs)
-                if (NFB == 2u) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[nb_], dgs[nb_]);
+                if (NFB == 2u) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[nb_], dgs[nb_], fe[Q6K ? nb_ : 0u]);
                 const _Float16* const bh = (sq & 1u) ? Ah1 : Ah0;
                 const _Float16* const bl = (sq & 1u) ? Al1 : Al0;
                 if constexpr (!IQN) {
@@ -2315,17 +2412,27 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
                                 for (int nb = 0; nb < NB; ++nb)
                                     acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fb[cb][nb][gi], acc[mb][nb], 0, 0, 0);
+                                if constexpr (Q6K) {
+                                    if (part == 0) {
+#pragma unroll
+                                        for (int nb = 0; nb < NB; ++nb)
+                                            acc[mb][nb] =
+                                                __builtin_amdgcn_mfma_f32_16x16x32_f16(a, fe[cb][nb][gi], acc[mb][nb], 0, 0, 0);
+                                    }
+                                }
                             }
                     {
                         // Issue order within the slab: PF A-fragment reads ahead, then
                         // per fragment its NB MFMAs, the read PF fragments on and (with
                         // two operand sets) a share of the next slab's B decode (VALU),
                         // so that LDS latency and the decode hide behind the MFMAs.
-                        constexpr int NF = 4 * MBE, PF = 4, VPF = NFB == 2u ? (NB == 2 ? 2 : 4) : 0;
+                        // Q6_K: A hi fragments (the first MBE of each 2 MBE) feed 2 NB MFMAs.
+                        constexpr int NF = 4 * MBE, PF = 4, VPF = NFB == 2u ? (Q6K ? 4 * NB : NB == 2 ? 2 : 4) : 0;
                         __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
                         for (int f = 0; f < NF; ++f) {
-                            __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+                            if (Q6K && ((f / MBE) & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x008, 2 * NB, 0);
+                            else __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
                             if (f + PF < NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                             if (VPF > 0) __builtin_amdgcn_sched_group_barrier(0x002, VPF, 0);
                         }
@@ -2355,7 +2462,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                             }
                     }
                 }
-                if (NFB == 1u) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[0], dgs[0]);
+                if (NFB == 1u) decode(sq == 3 ? nxt : cur, (sq + 1u) & 3u, qv, dv, fb[0], dgs[0], fe[0]);
                 if constexpr (Q4K) {
                     if (sq == 3) {
                         half8 fm[NB];
@@ -2393,7 +2500,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                         // at the previous superblock's end, two barriers ago).
                         store_s(Ss[(sb + 1u) & 1u]);  // past the last superblock: clamped, unread
                     }
-                } else if constexpr (IQG) {
+                } else if constexpr (IQG || Q6K) {
                     if (sq == 3) {
 #pragma unroll
                         for (int nb = 0; nb < NB; ++nb) {
@@ -2410,7 +2517,12 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 // stay in flight) before the barrier that publishes it; the slab's
                 // MFMAs stay on this side of it.
                 __builtin_amdgcn_sched_barrier(0);
-                if (sq == 0 && !IQN) wait_vmcnt<B_PER_SLAB + B_PER_SB>();
+                if constexpr (Q6K) {
+                    // ql per slab, qh at odd sq (the load opens a half), the header at sq 0
+                    if (sq == 0) wait_vmcnt<NB + B_PER_SB>();
+                    else if (sq & 1u) wait_vmcnt<2u * NB>();
+                    else wait_vmcnt<NB>();
+                } else if (sq == 0 && !IQN) wait_vmcnt<B_PER_SLAB + B_PER_SB>();
                 else wait_vmcnt<B_PER_SLAB>();
             }
         }
@@ -2524,7 +2636,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 
 // x [T][H] fp32 -> xh, xl [T][H] f16 with x 2^e_t = xh + xl (+ O(2^-22 |x|)),
 // e_t = x_exp(max |x_t|) per token (xstat), stored in column order `order` (A_NATURAL;
-// A_IQ3XXS, whose permutation keeps runs of 4 columns together, H % 256 == 0;
+// A_IQ3XXS and A_Q6K, whose permutations keep runs of 4 columns together, H % 256 == 0;
 // or A_IQ4NL, which spreads them 2 apart within each 32-column block), and the
 // natural 32-column sums of x 2^e_t, xs [T][H/32], used by the Q4_K mins term.
 // Item g covers x[4g, 4g + 4) (8 consecutive items per 32-column group, so the
@@ -2545,7 +2657,9 @@ __device__ inline void split_f16_part(const float* __restrict__ x, uint64_t n, _
                 split_f16(a[j], xh[o], xl[o]);
             }
         } else {
-            const uint64_t o = order == A_IQ3XXS ? (i & ~255ull) | a_pos<A_IQ3XXS>((uint32_t)i & 255u) : i;
+            const uint64_t o = order == A_IQ3XXS ? (i & ~255ull) | a_pos<A_IQ3XXS>((uint32_t)i & 255u)
+                               : order == A_Q6K  ? (i & ~255ull) | a_pos<A_Q6K>((uint32_t)i & 255u)
+                                                 : i;
 #pragma unroll
             for (int j = 0; j < 4; ++j) split_f16(a[j], xh[o + j], xl[o + j]);
         }

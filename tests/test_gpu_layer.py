@@ -151,17 +151,17 @@ def test_remaining_formats_decode_and_prefill(gpu, oracle, gk, dk):
 
 @pytest.mark.parametrize("gemm_mode", ["auto", "fp32"])
 def test_f16_gate_up_with_fp32_down(gpu, oracle, gemm_mode):
-    """A Q4_K_M layer's shape: Q4_K gate/up on the f16 GEMM writing fp32 act for a
-    Q6_K down on the fp32 GEMM over the same tiles, with a shared expert beside
-    them; the fp32 mode forces both onto the fp32 GEMM."""
+    """Q4_K gate/up on the f16 GEMM writing fp32 act for a down format without an
+    f16 path (Q8_0) on the fp32 GEMM over the same tiles, with a shared expert
+    beside them; the fp32 mode forces both onto the fp32 GEMM."""
     from ingot_amd.moe import GEMM_FP32
-    spec = CF.make_layer(112, 0, 2048, 32, 8, 768, Q4_K, Q6_K, bias="zipf", shared_ffn=768,
-                         shared_down_kind=Q6_K, shared_gated=True)
+    spec = CF.make_layer(112, 0, 2048, 32, 8, 768, Q4_K, Q8_0, bias="zipf", shared_ffn=768,
+                         shared_down_kind=Q8_0, shared_gated=True)
     layer = MoeLayer(gpu, spec)
     if gemm_mode == "fp32":
         layer.set_gemm_mode(GEMM_FP32)
     for T in (9, 200):
-        check_layer(layer, spec, CF.inputs(212, T, 2048, seed=T), oracle, f"Q4_K/Q6_K {gemm_mode} T={T}")
+        check_layer(layer, spec, CF.inputs(212, T, 2048, seed=T), oracle, f"Q4_K/Q8_0 {gemm_mode} T={T}")
     if gemm_mode == "auto":
         from ingot_amd.moe import STAGE_DOWN, STAGE_GATEUP
         assert layer.stage_kernel(STAGE_GATEUP) == "k_gemm_f16<gate_up>"
@@ -232,17 +232,29 @@ def test_shared_expert_gated_and_ungated(gpu, oracle):
         layer.destroy()
 
 
-BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110, IQ4_NL: 18,
-               IQ4_XS: 136}  # f16 d first
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ2_XS: 74, IQ2_S: 82, IQ3_XXS: 98, IQ3_S: 110, IQ4_NL: 18,
+               IQ4_XS: 136}
+D_OFFSET = {Q6_K: 208}  # byte offset of the block's f16 d (0 for the others)
 
 
 def zero_scales(m, every=7, phase=3):
     """Sets d = 0 in every `every`-th block of a matrix (ggml writes such blocks for all-zero weights)."""
-    bb = BLOCK_BYTES[m.kind]
+    bb, do = BLOCK_BYTES[m.kind], D_OFFSET.get(m.kind, 0)
     nblk = m.stride // bb
     blocks = m.data.copy().reshape(m.rows * m.count, nblk, bb)
     hit = (np.arange(blocks.shape[0] * nblk).reshape(-1, nblk) % every) == phase
-    blocks[hit, 0:2] = 0
+    blocks[hit, do:do + 2] = 0
+    m.data = blocks.reshape(-1)
+
+
+def extreme_q6k_scales(m, seed):
+    """Q6_K blocks with int8 scales drawn over all of [-128, 127] (|sc (q - 32)| up
+    to 4096, odd products above 2048 included) and their d scaled down by 64."""
+    rng = np.random.default_rng(seed)
+    blocks = m.data.copy().reshape(-1, 210)
+    blocks[:, 192:208] = rng.integers(0, 256, (blocks.shape[0], 16), dtype=np.uint8)
+    d = blocks[:, 208:210].copy().view(np.float16) / np.float16(64)
+    blocks[:, 208:210] = d.view(np.uint8)
     m.data = blocks.reshape(-1)
 
 
@@ -253,7 +265,8 @@ def zero_scales(m, every=7, phase=3):
                                       (IQ4_NL, Q4_K, 256), (IQ4_XS, IQ4_XS, 512), (Q4_K, IQ4_XS, 512),
                                       (IQ4_XS, IQ2_XS, 256), (IQ2_S, IQ2_S, 512), (IQ2_S, IQ4_XS, 512),
                                       (Q4_K, IQ2_S, 256), (IQ3_S, IQ3_S, 512), (IQ2_S, IQ3_S, 256),
-                                      (IQ3_S, IQ4_NL, 512)])
+                                      (IQ3_S, IQ4_NL, 512), (Q6_K, Q6_K, 512), (Q4_K, Q6_K, 512),
+                                      (Q6_K, IQ4_NL, 256), (IQ3_XXS, Q6_K, 256)])
 def test_f16_gemm_formats_shared_and_zero_scales(gpu, oracle, gk, dk, sf):
     """Every format pair the f16 grouped GEMM takes, with a shared expert that joins its launches
     (same formats and width, sf == 512) or runs on the fp32 GEMM beside them (sf == 256), and
@@ -269,6 +282,29 @@ def test_f16_gemm_formats_shared_and_zero_scales(gpu, oracle, gk, dk, sf):
         assert layer.stage_kernel(STAGE_GATEUP) == "k_gemm_f16<gate_up>"
         assert layer.stage_kernel(STAGE_DOWN) == "k_gemm_f16<down>"
         assert not layer.last_fallback
+    layer.destroy()
+
+
+@pytest.mark.parametrize("extreme", [False, True])
+def test_f16_q6k_down_unaligned_rows(gpu, oracle, extreme):
+    """A Q4_K_M layer's shape (Qwen3-30B-A3B: F = 768, Q6_K down): 630-byte down
+    rows, so every other row's superblocks start 2 bytes off a dword; a shared
+    expert of the same formats in the same launches; blocks with d = 0; and
+    (extreme) scales over the whole int8 range, so that B = sc (q - 32) needs
+    its f16 remainder part."""
+    from ingot_amd.moe import STAGE_DOWN, STAGE_GATEUP
+    spec = CF.make_layer(113, int(extreme), 2048, 32, 8, 768, Q4_K, Q6_K, bias="zipf", shared_ffn=768,
+                         shared_gated=True)
+    for m in (spec.down, spec.shared[2]):
+        if extreme:
+            extreme_q6k_scales(m, seed=m.rows)
+        zero_scales(m)
+    layer = MoeLayer(gpu, spec)
+    for T in (9, 70, 200):
+        check_layer(layer, spec, CF.inputs(213, T, 2048, seed=T), oracle, f"Q4_K/Q6_K F=768 extreme={extreme} T={T}")
+        if T > 8:
+            assert layer.stage_kernel(STAGE_GATEUP) == "k_gemm_f16<gate_up>"
+            assert layer.stage_kernel(STAGE_DOWN) == "k_gemm_f16<down>"
     layer.destroy()
 
 
