@@ -858,19 +858,27 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     if constexpr (HX) stage_half_tables<KIND>();
     else stage_codebooks<KIND>();
     __shared__ float s_sv[64];  // weight input of each selection
-    uint32_t key[NE];
-    float wv[NE];
-    bool ok[NE];
-    const bool bad = route_keys<NE>(logits + (uint64_t)t * E, bias, E, sigmoid_mode, key, wv, ok);
     uint32_t eid[NP];
     float ev[NP];
+    bool bad;
+    if constexpr (NP == 1) {
+        uint32_t key[NE];
+        float wv[NE];
+        bool ok[NE];
+        bad = route_keys<NE>(logits + (uint64_t)t * E, bias, E, sigmoid_mode, key, wv, ok);
+        eid[0] = wave_kth<NE>(key, wv, ok, wave < K ? wave : 0u, ev[0]);
+    } else {
+        // Several pairs per wave: the whole selection once (one threshold
+        // search for the K-th key, then the ranks among the K) instead of a
+        // search per pair; lane k holds selection k.
+        uint32_t my_id;
+        float my_v;
+        bad = wave_route<NE>(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, my_id, my_v);
 #pragma unroll
-    for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GU_WAVES * n;
-        if (n == 0 || k < K) eid[n] = wave_kth<NE>(key, wv, ok, k < K ? k : 0u, ev[n]);
-        else {  // no such pair: re-read pair 0's rows (not stored)
-            eid[n] = eid[0];
-            ev[n] = ev[0];
+        for (int n = 0; n < NP; ++n) {
+            const uint32_t k = wave + GU_WAVES * n, kk = k < K ? k : 0u;  // no such pair: re-read pair 0's rows (not stored)
+            eid[n] = (uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)kk);
+            ev[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), (int)kk));
         }
     }
     // Weight loads of the wave's pairs k = wave + 8n (n < NP; K <= 8 NP);
