@@ -79,6 +79,18 @@ bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw
     return dec_gate_up_cpl<KIND, 16>(s, cpl, np, rpw, grid, a);
 }
 
+template <int KIND, int KS>
+bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid,
+                                const DecGateUpArgs& a, const uint8_t* sg, const uint8_t* su, uint64_t sgs,
+                                uint64_t sus, float* sact) {
+    // the configs[2] shape: 512 experts, one chunk per lane, two pairs per wave, 2 rows
+    if (a.E > 512 || a.E <= 128 || cpl != 1 || np != 2 || rpw != 2) return false;
+    hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F, a.H,
+                       a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags, a.act,
+                       sg, su, sgs, sus, sact);
+    return true;
+}
+
 template <int KD, int KS>
 bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a) {
 #define DD(V)                                                                                                      \
@@ -109,4 +121,10 @@ bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a
 #define INGOT_INSTANTIATE_FUSED(KD, KS) \
     namespace ingot {                   \
     template bool launch_dec_down_k<KD, KS>(hipStream_t, uint32_t, dim3, const DownArgs&); \
+    }
+#define INGOT_INSTANTIATE_FUSED_GATE_UP(KG, KS)                                                                  \
+    namespace ingot {                                                                                            \
+    template bool launch_dec_gate_up_fused_k<KG, KS>(hipStream_t, uint32_t, uint32_t, uint32_t, dim3,           \
+                                                     const DecGateUpArgs&, const uint8_t*, const uint8_t*, uint64_t, \
+                                                     uint64_t, float*);                                          \
     }

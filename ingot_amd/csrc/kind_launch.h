@@ -19,6 +19,9 @@
 
 // Routed down + shared down fused in one decode kernel: (down kind, shared down kind).
 #define INGOT_FUSED_DOWN(X) X(17, 8) X(12, 12) X(20, 20) X(8, 8)
+// (routed gate/up kind, shared gate/up kind) pairs whose shared expert runs in
+// the routed decode gate/up kernel's free pair slot.
+#define INGOT_FUSED_GATE_UP(X) X(17, 8)
 
 namespace ingot {
 
@@ -92,6 +95,12 @@ bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw
 // k_dec_down<KD, KS>: decode down + combine (+ shared expert when KS >= 0) + residual.
 template <int KD, int KS>
 bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a);
+// k_dec_gate_up2<KIND, .., KS>: the same with the shared expert (format KS, width F)
+// in wave 7's free pair slot (K < 8 np); false if no instantiation covers the shape.
+template <int KIND, int KS>
+bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid,
+                                const DecGateUpArgs& a, const uint8_t* sg, const uint8_t* su, uint64_t sgs,
+                                uint64_t sus, float* sact);
 
 #define INGOT_DECLARE_KIND(K)                                                                               \
     extern template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, dim3, const GateUpArgs&); \
@@ -108,5 +117,11 @@ INGOT_KINDS(INGOT_DECLARE_KIND)
     extern template bool launch_dec_down_k<KD, KS>(hipStream_t, uint32_t, dim3, const DownArgs&);
 INGOT_FUSED_DOWN(INGOT_DECLARE_FUSED)
 #undef INGOT_DECLARE_FUSED
+#define INGOT_DECLARE_FUSED_GU(KG, KS)                                                                          \
+    extern template bool launch_dec_gate_up_fused_k<KG, KS>(hipStream_t, uint32_t, uint32_t, uint32_t, dim3, \
+                                                            const DecGateUpArgs&, const uint8_t*, const uint8_t*, \
+                                                            uint64_t, uint64_t, float*);
+INGOT_FUSED_GATE_UP(INGOT_DECLARE_FUSED_GU)
+#undef INGOT_DECLARE_FUSED_GU
 
 }  // namespace ingot

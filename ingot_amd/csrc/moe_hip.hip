@@ -414,6 +414,28 @@ static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, c
     }
 }
 
+// The same with the shared expert (gate/up format skind, ffn width F) in the
+// routed kernel's free pair slot, for the pairs of INGOT_FUSED_GATE_UP; false
+// (nothing launched) when no instantiation covers the shape.
+static bool launch_dec_gate_up_fused(hipStream_t s, uint32_t kind, uint32_t skind, const uint8_t* g,
+                                     const uint8_t* u, uint64_t gs, uint64_t us, const uint8_t* sg, const uint8_t* su,
+                                     uint64_t sgs, uint64_t sus, uint32_t F, uint32_t H, uint32_t T, const float* x,
+                                     const float* xstat, const float* logits, const float* bias, uint32_t E,
+                                     uint32_t K, uint32_t mode, float scale, float limit, uint32_t* ids, float* w,
+                                     uint32_t* flags, float* act, float* sact) {
+    const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
+    if (K >= GU_WAVES * np) return false;  // no free pair slot
+    const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
+    const dim3 grid((F + rpw - 1) / rpw, T);
+    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act};
+#define FG_(KG, KS)                                                                                              \
+    if (kind == KG && skind == KS) return launch_dec_gate_up_fused_k<KG, KS>(s, cpl, np, rpw, grid, a, sg, su, sgs, \
+                                                                             sus, sact);
+    INGOT_FUSED_GATE_UP(FG_)
+#undef FG_
+    return false;
+}
+
 // Decode down + combine: routed-only for every kind, plus a fused shared expert
 // for the format pairs the configurations use (can_fuse_shared). Returns false
 // if no instantiation covers the shape.
@@ -1232,6 +1254,12 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         const float scale = L->scale;
         const bool hs = hs_;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
+            // a shared expert as wide as the routed ones joins the routed kernel where that is instantiated
+            if (hs && SF == F && sgate.kind == sup.kind &&
+                launch_dec_gate_up_fused(ss, gate.kind, sgate.kind, gate.d, up.d, gate.stride, up.stride, sgate.d,
+                                         sup.d, sgate.stride, sup.stride, F, H, T, xin, xstat, lg, b, E, K, mode,
+                                         scale, limit, ids, wts, flags, act, sact))
+                return;
             launch_dec_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, T, xin, xstat, lg, b, E, K,
                                mode, scale, limit, ids, wts, flags, act);
             if (hs)

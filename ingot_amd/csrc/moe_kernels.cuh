@@ -821,9 +821,14 @@ __device__ __forceinline__ void load_xh_ilv(const float4* __restrict__ s, uint32
 // each lane keeps its input chunks in registers. The formats with f16 input
 // pairs (half_x) split x 2^e_t (x_exp of the max in the router's xstat[t]) and
 // take 2^-e_t out of the row sums.
+//   KS >= 0: the shared expert (format KS, ffn width F, weights sgate/sup)
+// runs in the pair slot k = 8 NP - 1 of wave 7, which the routed pairs leave
+// free (K < 8 NP), writing sact[t][r] = SwiGLU (its gate is applied by the
+// down kernel); its input is staged a second time when its format takes the
+// other input form.
 constexpr uint32_t GU_WAVES = 8;
 
-template <int KIND, int CPL, int RPW, int NP, int NE>
+template <int KIND, int CPL, int RPW, int NP, int NE, int KS = -1>
 __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
                                                       uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
                                                       const float* __restrict__ x, const float* __restrict__ xstat,
@@ -831,10 +836,17 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                                                       const float* __restrict__ bias, uint32_t E, uint32_t K,
                                                       uint32_t sigmoid_mode, float scale, float limit,
                                                       uint32_t* __restrict__ ids, float* __restrict__ wts,
-                                                      uint32_t* __restrict__ flags, float* __restrict__ act) {
+                                                      uint32_t* __restrict__ flags, float* __restrict__ act,
+                                                      const uint8_t* __restrict__ sgate = nullptr,
+                                                      const uint8_t* __restrict__ sup = nullptr, uint64_t sgstride = 0,
+                                                      uint64_t sustride = 0, float* __restrict__ sact = nullptr) {
     using Fm = Fmt<KIND>;
     constexpr bool HX = half_x<KIND>();  // input staged as f16 pairs (split_h4)
+    constexpr int KSV = KS < 0 ? KIND : KS;
+    using Fs = Fmt<KSV>;
+    constexpr bool SH = KS >= 0, HS = SH && half_x<KSV>(), XS2 = SH && HS != HX;
     __shared__ float4 s_x4[1024];  // interleaved chunks (ilv_slot), H <= 4096
+    __shared__ float4 s_xs4[XS2 ? 1024 : 1];  // the shared expert's input form
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
     const uint32_t nch = H / 32u;
@@ -853,10 +865,14 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         xa[m] = xok[m] ? *reinterpret_cast<const float4*>(xt + Fm::col(c, 4u * (ji & 7u)))
                        : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const float xm = HX ? xstat[2u * t] : 0.f;
+    const float xm = (HX || HS) ? xstat[2u * t] : 0.f;
     // decoded only after the barrier that publishes s_x4
     if constexpr (HX) stage_half_tables<KIND>();
     else stage_codebooks<KIND>();
+    if constexpr (SH && KSV != KIND) {
+        if constexpr (HS) stage_half_tables<KSV>();
+        else stage_codebooks<KSV>();
+    }
     __shared__ float s_sv[64];  // weight input of each selection
     uint32_t eid[NP];
     float ev[NP];
@@ -900,6 +916,23 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
         }
     }
+    // the shared expert's rows (wave 7)
+    const bool shw = SH && wave == GU_WAVES - 1u;
+    typename Fs::Raw sg[SH ? RPW : 1][SH ? CPL : 1], su[SH ? RPW : 1][SH ? CPL : 1];
+    if constexpr (SH) {
+        if (shw) {
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) {
+                const uint32_t r = min(r0 + i, F - 1);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const uint32_t c = min(lane + 64u * j, nch - 1);
+                    sg[i][j] = Fs::load_raw(sgate + (uint64_t)r * sgstride, c);
+                    su[i][j] = Fs::load_raw(sup + (uint64_t)r * sustride, c);
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
         const uint32_t k = wave + GU_WAVES * n;
@@ -911,7 +944,10 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     const int xe = x_exp(xm);
 #pragma unroll
     for (int m = 0; m < 2; ++m)
-        if (xok[m]) s_x4[threadIdx.x + 512u * m] = HX ? split_h4(ldexp4(xa[m], xe)) : xa[m];
+        if (xok[m]) {
+            s_x4[threadIdx.x + 512u * m] = HX ? split_h4(ldexp4(xa[m], xe)) : xa[m];
+            if constexpr (XS2) s_xs4[threadIdx.x + 512u * m] = HS ? split_h4(ldexp4(xa[m], xe)) : xa[m];
+        }
     __syncthreads();
     // Routing weights in selection order; block 0's wave 0 publishes them.
     const float w = wave_route_weight(lane < K ? s_sv[lane] : 0.f, K, sigmoid_mode, scale);
@@ -970,6 +1006,52 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                 }
                 if (k < K && lane == (uint32_t)i && r0 + i < F)
                     act[((uint64_t)t * K + k) * F + r0 + i] = swiglu(g, u, limit) * wk[n];
+            }
+        }
+    }
+    if constexpr (SH) {
+        if (shw) {
+            float gs[RPW], us[RPW];
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) gs[i] = us[i] = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = lane + 64u * j;
+                if (c >= nch) continue;
+                if constexpr (HS) {
+                    uint32_t sh[16], sl[16];
+                    if constexpr (XS2) load_xh_ilv(s_xs4, j, lane, sh, sl);
+                    else load_xh_ilv(s_x4, j, lane, sh, sl);
+#pragma unroll
+                    for (int i = 0; i < RPW; ++i) {
+                        gs[i] += Fs::dot_raw_h(sg[i][j], sh, sl);
+                        us[i] += Fs::dot_raw_h(su[i][j], sh, sl);
+                    }
+                } else {
+                    float sv[32];
+                    if constexpr (XS2) load_x_ilv(s_xs4, j, lane, sv);
+                    else load_x_ilv(s_x4, j, lane, sv);
+                    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        s0 += sv[q];
+                        s1 += sv[16 + q];
+                    }
+#pragma unroll
+                    for (int i = 0; i < RPW; ++i) {
+                        gs[i] += Fs::dot_raw(sg[i][j], c, sv, s0, s1);
+                        us[i] += Fs::dot_raw(su[i][j], c, sv, s0, s1);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) {
+                float g = wave_sum_dpp(gs[i]), u = wave_sum_dpp(us[i]);
+                if constexpr (HS) {
+                    g = ldexpf(g, -xe);
+                    u = ldexpf(u, -xe);
+                }
+                if (lane == (uint32_t)i && r0 + i < F) sact[(uint64_t)t * F + r0 + i] = swiglu(g, u, limit);
             }
         }
     }
