@@ -250,10 +250,11 @@ uint64_t ingot_layer_static_bytes(const ingot_layer* layer, uint32_t T);
 int ingot_layer_forward_add(ingot_layer* layer, const float* d_x, const float* d_a, uint32_t T, float* d_out,
                             uint32_t* d_ids, float* d_weights);
 /* Prefill GEMM arithmetic. INGOT_GEMM_AUTO (default): experts in Q4_K, Q5_K,
- * IQ2_XS, IQ2_S, IQ3_XXS (rows of a multiple of 512 columns), IQ4_NL and
- * IQ4_XS use the split-precision f16 MFMA GEMM (fp32-accurate to ~2^-21
- * relative: each operand is scaled by a power of two per token and split into
- * f16 hi + lo; the B operand is the format's integer), other formats the fp32
+ * Q6_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S (these four with rows of a multiple of
+ * 512 columns), IQ4_NL and IQ4_XS use the split-precision f16 MFMA GEMM
+ * (fp32-accurate to ~2^-21 relative: each operand is scaled by a power of two
+ * per token and split into f16 hi + lo; the B operand is the format's integer,
+ * for Q6_K an f16-rounded part and its exact remainder), other formats the fp32
  * MFMA GEMM. x may take any finite values. The activations are scaled by
  * 2^(2 e_t - 15) (e_t the exponent that brings the token's max |x| into
  * [2^10, 2^11)); when a row's max |act| so scaled leaves [2^-3, 2^14) (weights
