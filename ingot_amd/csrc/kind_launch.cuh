@@ -48,9 +48,16 @@ bool launch_gemm_k(hipStream_t s, dim3 grid, const GemmArgs& a) {
 template <int KIND, int NE>
 static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw, dim3 grid,
                             const DecGateUpArgs& a) {
-#define DGU(C, N, R)                                                                                          \
-    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F, \
-                       a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags, a.act)
+    // routing precomputed by k_route (a.pre): the instantiation that reads it, above 128 experts only
+#define DGU_(C, N, R, P)                                                                                         \
+    hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE, -1, P>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,  \
+                       a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, \
+                       a.flags, a.act)
+#define DGU(C, N, R)                     \
+    do {                                 \
+        if (NE > 2 && a.pre) DGU_(C, N, R, (NE > 2)); \
+        else DGU_(C, N, R, false);       \
+    } while (0)
     if (rpw == 3) {
         if (cpl == 1 && np == 1) { DGU(1, 1, 3); return true; }
         return false;
@@ -60,6 +67,7 @@ static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t r
     if (cpl == 2 && np == 1) { DGU(2, 1, 2); return true; }
     if (cpl == 2 && np == 2) { DGU(2, 2, 2); return true; }
 #undef DGU
+#undef DGU_
     return false;
 }
 
@@ -71,9 +79,14 @@ bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw
     if (a.E <= 128) return dec_gate_up_cpl<KIND, 2>(s, cpl, np, rpw, grid, a);
     if constexpr (KIND == 17)
         if (a.E <= 512 && cpl == 1 && np == 2 && rpw == 2) {
-            hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F,
-                               a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags,
-                               a.act);
+            if (a.pre)
+                hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, -1, true>), grid, dim3(512), 0, s, a.g, a.u, a.gs,
+                                   a.us, a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit,
+                                   a.ids, a.w, a.flags, a.act);
+            else
+                hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,
+                                   a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids,
+                                   a.w, a.flags, a.act);
             return true;
         }
     return dec_gate_up_cpl<KIND, 16>(s, cpl, np, rpw, grid, a);
@@ -85,9 +98,14 @@ bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32
                                 uint64_t sus, float* sact) {
     // the configs[2] shape: 512 experts, one chunk per lane, two pairs per wave, 2 rows
     if (a.E > 512 || a.E <= 128 || cpl != 1 || np != 2 || rpw != 2) return false;
-    hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F, a.H,
-                       a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags, a.act,
-                       sg, su, sgs, sus, sact);
+    if (a.pre)
+        hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS, true>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,
+                           a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w,
+                           a.flags, a.act, sg, su, sgs, sus, sact);
+    else
+        hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F,
+                           a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags,
+                           a.act, sg, su, sgs, sus, sact);
     return true;
 }
 

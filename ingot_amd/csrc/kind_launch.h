@@ -50,6 +50,7 @@ struct DecGateUpArgs {
     float* w;
     uint32_t* flags;
     float* act;
+    uint32_t pre;  // 1: ids and w hold the routing (k_route ran), inputs of the kernel
 };
 
 struct DownArgs {

@@ -401,11 +401,13 @@ static uint32_t dec_gate_up_rows(uint32_t F, uint32_t T, uint32_t cpl, uint32_t 
 static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const uint8_t* u, uint64_t gs,
                                uint64_t us, uint32_t F, uint32_t H, uint32_t T, const float* x, const float* xstat,
                                const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode,
-                               float scale, float limit, uint32_t* ids, float* w, uint32_t* flags, float* act) {
+                               float scale, float limit, uint32_t* ids, float* w, uint32_t* flags, float* act,
+                               uint32_t pre) {
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     dim3 grid((F + rpw - 1) / rpw, T);
-    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act};
+    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act,
+                          pre};
     switch (kind) {
 #define K_(KV) case KV: return launch_dec_gate_up_k<KV>(s, cpl, np, rpw, grid, a);
         INGOT_KINDS(K_)
@@ -422,12 +424,13 @@ static bool launch_dec_gate_up_fused(hipStream_t s, uint32_t kind, uint32_t skin
                                      uint64_t sgs, uint64_t sus, uint32_t F, uint32_t H, uint32_t T, const float* x,
                                      const float* xstat, const float* logits, const float* bias, uint32_t E,
                                      uint32_t K, uint32_t mode, float scale, float limit, uint32_t* ids, float* w,
-                                     uint32_t* flags, float* act, float* sact) {
+                                     uint32_t* flags, float* act, float* sact, uint32_t pre) {
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
     if (K >= GU_WAVES * np) return false;  // no free pair slot
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     const dim3 grid((F + rpw - 1) / rpw, T);
-    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act};
+    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act,
+                          pre};
 #define FG_(KG, KS)                                                                                              \
     if (kind == KG && skind == KS) return launch_dec_gate_up_fused_k<KG, KS>(s, cpl, np, rpw, grid, a, sg, su, sgs, \
                                                                              sus, sact);
@@ -1230,8 +1233,12 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         };
         L->stage_name[ST_ROUTER] = "k_router";
     }
-    // 2. route (prefill)
-    if (!decode) {
+    // 2. route (prefill; decode batches of several tokens over more than 128
+    //    experts, whose gate/up blocks then read the routing instead of each
+    //    repeating its token's: the search over 512 experts costs more than
+    //    the extra launch, over 128 it does not)
+    const bool pre_route = decode && T >= 2 && E > 128;
+    if (!decode || pre_route) {
         const float *lg = w.logits, *b = L->bias;
         uint32_t* ids = w.ids;
         float* wt = w.wts;
@@ -1258,10 +1265,10 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
             if (hs && SF == F && sgate.kind == sup.kind &&
                 launch_dec_gate_up_fused(ss, gate.kind, sgate.kind, gate.d, up.d, gate.stride, up.stride, sgate.d,
                                          sup.d, sgate.stride, sup.stride, F, H, T, xin, xstat, lg, b, E, K, mode,
-                                         scale, limit, ids, wts, flags, act, sact))
+                                         scale, limit, ids, wts, flags, act, sact, pre_route ? 1u : 0u))
                 return;
             launch_dec_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, T, xin, xstat, lg, b, E, K,
-                               mode, scale, limit, ids, wts, flags, act);
+                               mode, scale, limit, ids, wts, flags, act, pre_route ? 1u : 0u);
             if (hs)
                 launch_gemv_gate_up(ss, sgate.kind, sgate.d, sup.d, sgate.stride, sup.stride, SF, H, T, xin, nullptr, 1,
                                     limit, sact);

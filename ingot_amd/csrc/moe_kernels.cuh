@@ -826,9 +826,11 @@ __device__ __forceinline__ void load_xh_ilv(const float4* __restrict__ s, uint32
 // free (K < 8 NP), writing sact[t][r] = SwiGLU (its gate is applied by the
 // down kernel); its input is staged a second time when its format takes the
 // other input form.
+//   PRE: the routing is an input (k_route ran: ids and wts hold every pair's
+// expert and weight); the blocks skip the selection.
 constexpr uint32_t GU_WAVES = 8;
 
-template <int KIND, int CPL, int RPW, int NP, int NE, int KS = -1>
+template <int KIND, int CPL, int RPW, int NP, int NE, int KS = -1, bool PRE = false>
 __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
                                                       uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
                                                       const float* __restrict__ x, const float* __restrict__ xstat,
@@ -876,8 +878,16 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     __shared__ float s_sv[64];  // weight input of each selection
     uint32_t eid[NP];
     float ev[NP];
-    bool bad;
-    if constexpr (NP == 1) {
+    bool bad = false;
+    if constexpr (PRE) {
+        // routing done by k_route (batches of several tokens): ids and weights are inputs
+#pragma unroll
+        for (int n = 0; n < NP; ++n) {
+            const uint32_t k = wave + GU_WAVES * n;
+            eid[n] = min(ids[(uint64_t)t * K + (k < K ? k : 0u)], E - 1u);
+            ev[n] = 0.f;
+        }
+    } else if constexpr (NP == 1) {
         uint32_t key[NE];
         float wv[NE];
         bool ok[NE];
@@ -936,7 +946,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
         const uint32_t k = wave + GU_WAVES * n;
-        if (k < K && lane == 0) {
+        if (!PRE && k < K && lane == 0) {
             s_sv[k] = ev[n];
             if (blockIdx.x == 0) ids[(uint64_t)t * K + k] = eid[n];
         }
@@ -950,8 +960,9 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         }
     __syncthreads();
     // Routing weights in selection order; block 0's wave 0 publishes them.
-    const float w = wave_route_weight(lane < K ? s_sv[lane] : 0.f, K, sigmoid_mode, scale);
-    if (blockIdx.x == 0 && wave == 0) {
+    const float w = PRE ? (lane < K ? wts[(uint64_t)t * K + lane] : 0.f)
+                        : wave_route_weight(lane < K ? s_sv[lane] : 0.f, K, sigmoid_mode, scale);
+    if (!PRE && blockIdx.x == 0 && wave == 0) {
         if (flags && __any(bad) && lane == 0) atomicOr(flags, FLAG_NONFINITE);
         if (lane < K) wts[(uint64_t)t * K + lane] = w;
     }
