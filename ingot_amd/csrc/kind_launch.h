@@ -18,10 +18,11 @@
     X(0) X(1) X(2) X(8) X(10) X(12) X(13) X(14) X(16) X(17) X(18) X(20) X(21) X(22) X(23) X(29) X(30) X(42)
 
 // Routed down + shared down fused in one decode kernel: (down kind, shared down kind).
-#define INGOT_FUSED_DOWN(X) X(17, 8) X(12, 12) X(20, 20) X(8, 8)
+#define INGOT_FUSED_DOWN(X) X(17, 8) X(12, 12) X(20, 20) X(8, 8) X(21, 42)
 // (routed gate/up kind, shared gate/up kind) pairs whose shared expert runs in
-// the routed decode gate/up kernel's free pair slot.
-#define INGOT_FUSED_GATE_UP(X) X(17, 8)
+// the routed decode gate/up kernel's free pair slot (configs[2]; the IQ2_S /
+// IQ4_XS shared mix of an IQ2_XS-class checkpoint).
+#define INGOT_FUSED_GATE_UP(X) X(17, 8) X(22, 23)
 
 namespace ingot {
 

@@ -4,3 +4,4 @@
 INGOT_INSTANTIATE_KIND(18)
 INGOT_INSTANTIATE_KIND(21)
 INGOT_INSTANTIATE_KIND(29)
+INGOT_INSTANTIATE_FUSED(21, 42)

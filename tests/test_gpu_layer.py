@@ -57,6 +57,19 @@ def test_c2_decode_full(gpu, oracle):
     layer.destroy()
 
 
+def test_iq2s_iq3s_mix_decode_512_experts(gpu, oracle):
+    """An IQ2_XS-class checkpoint's mix at configs[2]'s shape: IQ2_S gate/up and IQ3_S down
+    over 512 experts (top-10), a gated shared expert with IQ4_XS gate/up and Q2_0 down of the
+    routed width (it joins the routed decode kernels), at 1 and 4 tokens."""
+    from ingot_amd.moe import IQ2_S, IQ3_S, IQ4_XS, Q2_0
+    spec = CF.make_layer(2, 0, 2048, 512, 10, 512, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
+                         shared_down_kind=Q2_0, shared_gated=True)
+    layer = MoeLayer(gpu, spec)
+    for T in (1, 4):
+        check_layer(layer, spec, CF.inputs(2, T, 2048, seed=T), oracle, f"IQ2_S/IQ3_S mix b={T}")
+    layer.destroy()
+
+
 def test_c3_prefill_full(gpu, oracle):
     spec = CF.c3_layer()
     layer = MoeLayer(gpu, spec)
