@@ -162,6 +162,12 @@ __device__ inline uint32_t* lds_iq3xxs_grid() {
     __shared__ uint32_t g[256];
     return g;
 }
+// The same grid for the f16 GEMM with each entry's 4 bytes spread into two
+// u16 pairs ({b0, b1}, {b2, b3}): the operand build multiplies them as they are.
+__device__ inline uint2* lds_iq3xxs_grid_u16() {
+    __shared__ uint2 g[256];
+    return g;
+}
 __device__ inline float* lds_iq4nl_values() {
     __shared__ float v[16];
     return v;
@@ -251,7 +257,11 @@ __device__ inline void stage_f16_tables() {
             lds_iq3_signmask()[i] = make_uint4(w[0], w[1], w[2], w[3]);
         }
     } else if constexpr (KIND == 18) {
-        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) lds_iq3xxs_grid()[i] = ingot_iq3xxs_grid[i];
+        for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) {
+            const uint32_t e = ingot_iq3xxs_grid[i];
+            lds_iq3xxs_grid_u16()[i] =
+                make_uint2((e & 0xffu) | ((e << 8) & 0xff0000u), ((e >> 16) & 0xffu) | ((e >> 8) & 0xff0000u));
+        }
         for (uint32_t i = threadIdx.x; i < 128u; i += blockDim.x) {
             const uint32_t s = ingot_ksign(i);
             uint32_t w[4];

@@ -2346,11 +2346,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
                 for (int gi = 0; gi < 2; ++gi) {
                     const uint4 m = lds_iq3_signmask()[(x >> (14u * (sq & 1u) + 7u * gi)) & 127u];
-                    const uint32_t e0 = lds_iq3xxs_grid()[(g >> (16 * gi)) & 255u];
-                    const uint32_t e1 = lds_iq3xxs_grid()[(g >> (16 * gi + 8)) & 255u];
+                    const uint2 e0 = lds_iq3xxs_grid_u16()[(g >> (16 * gi)) & 255u];
+                    const uint2 e1 = lds_iq3xxs_grid_u16()[(g >> (16 * gi + 8)) & 255u];
                     fb[nb][gi] = __builtin_bit_cast(
-                        half8, make_uint4(mad_u16x2(bytes01(e0), f2, m.x), mad_u16x2(bytes23(e0), f2, m.y),
-                                          mad_u16x2(bytes01(e1), f2, m.z), mad_u16x2(bytes23(e1), f2, m.w)));
+                        half8, make_uint4(mad_u16x2(e0.x, f2, m.x), mad_u16x2(e0.y, f2, m.y),
+                                          mad_u16x2(e1.x, f2, m.z), mad_u16x2(e1.y, f2, m.w)));
                 }
             } else {
                 uint32_t qa, qb;
