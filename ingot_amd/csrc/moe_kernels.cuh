@@ -2522,7 +2522,17 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                                     }
                                 }
                             }
-                    {
+                    if constexpr (IQG && MBE <= 2) {
+                        // IQ tiles of 1-2 row blocks: the slab's codebook and A reads
+                        // (about 6 per A fragment) all first, then the MFMAs with the
+                        // decode's VALU between them (C3 gate/up 270.5 to 265.8 us).
+                        __builtin_amdgcn_sched_group_barrier(0x100, 64, 0);
+#pragma unroll
+                        for (int f = 0; f < 4 * MBE; ++f) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+                        }
+                    } else {
                         // Issue order within the slab: PF A-fragment reads ahead, then
                         // per fragment its NB MFMAs, the read PF fragments on and (with
                         // two operand sets) a share of the next slab's B decode (VALU),
