@@ -28,6 +28,7 @@ struct ingot_ctx {
     std::string name;
     uint32_t* d_flags = nullptr;
     void* scratch = nullptr;  // this device's copy of `scratch` (hipGetSymbolAddress)
+    hipStream_t copy = nullptr;  // cached layers' expert copies (created with the first one)
 };
 
 // Workspace of the allocation-free forward (ingot_layer_forward_static): one
@@ -690,6 +691,10 @@ void ingot_ctx_destroy(ingot_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->copy) {
+        (void)hipStreamSynchronize(ctx->copy);
+        (void)hipStreamDestroy(ctx->copy);
+    }
     if (ctx->d_flags) (void)hipFree(ctx->d_flags);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
@@ -1161,8 +1166,32 @@ static int cached_expert_passes(ingot_layer* L, const Ws& w, uint32_t T) {
     const uint8_t* host[3] = {L->hgate, L->hup, L->hdown};
     std::vector<std::vector<uint32_t>> tables;  // kept until the stream drains
     ExpertCache& c = *L->cache;
+    // Copies run on their own stream, so that a pass's misses load while the
+    // previous pass computes: a copy into a slot that an earlier pass of this
+    // forward read first waits for that pass's done event, and each pass's
+    // products wait for its copies. The cache decisions (claims, commits,
+    // counters) are made on the host in the same order as without overlap.
+    if (!ctx->copy) HIP_TRY(ctx, hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking));
+    hipStream_t cst = ctx->copy;
+    struct Events {
+        std::vector<hipEvent_t> v;
+        ~Events() {
+            for (hipEvent_t e : v) (void)hipEventDestroy(e);
+        }
+    } evs;
+    auto record = [&](hipStream_t st, hipEvent_t* e) -> hipError_t {
+        hipError_t r = hipEventCreateWithFlags(e, hipEventDisableTiming);
+        if (r != hipSuccess) return r;
+        evs.v.push_back(*e);
+        return hipEventRecord(*e, st);
+    };
+    std::vector<int> slot_pass(c.slots(), -1);  // last pass of this forward that read the slot
+    std::vector<hipEvent_t> done;                // per pass: its down kernel has run
+    int waited = -1;                             // cst already waits for the passes up to this one
     size_t i = 0;
     for (bool first = true; first || i < order.size(); first = false) {
+        const int k = (int)done.size();
+        bool copied = false;
         std::vector<uint32_t> pinned;
         tables.emplace_back(E + 1, NO_SLOT);
         std::vector<uint32_t>& slot_of = tables.back();
@@ -1172,23 +1201,38 @@ static int cached_expert_passes(ingot_layer* L, const Ws& w, uint32_t T) {
             const int slot = c.claim(e, pinned.data(), (uint32_t)pinned.size(), &load);
             if (slot < 0) return fail(ctx, INGOT_INVALID, "no reusable expert slot");
             if (load) {
+                const int prev = slot_pass[slot];
+                if (prev > waited) {
+                    HIP_TRY(ctx, hipStreamWaitEvent(cst, done[prev], 0));
+                    waited = prev;
+                }
                 for (int m = 0; m < 3; ++m) {
                     const uint64_t bytes = dev[m]->rows * dev[m]->stride;
                     HIP_TRY(ctx, hipMemcpyAsync(dev[m]->d + (uint64_t)slot * bytes, host[m] + (uint64_t)e * bytes, bytes,
-                                                hipMemcpyHostToDevice, s));
+                                                hipMemcpyHostToDevice, cst));
                     c.bytes += bytes;
                 }
                 c.commit((uint32_t)slot, e);
+                copied = true;
             }
+            slot_pass[slot] = k;
             slot_of[e] = (uint32_t)slot;
             pinned.push_back((uint32_t)slot);
             ++i;
+        }
+        if (copied) {
+            hipEvent_t ev;
+            HIP_TRY(ctx, record(cst, &ev));
+            HIP_TRY(ctx, hipStreamWaitEvent(s, ev, 0));
         }
         slot_of[E] = first ? 0u : NO_SLOT;
         HIP_TRY(ctx, hipMemcpyAsync(w.slot_of, slot_of.data(), 4ull * (E + 1), hipMemcpyHostToDevice, s));
         L->pass = {w.slot_of, first};
         L->stage[ST_GATEUP](s);
         L->stage[ST_DOWN](s);
+        hipEvent_t d;
+        HIP_TRY(ctx, record(s, &d));
+        done.push_back(d);
     }
     L->pass = {};
     L->stage[ST_COMBINE](s);
