@@ -157,7 +157,9 @@ int ingot_route_batch(ingot_ctx* ctx, const float* d_logits, const float* d_bias
                       uint32_t K, uint32_t routing, float scale, uint32_t* d_ids, float* d_weights);
 /* Synchronizes, reads and clears the device flags; INGOT_NONFINITE if a
  * kernel met a non-finite router logit since the last check, else INGOT_RANGE
- * if a prefill forward's activations left the split-f16 range. */
+ * if a prefill forward's activations left the split-f16 range, else
+ * INGOT_NONFINITE if a layer forward wrote a non-finite output value (the
+ * device-side form of the reference's read-back check, src/metal.rs:1575-1577). */
 int ingot_ctx_check_device_flags(ingot_ctx* ctx);
 
 /* ---- resident layer ---- */
@@ -224,7 +226,9 @@ void ingot_layer_destroy(ingot_layer* layer);
  * before graph capture, which must not allocate). */
 int ingot_layer_reserve(ingot_layer* layer, uint32_t T);
 /* out[T][H] = layer(x[T][H]); device pointers, asynchronous on the context
- * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL. */
+ * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL.
+ * A non-finite router logit or output value sets the context's device flags
+ * (ingot_ctx_check_device_flags). */
 int ingot_layer_forward(ingot_layer* layer, const float* d_x, uint32_t T, float* d_out, uint32_t* d_ids,
                         float* d_weights);
 /* No counterpart in the reference: the same forward as ingot_layer_forward for

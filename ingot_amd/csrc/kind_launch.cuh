@@ -26,13 +26,15 @@ bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t rpw, dim3 grid,
 
 template <int KS>
 bool launch_shared_add_k(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H,
-                         uint32_t SF, const float* sact, const float* sgl, float* out) {
+                         uint32_t SF, const float* sact, const float* sgl, float* out, uint32_t* flags) {
     if (cpl == 1) {
-        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 1>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
+        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 1>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out,
+                           flags);
         return true;
     }
     if (cpl == 2) {
-        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 2>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out);
+        hipLaunchKernelGGL((k_gemv_shared_down_add<KS, 2>), grid, dim3(256), 0, s, sd, sds, H, SF, sact, sgl, out,
+                           flags);
         return true;
     }
     return false;
@@ -114,7 +116,8 @@ bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a
 #define DD(V)                                                                                                      \
     case V:                                                                                                        \
         hipLaunchKernelGGL((k_dec_down<KD, KS, V, DEC_RPW>), grid, dim3(DOWN_THREADS), 0, s, a.down, a.dstride,    \
-                           a.sdown, a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.sgl, a.K, a.res, a.out);   \
+                           a.sdown, a.sdstride, a.H, a.F, a.SF, a.act, a.sact, a.ids, a.sgl, a.K, a.res, a.out,    \
+                           a.flags);                                                                       \
         return true;
     switch (vpl) {
         DD(1) DD(2) DD(3) DD(4) DD(5) DD(6)  // K F + SF <= DOWN_LDS_FLOATS: at most 384 chunks
@@ -129,7 +132,7 @@ bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a
     namespace ingot {                                                                                            \
     template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, dim3, const GateUpArgs&);            \
     template bool launch_shared_add_k<K>(hipStream_t, uint32_t, dim3, const uint8_t*, uint64_t, uint32_t,        \
-                                         uint32_t, const float*, const float*, float*);                          \
+                                         uint32_t, const float*, const float*, float*, uint32_t*);               \
     template bool launch_gemm_k<K, true>(hipStream_t, dim3, const GemmArgs&);                                    \
     template bool launch_gemm_k<K, false>(hipStream_t, dim3, const GemmArgs&);                                   \
     template bool launch_dec_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, uint32_t, dim3, const DecGateUpArgs&); \

@@ -64,6 +64,7 @@ struct DownArgs {
     uint32_t K;
     const float* res;
     float* out;
+    uint32_t* flags;  // FLAG_OUT_NONFINITE
 };
 
 struct GemmArgs {
@@ -87,7 +88,7 @@ bool launch_gemv_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t rpw, dim3 grid,
 // k_gemv_shared_down_add: out[t] += sigmoid gate * D_s sact[t].
 template <int KS>
 bool launch_shared_add_k(hipStream_t s, uint32_t cpl, dim3 grid, const uint8_t* sd, uint64_t sds, uint32_t H,
-                         uint32_t SF, const float* sact, const float* sgl, float* out);
+                         uint32_t SF, const float* sact, const float* sgl, float* out, uint32_t* flags);
 // k_gemm<KIND, GATEUP>: fp32-MFMA grouped GEMM over dispatch tiles.
 template <int KIND, bool GATEUP>
 bool launch_gemm_k(hipStream_t s, dim3 grid, const GemmArgs& a);
@@ -107,7 +108,8 @@ bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32
 #define INGOT_DECLARE_KIND(K)                                                                               \
     extern template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, dim3, const GateUpArgs&); \
     extern template bool launch_shared_add_k<K>(hipStream_t, uint32_t, dim3, const uint8_t*, uint64_t,      \
-                                                uint32_t, uint32_t, const float*, const float*, float*);    \
+                                                uint32_t, uint32_t, const float*, const float*, float*,     \
+                                                uint32_t*);                                                 \
     extern template bool launch_gemm_k<K, true>(hipStream_t, dim3, const GemmArgs&);                        \
     extern template bool launch_gemm_k<K, false>(hipStream_t, dim3, const GemmArgs&);                       \
     extern template bool launch_dec_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, uint32_t, dim3,           \

@@ -276,11 +276,11 @@ bool launch_gemv_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, const u
 }
 
 bool launch_shared_down_add(hipStream_t s, uint32_t ks, const uint8_t* sd, uint64_t sds, uint32_t H, uint32_t SF,
-                            uint32_t T, const float* sact, const float* sgl, float* out) {
+                            uint32_t T, const float* sact, const float* sgl, float* out, uint32_t* flags) {
     const uint32_t cpl = (SF / 32 + 63) / 64;
     dim3 grid((H + 3) / 4, T);
     switch (ks) {
-#define K_(KV) case KV: return launch_shared_add_k<KV>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out);
+#define K_(KV) case KV: return launch_shared_add_k<KV>(s, cpl, grid, sd, sds, H, SF, sact, sgl, out, flags);
         INGOT_KINDS(K_)
 #undef K_
         default: return false;
@@ -727,6 +727,7 @@ int ingot_ctx_check_device_flags(ingot_ctx* ctx) {
     if (flags & FLAG_RANGE)
         return fail(ctx, INGOT_RANGE,
                     "prefill activations outside the range of the split-f16 GEMM: re-run with INGOT_GEMM_FP32");
+    if (flags & FLAG_OUT_NONFINITE) return fail(ctx, INGOT_NONFINITE, "layer output contains non-finite values");
     return INGOT_OK;
 }
 
@@ -1318,7 +1319,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
                                     limit, sact);
         };
         L->stage_name[ST_GATEUP] = "k_dec_gate_up2";
-        DownArgs a{down.d, sdown.d, down.stride, sdown.stride, H, F, SF, act, sact, ids, sgl, K, res, d_out};
+        DownArgs a{down.d, sdown.d, down.stride, sdown.stride, H, F, SF, act, sact, ids, sgl, K, res, d_out, flags};
         if (!hs || fuse_shared) {
             const int ks = hs ? ks_ : -1;
             L->stage[ST_DOWN] = [=](hipStream_t ss) { gemv_down(ss, down.kind, ks, a, T); };
@@ -1327,7 +1328,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
             ar.sdown = nullptr;
             L->stage[ST_DOWN] = [=](hipStream_t ss) {
                 gemv_down(ss, down.kind, -1, ar, T);
-                launch_shared_down_add(ss, sdown.kind, sdown.d, sdown.stride, H, SF, T, sact, sgl, d_out);
+                launch_shared_down_add(ss, sdown.kind, sdown.d, sdown.stride, H, SF, T, sact, sgl, d_out, flags);
             };
         }
         L->stage_name[ST_DOWN] = "k_dec_down";
@@ -1426,7 +1427,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         const uint32_t shared_scaled = merge ? 1u : 0u;
         L->stage[ST_COMBINE] = [=](hipStream_t ss) {
             hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, ss, Y, hs ? Ys : nullptr,
-                               inverse, wts, sgl, res, T, H, K, d_out, yscale, shared_scaled);
+                               inverse, wts, sgl, res, T, H, K, d_out, yscale, shared_scaled, flags);
         };
         L->stage_name[ST_COMBINE] = "k_combine";
     }

@@ -29,11 +29,15 @@
 namespace ingot {
 
 constexpr int WAVE = 64;
-constexpr uint32_t FLAG_NONFINITE = 1u;
+constexpr uint32_t FLAG_NONFINITE = 1u;  // a router logit or bias
 // An operand of the split-f16 arithmetic left the range in which it is exact
 // (see ACT_EXP_C); the outputs of the forwards since the last check are not
 // valid, and the fp32 GEMM must be used for these inputs.
 constexpr uint32_t FLAG_RANGE = 2u;
+// A kernel that writes a layer output (k_dec_down, k_gemv_shared_down_add,
+// k_combine) wrote a non-finite value; the reference rejects such an output
+// on read-back (src/metal.rs:1575-1577).
+constexpr uint32_t FLAG_OUT_NONFINITE = 4u;
 
 // ------------------------------------------- f16-split operand scaling
 // Every operand that is split into f16 hi + lo (x for the f16 GEMM and the
@@ -1095,7 +1099,8 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
                                                            const float* __restrict__ act, const float* __restrict__ sact,
                                                            const uint32_t* __restrict__ ids,
                                                            const float* __restrict__ sgl, uint32_t K,
-                                                           const float* __restrict__ res, float* __restrict__ out) {
+                                                           const float* __restrict__ res, float* __restrict__ out,
+                                                           uint32_t* __restrict__ flags) {
     using Fd = Fmt<KD>;
     using Fs = Fmt<(KS < 0 ? KD : KS)>;
     constexpr bool HD = half_x<KD>(), HS = KS >= 0 && half_x<(KS < 0 ? KD : KS)>();  // f16-pair inputs
@@ -1257,6 +1262,7 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
         if (lane == (uint32_t)i && r < H) {
             if (res) sum += resv;
             out[(uint64_t)t * H + r] = sum;
+            if (!isfinite(sum)) atomicOr(flags, FLAG_OUT_NONFINITE);
         }
     }
 }
@@ -1327,7 +1333,8 @@ __global__ __launch_bounds__(256) void k_gemv_gate_up(const uint8_t* __restrict_
 template <int KS, int CPL>
 __global__ __launch_bounds__(256) void k_gemv_shared_down_add(const uint8_t* __restrict__ sdown, uint64_t sdstride,
                                                               uint32_t H, uint32_t SF, const float* __restrict__ sact,
-                                                              const float* __restrict__ sgl, float* __restrict__ out) {
+                                                              const float* __restrict__ sgl, float* __restrict__ out,
+                                                              uint32_t* __restrict__ flags) {
     using Fs = Fmt<KS>;
     if constexpr (has_codebook<KS>()) {
         stage_codebooks<KS>();
@@ -1355,7 +1362,11 @@ __global__ __launch_bounds__(256) void k_gemv_shared_down_add(const uint8_t* __r
         acc += Fs::dot(sdown + (uint64_t)r * sdstride, c, xv, s0, s1);
     }
     acc = wave_sum(acc);
-    if (lane == 0) out[(uint64_t)t * H + r] += acc;
+    if (lane == 0) {
+        const float o = out[(uint64_t)t * H + r] + acc;
+        out[(uint64_t)t * H + r] = o;
+        if (!isfinite(o)) atomicOr(flags, FLAG_OUT_NONFINITE);
+    }
 }
 
 // ------------------------------------------------------- prefill: dispatch
@@ -2813,7 +2824,8 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
                                                  const uint32_t* __restrict__ inverse, const float* __restrict__ wts,
                                                  const float* __restrict__ sgl, const float* __restrict__ res,
                                                  uint32_t T, uint32_t H, uint32_t K, float* __restrict__ out,
-                                                 const float* __restrict__ xstat, uint32_t shared_scaled) {
+                                                 const float* __restrict__ xstat, uint32_t shared_scaled,
+                                                 uint32_t* __restrict__ flags) {
     // grid (ceil(H / 1024), T): the token is uniform in the block, so its
     // packed positions and weights are scalar loads.
     const uint32_t t = blockIdx.y, c = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
@@ -2838,6 +2850,7 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
         s.x += r.x; s.y += r.y; s.z += r.z; s.w += r.w;
     }
     *reinterpret_cast<float4*>(out + (uint64_t)t * H + c) = s;
+    if (!(isfinite(s.x) && isfinite(s.y) && isfinite(s.z) && isfinite(s.w))) atomicOr(flags, FLAG_OUT_NONFINITE);
 }
 
 // ---------------------------------------------- generic (drop-in) kernels
@@ -2881,13 +2894,6 @@ __global__ void k_combine_host(const float* __restrict__ routed, const float* __
     for (uint32_t e = 0; e < K; ++e) s += routed[(uint64_t)e * H + i] * w[e];
     if (shared) s += shared[i] / (1.0f + expf(-slogit[0]));
     out[i] = s;
-}
-
-// Non-finite scan of a device buffer: sets FLAG_NONFINITE in flags.
-__global__ void k_check_finite(const float* __restrict__ v, uint64_t n, uint32_t* __restrict__ flags) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    bool bad = i < n && !isfinite(v[i]);
-    if (__any(bad) && (threadIdx.x & 63u) == 0) atomicOr(flags, FLAG_NONFINITE);
 }
 
 #endif  // INGOT_KIND_UNIT

@@ -555,6 +555,9 @@ int forward(const oracle_layer* L, const float* x, uint32_t T, float* out, uint3
         }
     if (ids_out) std::memcpy(ids_out, ids.data(), sizeof(uint32_t) * P);
     if (w_out) std::memcpy(w_out, w.data(), sizeof(float) * P);
+    // The reference rejects a non-finite output on read-back (src/metal.rs:1575-1577).
+    for (uint64_t i = 0; i < (uint64_t)T * H; ++i)
+        if (!std::isfinite(out[i])) return ORACLE_NONFINITE;
     return ORACLE_OK;
 }
 

@@ -76,7 +76,9 @@ void oracle_router_logits(const float* W, const float* x, uint32_t T, uint32_t E
 /* y[r] = sum_j W[r][j] x[j] for a single matrix (count 1), f64 accumulation. */
 int oracle_project(const oracle_matrix* m, const float* x, double* y);
 
-/* Full layer: out[T][H]; ids/w [T][K] (may be NULL). threads <= 0: all cores. */
+/* Full layer: out[T][H]; ids/w [T][K] (may be NULL). threads <= 0: all cores.
+ * ORACLE_NONFINITE for a non-finite input, or (after writing out, ids and w)
+ * for a non-finite output value. */
 int oracle_moe_forward(const oracle_layer* L, const float* x, uint32_t T, float* out,
                        uint32_t* ids, float* w, int precision, int threads);
 

@@ -453,6 +453,39 @@ def test_nonfinite_input_rejected(gpu):
     layer.destroy()
 
 
+@pytest.mark.parametrize("case", ["decode", "decode_fused_shared", "decode_shared_add", "prefill"])
+def test_nonfinite_output_flagged(gpu, oracle, case):
+    """Finite inputs (N(0,1) x 1e25) whose expert products overflow fp32: the
+    oracle rejects the output, and the kernel that writes the layer output
+    (k_dec_down, k_gemv_shared_down_add, k_combine) raises the device flag;
+    a finite forward afterwards raises nothing."""
+    kw = {}
+    if case == "decode_fused_shared":
+        kw = dict(shared_ffn=256, shared_gate_kind=Q4_K, shared_down_kind=Q4_K)
+    elif case == "decode_shared_add":
+        kw = dict(shared_ffn=256, shared_gate_kind=Q8_0, shared_down_kind=Q8_0)
+    spec = small_layer(Q4_K, Q4_K, **kw)
+    T = 64 if case == "prefill" else 1
+    x = CF.inputs(15, T, 2048) * np.float32(1e25)
+    assert np.isfinite(x).all()
+    assert oracle.moe_forward(spec, x, oracle.F64)[0] == oracle.NONFINITE
+    layer = MoeLayer(gpu, spec)
+    if case == "prefill":
+        from ingot_amd.moe import GEMM_FP32
+        layer.set_gemm_mode(GEMM_FP32)  # the split-f16 GEMM would report the range first
+    d = gpu.to_device(x)
+    out = gpu.buffer(4 * T * 2048)
+    layer.forward(d, T, out)
+    with pytest.raises(NonFinite, match="output"):
+        gpu.check_device_flags()
+    gpu.check_device_flags()  # cleared
+    layer.forward(gpu.to_device(CF.inputs(15, T, 2048)), T, out)
+    gpu.check_device_flags()
+    with pytest.raises(NonFinite):
+        layer(x)
+    layer.destroy()
+
+
 def test_layer_rejects_bad_shapes(gpu):
     spec = small_layer(Q4_K, Q4_K)
     bad = LayerSpec(**{**spec.__dict__})

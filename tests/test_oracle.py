@@ -451,6 +451,15 @@ def test_layer_errors(oracle):
     bad = LayerSpec(**{**spec.__dict__})
     bad.top_k = 5
     assert oracle.moe_forward(bad, CF.inputs(94, 1, 512), oracle.F64)[0] == oracle.INVALID
+    # a finite input whose expert products overflow fp32: the output is rejected
+    # (src/metal.rs:1575-1577); the routing, invariant under a positive scale, is still written
+    x = CF.inputs(94, 2, 512)
+    st, _, ids, _ = oracle.moe_forward(spec, x, oracle.F64)
+    assert st == oracle.OK
+    for prec in (oracle.F64, oracle.F32):
+        st, out, ids2, _ = oracle.moe_forward(spec, x * np.float32(1e25), prec)
+        assert st == oracle.NONFINITE and not np.isfinite(out).all()
+        assert np.array_equal(ids, ids2)
 
 
 def test_rmsnorm_residual_equation(oracle):
