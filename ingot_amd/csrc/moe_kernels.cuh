@@ -2827,26 +2827,57 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
                                                  const float* __restrict__ xstat, uint32_t shared_scaled,
                                                  uint32_t* __restrict__ flags) {
     // grid (ceil(H / 1024), T): the token is uniform in the block, so its
-    // packed positions and weights are scalar loads.
+    // packed positions and weights are scalar loads. The shared row and the
+    // residual are loaded first, then the routed rows in batches of CB whose
+    // loads are all issued before the first is used (one memory round trip per
+    // batch instead of one per pair; the K % CB left over one at a time); the
+    // sum keeps the route order.
+    constexpr uint32_t CB = 8;
     const uint32_t t = blockIdx.y, c = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
     if (c >= H) return;
     const int ue = xstat ? -act_exp(ld_xstat(xstat, t)) : 0;
+    float4 ys = make_float4(0.f, 0.f, 0.f, 0.f), r = ys;
+    if (Ys) ys = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
+    if (res) r = *reinterpret_cast<const float4*>(res + (uint64_t)t * H + c);
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t k = 0; k < K; ++k) {
-        const uint32_t p = t * K + k;
-        const float w = wts[p];
-        const float4 y = *reinterpret_cast<const float4*>(Y + (uint64_t)inverse[p] * H + c);
-        s.x += w * y.x; s.y += w * y.y; s.z += w * y.z; s.w += w * y.w;
+    uint32_t k = 0;
+    for (; k + CB <= K; k += CB) {
+        float w[CB];
+        uint32_t iv[CB];
+        float4 y[CB];
+#pragma unroll
+        for (uint32_t u = 0; u < CB; ++u) {
+            w[u] = wts[t * K + k + u];
+            iv[u] = inverse[t * K + k + u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < CB; ++u) y[u] = *reinterpret_cast<const float4*>(Y + (uint64_t)iv[u] * H + c);
+#pragma unroll
+        for (uint32_t u = 0; u < CB; ++u) {
+            s.x = __builtin_fmaf(w[u], y[u].x, s.x);
+            s.y = __builtin_fmaf(w[u], y[u].y, s.y);
+            s.z = __builtin_fmaf(w[u], y[u].z, s.z);
+            s.w = __builtin_fmaf(w[u], y[u].w, s.w);
+        }
+    }
+    for (; k < K; ++k) {
+        const float w = wts[t * K + k];
+        const float4 y = *reinterpret_cast<const float4*>(Y + (uint64_t)inverse[t * K + k] * H + c);
+        s.x = __builtin_fmaf(w, y.x, s.x);
+        s.y = __builtin_fmaf(w, y.y, s.y);
+        s.z = __builtin_fmaf(w, y.z, s.z);
+        s.w = __builtin_fmaf(w, y.w, s.w);
     }
     s = ldexp4(s, ue);
     if (Ys) {
         const float w = sgl ? ingot_det_sigmoid(sgl[t]) : 1.0f;
-        float4 y = *reinterpret_cast<const float4*>(Ys + (uint64_t)t * H + c);
-        if (shared_scaled) y = ldexp4(y, ue);
-        s.x += y.x * w; s.y += y.y * w; s.z += y.z * w; s.w += y.w * w;
+        if (shared_scaled) ys = ldexp4(ys, ue);
+        s.x = __builtin_fmaf(ys.x, w, s.x);
+        s.y = __builtin_fmaf(ys.y, w, s.y);
+        s.z = __builtin_fmaf(ys.z, w, s.z);
+        s.w = __builtin_fmaf(ys.w, w, s.w);
     }
     if (res) {
-        const float4 r = *reinterpret_cast<const float4*>(res + (uint64_t)t * H + c);
         s.x += r.x; s.y += r.y; s.z += r.z; s.w += r.w;
     }
     *reinterpret_cast<float4*>(out + (uint64_t)t * H + c) = s;
