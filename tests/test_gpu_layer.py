@@ -39,6 +39,17 @@ def test_c1_prefill_full(gpu, oracle):
     layer.destroy()
 
 
+def test_c1_prefill_4096_tokens(gpu, oracle):
+    """Eight times the C1 batch: 32,768 pairs through one dispatch block, the
+    hot expert (all but one token here) in 32 tiles of up to 128 pairs."""
+    spec = CF.c1_layer()
+    layer = MoeLayer(gpu, spec)
+    x = CF.inputs(1, 4096, 2048, seed=5)
+    out, ids, _ = check_layer(layer, spec, x, oracle, "C1 prefill 4096")
+    assert np.bincount(ids.ravel(), minlength=128).max() > 31 * 128
+    layer.destroy()
+
+
 def test_c1_prefill_fp32_gemm_mode(gpu, oracle):
     """The fp32 MFMA GEMM (the path for non-Q4_K formats) on the C1 layer."""
     from ingot_amd.moe import GEMM_FP32
