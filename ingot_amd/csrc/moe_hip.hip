@@ -134,6 +134,7 @@ int validate(const ingot_matrix* m) {
 
 struct DevMatrix {
     uint8_t* d = nullptr;
+    uint8_t* t = nullptr;  // the same bytes in the f16 GEMM's tiled layout (tiled_kind), or NULL
     uint64_t nbytes = 0, cols = 0, rows = 0, count = 0, stride = 0;
     uint32_t kind = 0;
 };
@@ -180,6 +181,28 @@ int upload_scoped(ingot_ctx* ctx, DevScope& sc, const ingot_matrix* m, DevMatrix
     const int st = upload_matrix(ctx, m, out);
     if (st == INGOT_OK) sc.p.push_back(out->d);
     return st;
+}
+
+// Formats with a tiled layout for the f16 GEMM (k_tile_weights): Q4_K,
+// IQ3_XXS and IQ4_NL, for the column counts the f16 GEMM takes them at, in
+// whole 16-row groups.
+bool tiled_kind(const DevMatrix& m) {
+    const bool cols_ok = (m.kind == 12 && m.cols % 256 == 0) || (m.kind == 18 && m.cols % 512 == 0) ||
+                         (m.kind == 20 && m.cols % 64 == 0);
+    return cols_ok && m.rows % 16 == 0;
+}
+
+// m->t = m->d in the tiled layout (resident layers; the decode kernels and the
+// fp32 GEMM keep reading m->d).
+int make_tiled(ingot_ctx* ctx, DevMatrix* m) {
+    if (!m->d || !tiled_kind(*m)) return INGOT_OK;
+    HIP_TRY(ctx, hipMalloc(reinterpret_cast<void**>(&m->t), m->nbytes));
+    const uint64_t blocks = std::min<uint64_t>((m->nbytes + 255) / 256, 1u << 20);
+    hipLaunchKernelGGL(k_tile_weights, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, m->d, m->t, m->nbytes,
+                       m->kind, m->stride);
+    HIP_TRY(ctx, hipGetLastError());
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return INGOT_OK;
 }
 
 template <typename T>
@@ -330,9 +353,19 @@ bool f16_tt128_kind(uint32_t kind) { return kind == 12 || kind == 13 || kind == 
 
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
 // projection's a_order); tt128: tiles of up to 128 tokens (f16_tt128_kind).
+// tl: the weights are the tiled copies (Q4_K, IQ3_XXS, IQ4_NL).
 template <bool GATEUP, typename... Args>
-bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, dim3 grid, Args... args) {
-#define F16(KV, AO, TT) hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT>), grid, dim3(2 * TT), 0, s, args...)
+bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, bool tl, dim3 grid, Args... args) {
+#define F16(KV, AO, TT)                                                                                      \
+    do {                                                                                                     \
+        if constexpr (KV == 12 || KV == 18 || KV == 20) {                                                    \
+            if (tl) {                                                                                        \
+                hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT, true>), grid, dim3(2 * TT), 0, s, args...); \
+                break;                                                                                       \
+            }                                                                                                \
+        }                                                                                                    \
+        hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT>), grid, dim3(2 * TT), 0, s, args...);             \
+    } while (0)
 #define F16_GU(KV, TT)                                          \
     switch (aord) {                                             \
         case A_IQ4NL: F16(KV, A_IQ4NL, TT); return true;        \
@@ -574,8 +607,10 @@ struct ingot_layer {
 };
 
 static void free_dev(ingot_layer* L) {
-    for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown})
+    for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) {
         if (m->d) (void)hipFree(m->d);
+        if (m->t) (void)hipFree(m->t);
+    }
     for (float* p : {L->router, L->bias, L->sgvec, L->gain})
         if (p) (void)hipFree(p);
     if (L->ws) (void)hipFree(L->ws);
@@ -1005,6 +1040,9 @@ static int create_layer(ingot_ctx* ctx, const ingot_layer_desc* d, uint32_t slot
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_gate, &L->sgate);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_up, &L->sup);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_down, &L->sdown);
+    if (slots == 0)
+        for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown})
+            if (st == INGOT_OK) st = make_tiled(ctx, m);
     if (st != INGOT_OK) {
         free_dev(L);
         delete L;
@@ -1085,8 +1123,9 @@ int ingot_layer_clone(const ingot_layer* src, ingot_layer** out) {
     DevMatrix* dm[6] = {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown};
     for (int i = 0; i < 6 && st == INGOT_OK; ++i) {
         *dm[i] = *sm[i];
-        dm[i]->d = nullptr;
+        dm[i]->d = dm[i]->t = nullptr;
         st = dup(sm[i]->d, sm[i]->nbytes, (void**)&dm[i]->d);
+        if (st == INGOT_OK) st = dup(sm[i]->t, sm[i]->nbytes, (void**)&dm[i]->t);
     }
     if (st != INGOT_OK) {
         free_dev(L);
@@ -1114,7 +1153,8 @@ int ingot_layer_set_gemm_mode(ingot_layer* L, uint32_t mode) {
 uint64_t ingot_layer_weight_bytes(const ingot_layer* L) {
     if (!L) return 0;
     uint64_t b = 4ull * L->E * L->H;
-    for (const DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) b += m->nbytes;
+    for (const DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown})
+        b += m->nbytes * (m->t ? 2u : 1u);
     return b;
 }
 
@@ -1362,6 +1402,11 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         // most one per token) and both projections have the TT 128 kernel.
         const bool tt128 = f16 && T > TM && f16_tt128_kind(gate.kind) && f16_tt128_kind(down.kind);
         const uint32_t tm = tt128 ? 2u * TM : TM;
+        // The f16 GEMMs read the tiled copies where every matrix of the launch has one.
+        const bool tlg = f16gu && gate.t && up.t && (!merge || (sgate.t && sup.t));
+        const bool tld = f16 && down.t && (!merge || sdown.t);
+        const uint8_t *g16 = tlg ? gate.t : gate.d, *u16 = tlg ? up.t : up.d, *d16 = tld ? down.t : down.d;
+        const uint8_t *sg16 = tlg ? sgate.t : sgate.d, *su16 = tlg ? sup.t : sup.d, *sd16 = tld ? sdown.t : sdown.d;
         const uint32_t S = merge ? T : 0u, capf = cap + (merge ? scap : 0u), e_sh = merge ? E : 0xffffffffu;
         _Float16 *xh = w.xh, *xl = w.xl, *acth = w.acth, *actl = w.actl;
         float *xs = w.xs, *acts = w.acts;
@@ -1390,8 +1435,8 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             const uint32_t* so = LL->pass.slot_of;
             if (f16gu) {
-                launch_gemm_f16<true>(ss, gate.kind, aord, tt128, dim3(8 * (F / 64) * ((capf + 7) / 8)), gate.d, up.d,
-                                      merge ? sgate.d : nullptr, merge ? sup.d : nullptr, e_sh, gate.stride, up.stride,
+                launch_gemm_f16<true>(ss, gate.kind, aord, tt128, tlg, dim3(8 * (F / 64) * ((capf + 7) / 8)), g16, u16,
+                                      merge ? sg16 : nullptr, merge ? su16 : nullptr, e_sh, gate.stride, up.stride,
                                       F, H, (const _Float16*)xh, (const _Float16*)xl, (const float*)xs,
                                       (const uint32_t*)pairs, K, (const uint32_t*)tiles, F, limit,
                                       f16 ? (float*)nullptr : act, acth, actl, mins ? acts : nullptr, F / 64, T,
@@ -1408,8 +1453,8 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         L->stage[ST_DOWN] = [=](hipStream_t ss) {
             const uint32_t* so = LL->pass.slot_of;
             if (f16)
-                launch_gemm_f16<false>(ss, down.kind, A_NATURAL, tt128, dim3(8 * (H / 128) * ((capf + 7) / 8)), down.d,
-                                       (const uint8_t*)nullptr, merge ? sdown.d : nullptr, (const uint8_t*)nullptr, e_sh,
+                launch_gemm_f16<false>(ss, down.kind, A_NATURAL, tt128, tld, dim3(8 * (H / 128) * ((capf + 7) / 8)), d16,
+                                       (const uint8_t*)nullptr, merge ? sd16 : nullptr, (const uint8_t*)nullptr, e_sh,
                                        down.stride, 0ull, H, F, (const _Float16*)acth, (const _Float16*)actl,
                                        (const float*)acts, (const uint32_t*)nullptr, K, (const uint32_t*)tiles, H, 0.f,
                                        Y, (_Float16*)nullptr, (_Float16*)nullptr, (float*)nullptr, H / 128,

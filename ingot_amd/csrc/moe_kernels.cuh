@@ -1854,6 +1854,24 @@ __device__ __forceinline__ half8 q4_operand(uint32_t b0, uint32_t b1, uint32_t s
 
 constexpr uint32_t TM16 = 64;  // tokens per tile of the f16 GEMM
 
+// Tiled weight layout of the f16 GEMM (k_tile_weights): a matrix's rows in
+// groups of 16 (a B row block), each group's 16 rows of bytes (16 x the row
+// stride, the same span as in GGUF order) rearranged into records, one per
+// superblock (Q4_K, IQ3_XXS) or 64-column slab (IQ4_NL), in which each load
+// instruction of the GEMM reads one contiguous span: lane l = 16 kq + ln
+// (row ln of the group, column quarter kq) finds its bytes at l times their
+// size. Record bytes:
+//   Q4_K (2304 per superblock): the 16 rows' 16-byte headers {d, dmin,
+//     scales} at 16 ln; then per slab sq = 0..3 of the superblock, at
+//     256 + 512 sq + 8 l, the 8 nibble bytes 16 + 32 sq + 8 kq .. + 7 of row ln.
+//   IQ3_XXS (1568 per superblock): at 16 l the 16 grid-index bytes
+//     2 + 16 kq .. + 15 of row ln; at 1024 + 8 l its aux words 66 + 8 kq .. + 7;
+//     at 1536 + 2 ln the row's d.
+//   IQ4_NL (576 per slab of two 18-byte blocks): at 8 l the nibble bytes
+//     2 + 4 kq .. + 3 of the slab's first block, then those of its second;
+//     at 512 + 4 ln the row's two d.
+constexpr uint32_t TILE_Q4K = 2304, TILE_IQ3XXS = 1568, TILE_IQ4NL = 576;
+
 // Raw buffer access: base and size in a buffer resource (scalar registers),
 // per-lane byte offset in a vector register, uniform byte offset in a scalar
 // register; reads past `bytes` return zero. Word 3 is the gfx9 raw-buffer
@@ -1902,7 +1920,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // as 8 x 2 MFMA tiles. Each decoded B fragment then feeds 16 MFMAs instead of
 // 8 and each weight byte is fetched once per 128 tokens instead of 64; the A
 // slab (128 rows) is shared by the 4 waves through LDS.
-template <int KIND, bool GATEUP, int AORD, int TT>
+//   TL: the weights are in the tiled layout of k_tile_weights (Q4_K, IQ3_XXS,
+// IQ4_NL), where each B load instruction reads one contiguous span (every lane
+// the bytes it decodes) instead of 16 rows' scattered pieces.
+template <int KIND, bool GATEUP, int AORD, int TT, bool TL = false>
 __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ ws0,
     const uint8_t* __restrict__ ws1, uint32_t e_shared, uint64_t stride0, uint64_t stride1, uint32_t rows_per_expert,
@@ -1963,6 +1984,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // byte it uses sits in a dword past its superblock), and d comes from a
     // 16-bit load.
     constexpr bool Q6K = KIND == 14;
+    static_assert(!TL || KIND == 12 || KIND == 18 || KIND == 20, "tiled layouts: Q4_K, IQ3_XXS, IQ4_NL");
     // (two operand sets per fragment: TT 128's 2 row blocks per wave fit the registers, 4 do not)
     static_assert(!Q6K || TT == 128, "Q6_K runs on 128-token tiles (which also take tiles of 64)");
     constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : IQ3S ? 110u : Q6K ? 210u : 98u;
@@ -2078,7 +2100,8 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= (int)HB ? rw1 : rw0;
-            if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
+            if constexpr (TL && Q4K) nhdr[nb] = buf_load16(rw, 16u * ln, bsoff[nb] + sb * TILE_Q4K);
+            else if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
             if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
             if constexpr (IQ2S) {
                 const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
@@ -2098,6 +2121,12 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 nqh3[nb] = buf_load16(rw, boff[nb], u + 64u);
                 nsc3[nb] = buf_load8(rw, boff[nb], u + 104u);
                 n_d[nb] = buf_load4(rw, boff[nb], u);
+            } else if constexpr (TL && IQ3) {
+                const uint32_t u = bsoff[nb] + sb * TILE_IQ3XXS;
+                nhdr[nb] = buf_load16(rw, 16u * lane, u);  // grid-index bytes
+                const uint2 a = buf_load8(rw, 8u * lane, u + 1024u);  // aux words
+                n3[nb] = make_uint3(a.x, a.y, 0u);
+                n_d[nb] = buf_load4(rw, 4u * (ln >> 1), u + 1536u);
             } else if constexpr (IQG) {
                 const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
                 nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);
@@ -2137,6 +2166,10 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                     nq[rs][nb].w = h[0];
                     nd[rs][nb] = make_uint2(h[1], h[2]);
                 }
+            } else if constexpr (TL && Q4K) {
+                const uint2 v = buf_load8(rw, 8u * lane, bsoff[nb] + (s >> 2) * TILE_Q4K + 256u + 512u * (s & 3u));
+                nq[rs][nb].x = v.x;
+                nq[rs][nb].y = v.y;
             } else if constexpr (Q4K) {
                 const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * SBB + QOFF + 32u * (s & 3u));
                 nq[rs][nb].x = v.x;
@@ -2146,6 +2179,15 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 nq[rs][nb].x = buf_load4(rw, boff[nb] + 4u * kq, u + 8u + 16u * g0);
                 n1[rs][nb] = buf_load4(rw, boff[nb] + 4u * kq, u + 24u + 16u * g0);
                 nd[rs][nb] = buf_load8(rw, boff[nb], u);
+            } else if constexpr (TL && IQ4) {
+                // qa, qb (the two blocks' nibble words) and the row's d0 | d1 << 16
+                const uint32_t u = bsoff[nb] + TILE_IQ4NL * s;
+                const uint2 q = buf_load8(rw, 8u * lane, u);
+                nq[rs][nb].x = q.x;
+                nq[rs][nb].y = q.y;
+                n1[rs][nb] = q.y;
+                const uint32_t dw = buf_load4(rw, 4u * ln, u + 512u);
+                nd[rs][nb] = make_uint2(dw, dw);
             } else if constexpr (IQ4) {
                 const uint32_t u = bsoff[nb] + 36u * s;
                 const uint2 q = buf_load8(rw, boff[nb] + 4u * kq, u);
@@ -2157,6 +2199,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
     };
     auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
+        if constexpr (TL && IQ3) return (ln & 1u) ? n_d[nb] >> 16 : n_d[nb];
         if constexpr (IQG) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
         if constexpr (Q6K) return n_d[nb];
         return nhdr[nb].x;
@@ -2218,6 +2261,14 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint32_t qh16 = ((kq < 2u ? h0 : h1) >> (16u * (kq & 1u))) & 0xffffu;
                 const uint32_t sc8 = (al(nsc3[nb].y, nsc3[nb].x) >> (8u * kq)) & 255u;
                 st.mn[nb][0] = qh16 | (sc8 << 16);
+                st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
+            } else if constexpr (TL && IQ3) {
+                st.gw[nb][0] = nhdr[nb].x;
+                st.gw[nb][1] = nhdr[nb].y;
+                st.gw[nb][2] = nhdr[nb].z;
+                st.gw[nb][3] = nhdr[nb].w;
+                st.aw[nb][0] = n3[nb].x;
+                st.aw[nb][1] = n3[nb].y;
                 st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
             } else if constexpr (IQG) {
                 const bool odd = (sb & 1u) != 0u;
@@ -2380,7 +2431,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                     d0 = d * (float)s0;
                     d1 = d * (float)s1;
                 } else {
-                    qa = __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u);
+                    qa = TL ? qv[nb].x : __builtin_amdgcn_alignbit(qv[nb].y, qv[nb].x, 16u);
                     qb = qv[nb].z;
                     d0 = half_bits_to_float(dv[nb].x & 0xffffu);
                     d1 = half_bits_to_float(dv[nb].y >> 16);
@@ -2410,9 +2461,13 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     };
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
-    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? 4u * NB : IQ4X ? 3u * NB : 0u;
-    constexpr uint32_t B_PER_SB =
-        Q5K ? 2u * NB + 1u : Q4K ? NB + 1u : (IQ2S || IQ3S) ? 7u * NB : IQG ? 5u * NB : Q6K ? 3u * NB : 0u;
+    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? (TL ? 2u : 4u) * NB : IQ4X ? 3u * NB : 0u;
+    constexpr uint32_t B_PER_SB = Q5K                ? 2u * NB + 1u
+                                  : Q4K              ? NB + 1u
+                                  : (IQ2S || IQ3S)   ? 7u * NB
+                                  : IQG              ? (TL ? 3u : 5u) * NB
+                                  : Q6K              ? 3u * NB
+                                                     : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
         constexpr uint32_t DEPTH = (!Q4K && !Q6K && MBE <= 2) ? 4u : 2u;
@@ -2925,6 +2980,47 @@ __global__ void k_combine_host(const float* __restrict__ routed, const float* __
     for (uint32_t e = 0; e < K; ++e) s += routed[(uint64_t)e * H + i] * w[e];
     if (shared) s += shared[i] / (1.0f + expf(-slogit[0]));
     out[i] = s;
+}
+
+// The GGUF-order byte of a tiled group's byte r (see TILE_Q4K): its offset
+// from the group's first row.
+__device__ __forceinline__ uint64_t tiled_source(uint32_t kind, uint32_t r, uint64_t stride) {
+    if (kind == 12) {
+        const uint32_t sb = r / TILE_Q4K, q = r % TILE_Q4K;
+        if (q < 256u) return (q >> 4) * stride + 144u * sb + (q & 15u);
+        const uint32_t t = q - 256u, sq = t >> 9, u = t & 511u, l = u >> 3;
+        return (l & 15u) * stride + 144u * sb + 16u + 32u * sq + 8u * (l >> 4) + (u & 7u);
+    }
+    if (kind == 18) {
+        const uint32_t sb = r / TILE_IQ3XXS, q = r % TILE_IQ3XXS;
+        if (q < 1024u) return ((q >> 4) & 15u) * stride + 98u * sb + 2u + 16u * (q >> 8) + (q & 15u);
+        if (q < 1536u) {
+            const uint32_t t = q - 1024u, l = t >> 3;
+            return (l & 15u) * stride + 98u * sb + 66u + 8u * (l >> 4) + (t & 7u);
+        }
+        const uint32_t t = q - 1536u;
+        return (t >> 1) * stride + 98u * sb + (t & 1u);
+    }
+    // IQ4_NL
+    const uint32_t sl = r / TILE_IQ4NL, q = r % TILE_IQ4NL;
+    if (q < 512u) {
+        const uint32_t l = q >> 3, b = q & 7u;
+        return (l & 15u) * stride + 36u * sl + 18u * (b >> 2) + 2u + 4u * (l >> 4) + (b & 3u);
+    }
+    const uint32_t t = q - 512u, b = t & 3u;
+    return (t >> 2) * stride + 36u * sl + (b < 2u ? b : 16u + b);
+}
+
+// dst = src (count x rows rows of `stride` bytes, rows % 16 == 0) in the
+// tiled layout; one byte per thread.
+__global__ __launch_bounds__(256) void k_tile_weights(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                      uint64_t nbytes, uint32_t kind, uint64_t stride) {
+    const uint64_t gbytes = 16u * stride;
+    for (uint64_t o = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; o < nbytes;
+         o += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t g = o / gbytes;
+        dst[o] = src[g * gbytes + tiled_source(kind, (uint32_t)(o - g * gbytes), stride)];
+    }
 }
 
 #endif  // INGOT_KIND_UNIT
