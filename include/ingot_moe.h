@@ -183,7 +183,11 @@ typedef struct ingot_layer_desc {
     float norm_eps;
 } ingot_layer_desc;
 
-/* Copies the layer to device memory (every expert resident). */
+/* Copies the layer to device memory (every expert resident). A matrix in a
+ * format the f16 prefill GEMM decodes (all but Q6_K; rows a multiple of 16)
+ * also gets a second copy, reordered so that each of that GEMM's weight
+ * loads reads one contiguous span; it doubles those matrices' device
+ * memory. */
 int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* desc, ingot_layer** out);
 /* A second resident copy of the same weights at new device addresses (not for
  * cached layers). */
@@ -268,7 +272,7 @@ int ingot_layer_forward_add(ingot_layer* layer, const float* d_x, const float* d
  * INGOT_GEMM_FP32: always the fp32 MFMA GEMM. */
 enum ingot_gemm_mode { INGOT_GEMM_AUTO = 0, INGOT_GEMM_FP32 = 1 };
 int ingot_layer_set_gemm_mode(ingot_layer* layer, uint32_t mode);
-/* Device bytes held by the layer's weights. */
+/* Device bytes held by the layer's weights (with the reordered copies). */
 uint64_t ingot_layer_weight_bytes(const ingot_layer* layer);
 
 /* ---- graphs and timing on the context stream ---- */

@@ -183,12 +183,17 @@ int upload_scoped(ingot_ctx* ctx, DevScope& sc, const ingot_matrix* m, DevMatrix
     return st;
 }
 
-// Formats with a tiled layout for the f16 GEMM (k_tile_weights): Q4_K,
-// IQ3_XXS and IQ4_NL, for the column counts the f16 GEMM takes them at, in
+// Formats with a tiled layout for the f16 GEMM (k_tile_weights): every f16
+// GEMM format but Q6_K, for the column counts the f16 GEMM takes them at, in
 // whole 16-row groups.
 bool tiled_kind(const DevMatrix& m) {
-    const bool cols_ok = (m.kind == 12 && m.cols % 256 == 0) || (m.kind == 18 && m.cols % 512 == 0) ||
-                         (m.kind == 20 && m.cols % 64 == 0);
+    bool cols_ok = false;
+    switch (m.kind) {
+        case 12: case 13: case 23: cols_ok = m.cols % 256 == 0; break;
+        case 17: case 18: case 21: case 22: cols_ok = m.cols % 512 == 0; break;
+        case 20: cols_ok = m.cols % 64 == 0; break;
+        default: break;
+    }
     return cols_ok && m.rows % 16 == 0;
 }
 
@@ -353,12 +358,12 @@ bool f16_tt128_kind(uint32_t kind) { return kind == 12 || kind == 13 || kind == 
 
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
 // projection's a_order); tt128: tiles of up to 128 tokens (f16_tt128_kind).
-// tl: the weights are the tiled copies (Q4_K, IQ3_XXS, IQ4_NL).
+// tl: the weights are the tiled copies (tiled_kind).
 template <bool GATEUP, typename... Args>
 bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, bool tl, dim3 grid, Args... args) {
 #define F16(KV, AO, TT)                                                                                      \
     do {                                                                                                     \
-        if constexpr (KV == 12 || KV == 18 || KV == 20) {                                                    \
+        if constexpr (KV != 14) {                                                                            \
             if (tl) {                                                                                        \
                 hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT, true>), grid, dim3(2 * TT), 0, s, args...); \
                 break;                                                                                       \

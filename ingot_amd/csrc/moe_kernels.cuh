@@ -1857,7 +1857,7 @@ constexpr uint32_t TM16 = 64;  // tokens per tile of the f16 GEMM
 // Tiled weight layout of the f16 GEMM (k_tile_weights): a matrix's rows in
 // groups of 16 (a B row block), each group's 16 rows of bytes (16 x the row
 // stride, the same span as in GGUF order) rearranged into records, one per
-// superblock (Q4_K, IQ3_XXS) or 64-column slab (IQ4_NL), in which each load
+// superblock (IQ4_NL: per 64-column slab), in which each load
 // instruction of the GEMM reads one contiguous span: lane l = 16 kq + ln
 // (row ln of the group, column quarter kq) finds its bytes at l times their
 // size. Record bytes:
@@ -1871,6 +1871,32 @@ constexpr uint32_t TM16 = 64;  // tokens per tile of the f16 GEMM
 //     2 + 4 kq .. + 3 of the slab's first block, then those of its second;
 //     at 512 + 4 ln the row's two d.
 constexpr uint32_t TILE_Q4K = 2304, TILE_IQ3XXS = 1568, TILE_IQ4NL = 576;
+//   Q5_K (2816): headers as Q4_K; at 256 + 8 l the qh bytes 16 + 8 kq .. + 7
+//     of row ln; per slab, at 768 + 512 sq + 8 l, the nibble bytes
+//     48 + 32 sq + 8 kq .. + 7.
+//   IQ2_XS (1184): at 16 l the codes 2 + 16 kq .. + 15 of row ln; at
+//     1024 + 8 ln the row's 8 scale bytes; at 1152 + 2 ln its d.
+//   IQ2_S (1312): at 16 l the index bytes 2 + 8 kq .. + 7 of row ln, then its
+//     sign bytes 34 + 8 kq .. + 7; at 1024 + 4 l the qh bytes 66 + 2 kq, + 1
+//     and the scale bytes 74 + 2 kq, + 1; at 1280 + 2 ln the row's d.
+//   IQ3_S (1760): at 16 l the grid-index bytes 2 + 16 kq .. + 15 of row ln;
+//     at 1024 + 8 l its sign bytes 74 + 8 kq .. + 7; at 1536 + 12 ln the row's
+//     8 qh bytes and 4 scale bytes; at 1728 + 2 ln its d.
+//   IQ4_XS (2176): per slab sq, at 512 sq + 8 l the nibble bytes 4 kq .. + 3
+//     of blocks 2 sq and 2 sq + 1 of row ln; at 2048 + 8 ln the row's d,
+//     scales_h and scales_l.
+constexpr uint32_t TILE_Q5K = 2816, TILE_IQ2XS = 1184, TILE_IQ2S = 1312, TILE_IQ3S = 1760, TILE_IQ4XS = 2176;
+__host__ __device__ constexpr uint32_t tile_record(int kind) {
+    return kind == 12   ? TILE_Q4K
+           : kind == 13 ? TILE_Q5K
+           : kind == 17 ? TILE_IQ2XS
+           : kind == 18 ? TILE_IQ3XXS
+           : kind == 20 ? TILE_IQ4NL
+           : kind == 21 ? TILE_IQ3S
+           : kind == 22 ? TILE_IQ2S
+           : kind == 23 ? TILE_IQ4XS
+                        : 0u;
+}
 
 // Raw buffer access: base and size in a buffer resource (scalar registers),
 // per-lane byte offset in a vector register, uniform byte offset in a scalar
@@ -1920,9 +1946,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // as 8 x 2 MFMA tiles. Each decoded B fragment then feeds 16 MFMAs instead of
 // 8 and each weight byte is fetched once per 128 tokens instead of 64; the A
 // slab (128 rows) is shared by the 4 waves through LDS.
-//   TL: the weights are in the tiled layout of k_tile_weights (Q4_K, IQ3_XXS,
-// IQ4_NL), where each B load instruction reads one contiguous span (every lane
-// the bytes it decodes) instead of 16 rows' scattered pieces.
+//   TL: the weights are in the tiled layout of k_tile_weights (every format
+// here but Q6_K), where each B load instruction reads one contiguous span
+// (every lane the bytes it decodes) instead of 16 rows' scattered pieces.
 template <int KIND, bool GATEUP, int AORD, int TT, bool TL = false>
 __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, const uint8_t* __restrict__ ws0,
@@ -1984,11 +2010,13 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // byte it uses sits in a dword past its superblock), and d comes from a
     // 16-bit load.
     constexpr bool Q6K = KIND == 14;
-    static_assert(!TL || KIND == 12 || KIND == 18 || KIND == 20, "tiled layouts: Q4_K, IQ3_XXS, IQ4_NL");
+    static_assert(!TL || (KIND != 14 && KIND != 0), "no tiled layout for Q6_K");
     // (two operand sets per fragment: TT 128's 2 row blocks per wave fit the registers, 4 do not)
     static_assert(!Q6K || TT == 128, "Q6_K runs on 128-token tiles (which also take tiles of 64)");
     constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : IQ3S ? 110u : Q6K ? 210u : 98u;
     constexpr uint32_t SBB = Q5K ? 176u : 144u, QOFF = Q5K ? 48u : 16u;
+    // tiled record bytes (per superblock; IQ4_NL: per slab)
+    constexpr uint32_t TREC = tile_record(KIND);
     constexpr uint32_t UNR = 4u;
     // A slab buffers (hi, lo; by slab parity): 64 halves (128 B) per token row,
     // 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7), so that the fragment
@@ -2100,10 +2128,26 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= (int)HB ? rw1 : rw0;
-            if constexpr (TL && Q4K) nhdr[nb] = buf_load16(rw, 16u * ln, bsoff[nb] + sb * TILE_Q4K);
+            if constexpr (TL && Q4K) nhdr[nb] = buf_load16(rw, 16u * ln, bsoff[nb] + sb * TREC);
             else if constexpr (Q4K) nhdr[nb] = buf_load16(rw, boff[nb], bsoff[nb] + sb * SBB);
-            if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
-            if constexpr (IQ2S) {
+            if constexpr (TL && Q5K) nqh[nb] = buf_load8(rw, 8u * lane, bsoff[nb] + sb * TREC + 256u);
+            else if constexpr (Q5K) nqh[nb] = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + sb * SBB + 16u);
+            if constexpr (TL && IQ2S) {
+                const uint32_t u = bsoff[nb] + sb * TREC;
+                const uint4 is = buf_load16(rw, 16u * lane, u);  // index bytes, sign bytes
+                n3[nb] = make_uint3(is.x, is.y, 0u);
+                ns3[nb] = make_uint3(is.z, is.w, 0u);
+                nhdr[nb].x = buf_load4(rw, 4u * lane, u + 1024u);  // qh16 | sc16 << 16
+                n_d[nb] = buf_load4(rw, 4u * (ln >> 1), u + 1280u);
+            } else if constexpr (TL && IQ3S) {
+                const uint32_t u = bsoff[nb] + sb * TREC;
+                nhdr[nb] = buf_load16(rw, 16u * lane, u);  // grid-index bytes
+                const uint2 g = buf_load8(rw, 8u * lane, u + 1024u);  // sign bytes
+                n3[nb] = make_uint3(g.x, g.y, 0u);
+                const auto h = __builtin_amdgcn_raw_buffer_load_b96(rw, (int)(12u * ln), (int)(u + 1536u), 0);
+                nqh3[nb] = make_uint4(h[0], h[1], h[2], 0u);  // the row's qh bytes, scale bytes
+                n_d[nb] = buf_load4(rw, 4u * (ln >> 1), u + 1728u);
+            } else if constexpr (IQ2S) {
                 const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
                 nhdr[nb] = buf_load16(rw, boff[nb], u + 64u);  // index high bits and scales
                 n5[nb] = buf_load4(rw, boff[nb], u + 80u);
@@ -2121,12 +2165,14 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 nqh3[nb] = buf_load16(rw, boff[nb], u + 64u);
                 nsc3[nb] = buf_load8(rw, boff[nb], u + 104u);
                 n_d[nb] = buf_load4(rw, boff[nb], u);
-            } else if constexpr (TL && IQ3) {
-                const uint32_t u = bsoff[nb] + sb * TILE_IQ3XXS;
-                nhdr[nb] = buf_load16(rw, 16u * lane, u);  // grid-index bytes
-                const uint2 a = buf_load8(rw, 8u * lane, u + 1024u);  // aux words
+            } else if constexpr (TL && (IQ3 || IQ2)) {
+                // IQ3_XXS: the lane's grid-index bytes and aux words, the row's d;
+                // IQ2_XS: the lane's codes, the row's 8 scale bytes and d
+                const uint32_t u = bsoff[nb] + sb * TREC;
+                nhdr[nb] = buf_load16(rw, 16u * lane, u);
+                const uint2 a = buf_load8(rw, IQ3 ? 8u * lane : 8u * ln, u + 1024u);
                 n3[nb] = make_uint3(a.x, a.y, 0u);
-                n_d[nb] = buf_load4(rw, 4u * (ln >> 1), u + 1536u);
+                n_d[nb] = buf_load4(rw, 4u * (ln >> 1), u + (IQ3 ? 1536u : 1152u));
             } else if constexpr (IQG) {
                 const uint32_t u = (bsoff[nb] + sb * IQB) & ~3u;
                 nhdr[nb] = buf_load16(rw, boff[nb] + 16u * kq, u);
@@ -2167,13 +2213,19 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                     nd[rs][nb] = make_uint2(h[1], h[2]);
                 }
             } else if constexpr (TL && Q4K) {
-                const uint2 v = buf_load8(rw, 8u * lane, bsoff[nb] + (s >> 2) * TILE_Q4K + 256u + 512u * (s & 3u));
+                const uint2 v = buf_load8(rw, 8u * lane, bsoff[nb] + (s >> 2) * TREC + (Q5K ? 768u : 256u) + 512u * (s & 3u));
                 nq[rs][nb].x = v.x;
                 nq[rs][nb].y = v.y;
             } else if constexpr (Q4K) {
                 const uint2 v = buf_load8(rw, boff[nb] + 8u * kq, bsoff[nb] + (s >> 2) * SBB + QOFF + 32u * (s & 3u));
                 nq[rs][nb].x = v.x;
                 nq[rs][nb].y = v.y;
+            } else if constexpr (TL && IQ4X) {
+                const uint32_t u = bsoff[nb] + (s >> 2) * TREC;
+                const uint2 q = buf_load8(rw, 8u * lane, u + 512u * (s & 3u));
+                nq[rs][nb].x = q.x;
+                n1[rs][nb] = q.y;
+                nd[rs][nb] = buf_load8(rw, 8u * ln, u + 2048u);
             } else if constexpr (IQ4X) {
                 const uint32_t u = bsoff[nb] + (s >> 2) * 136u, g0 = 2u * (s & 3u);
                 nq[rs][nb].x = buf_load4(rw, boff[nb] + 4u * kq, u + 8u + 16u * g0);
@@ -2181,7 +2233,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 nd[rs][nb] = buf_load8(rw, boff[nb], u);
             } else if constexpr (TL && IQ4) {
                 // qa, qb (the two blocks' nibble words) and the row's d0 | d1 << 16
-                const uint32_t u = bsoff[nb] + TILE_IQ4NL * s;
+                const uint32_t u = bsoff[nb] + TREC * s;
                 const uint2 q = buf_load8(rw, 8u * lane, u);
                 nq[rs][nb].x = q.x;
                 nq[rs][nb].y = q.y;
@@ -2199,7 +2251,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
         }
     };
     auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
-        if constexpr (TL && IQ3) return (ln & 1u) ? n_d[nb] >> 16 : n_d[nb];
+        if constexpr (TL && IQG) return (ln & 1u) ? n_d[nb] >> 16 : n_d[nb];
         if constexpr (IQG) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
         if constexpr (Q6K) return n_d[nb];
         return nhdr[nb].x;
@@ -2228,6 +2280,24 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 // dmin 2^24, times 32: the group sums enter the MFMA divided by 32
                 st.dmn[nb] = half_bits_to_float(nhdr[nb].x >> 16) * 536870912.f;
                 if (half_bits_to_float(nhdr[nb].x) == 0.f) st.sc[nb][0] = st.sc[nb][1] = 0u;
+            } else if constexpr (TL && IQ2S) {
+                st.gw[nb][0] = n3[nb].x;
+                st.gw[nb][1] = n3[nb].y;
+                st.gw[nb][2] = ns3[nb].x;
+                st.gw[nb][3] = ns3[nb].y;
+                st.aw[nb][0] = nhdr[nb].x;
+                st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
+            } else if constexpr (TL && IQ3S) {
+                st.gw[nb][0] = nhdr[nb].x;
+                st.gw[nb][1] = nhdr[nb].y;
+                st.gw[nb][2] = nhdr[nb].z;
+                st.gw[nb][3] = nhdr[nb].w;
+                st.aw[nb][0] = n3[nb].x;
+                st.aw[nb][1] = n3[nb].y;
+                const uint32_t qh16 = ((kq < 2u ? nqh3[nb].x : nqh3[nb].y) >> (16u * (kq & 1u))) & 0xffffu;
+                const uint32_t sc8 = (nqh3[nb].z >> (8u * kq)) & 255u;
+                st.mn[nb][0] = qh16 | (sc8 << 16);
+                st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
             } else if constexpr (IQ2S) {
                 // gw: the lane's index words (0, 1) and sign words (2, 3);
                 // aw[0]: index high-bit bytes of its groups 2 kq, 2 kq + 1 in
@@ -2262,7 +2332,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint32_t sc8 = (al(nsc3[nb].y, nsc3[nb].x) >> (8u * kq)) & 255u;
                 st.mn[nb][0] = qh16 | (sc8 << 16);
                 st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
-            } else if constexpr (TL && IQ3) {
+            } else if constexpr (TL && (IQ3 || IQ2)) {
                 st.gw[nb][0] = nhdr[nb].x;
                 st.gw[nb][1] = nhdr[nb].y;
                 st.gw[nb][2] = nhdr[nb].z;
@@ -2461,10 +2531,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     };
     // Vector-memory loads issued after a slab's A DMA: the B ring's, and at a
     // superblock's first slab its header (and Q4_K group sums).
-    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? (TL ? 2u : 4u) * NB : IQ4X ? 3u * NB : 0u;
+    constexpr uint32_t B_PER_SLAB = Q4K ? NB : IQ4 ? (TL ? 2u : 4u) * NB : IQ4X ? (TL ? 2u : 3u) * NB : 0u;
     constexpr uint32_t B_PER_SB = Q5K                ? 2u * NB + 1u
                                   : Q4K              ? NB + 1u
-                                  : (IQ2S || IQ3S)   ? 7u * NB
+                                  : IQ2S             ? (TL ? 3u : 7u) * NB
+                                  : IQ3S             ? (TL ? 4u : 7u) * NB
                                   : IQG              ? (TL ? 3u : 5u) * NB
                                   : Q6K              ? 3u * NB
                                                      : 0u;
@@ -2990,6 +3061,59 @@ __device__ __forceinline__ uint64_t tiled_source(uint32_t kind, uint32_t r, uint
         if (q < 256u) return (q >> 4) * stride + 144u * sb + (q & 15u);
         const uint32_t t = q - 256u, sq = t >> 9, u = t & 511u, l = u >> 3;
         return (l & 15u) * stride + 144u * sb + 16u + 32u * sq + 8u * (l >> 4) + (u & 7u);
+    }
+    if (kind == 13) {
+        const uint32_t sb = r / TILE_Q5K, q = r % TILE_Q5K;
+        if (q < 256u) return (q >> 4) * stride + 176u * sb + (q & 15u);
+        if (q < 768u) {
+            const uint32_t t = q - 256u, l = t >> 3;
+            return (l & 15u) * stride + 176u * sb + 16u + 8u * (l >> 4) + (t & 7u);
+        }
+        const uint32_t t = q - 768u, sq = t >> 9, u = t & 511u, l = u >> 3;
+        return (l & 15u) * stride + 176u * sb + 48u + 32u * sq + 8u * (l >> 4) + (u & 7u);
+    }
+    if (kind == 17) {
+        const uint32_t sb = r / TILE_IQ2XS, q = r % TILE_IQ2XS;
+        if (q < 1024u) return ((q >> 4) & 15u) * stride + 74u * sb + 2u + 16u * (q >> 8) + (q & 15u);
+        if (q < 1152u) return ((q - 1024u) >> 3) * stride + 74u * sb + 66u + (q & 7u);
+        const uint32_t t = q - 1152u;
+        return (t >> 1) * stride + 74u * sb + (t & 1u);
+    }
+    if (kind == 22) {
+        const uint32_t sb = r / TILE_IQ2S, q = r % TILE_IQ2S;
+        if (q < 1024u) {
+            const uint32_t l = q >> 4, b = q & 15u;
+            return (l & 15u) * stride + 82u * sb + (b < 8u ? 2u : 26u) + 8u * (l >> 4) + b;
+        }
+        if (q < 1280u) {
+            const uint32_t t = q - 1024u, l = t >> 2, b = t & 3u;
+            return (l & 15u) * stride + 82u * sb + (b < 2u ? 66u : 72u) + 2u * (l >> 4) + b;
+        }
+        const uint32_t t = q - 1280u;
+        return (t >> 1) * stride + 82u * sb + (t & 1u);
+    }
+    if (kind == 21) {
+        const uint32_t sb = r / TILE_IQ3S, q = r % TILE_IQ3S;
+        if (q < 1024u) return ((q >> 4) & 15u) * stride + 110u * sb + 2u + 16u * (q >> 8) + (q & 15u);
+        if (q < 1536u) {
+            const uint32_t t = q - 1024u, l = t >> 3;
+            return (l & 15u) * stride + 110u * sb + 74u + 8u * (l >> 4) + (t & 7u);
+        }
+        if (q < 1728u) {
+            const uint32_t t = q - 1536u, row = t / 12u, b = t % 12u;
+            return row * stride + 110u * sb + (b < 8u ? 66u + b : 98u + b);
+        }
+        const uint32_t t = q - 1728u;
+        return (t >> 1) * stride + 110u * sb + (t & 1u);
+    }
+    if (kind == 23) {
+        const uint32_t sb = r / TILE_IQ4XS, q = r % TILE_IQ4XS;
+        if (q < 2048u) {
+            const uint32_t sq = q >> 9, u = q & 511u, l = u >> 3, b = u & 7u;
+            return (l & 15u) * stride + 136u * sb + 8u + 16u * (2u * sq + (b >> 2)) + 4u * (l >> 4) + (b & 3u);
+        }
+        const uint32_t t = q - 2048u;
+        return (t >> 3) * stride + 136u * sb + (t & 7u);
     }
     if (kind == 18) {
         const uint32_t sb = r / TILE_IQ3XXS, q = r % TILE_IQ3XXS;

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from ingot_amd import configs as CF
-from ingot_amd.moe import IQ4_NL, Q4_K, InvalidData, MoeLayer
+from ingot_amd.moe import IQ2_S, IQ2_XS, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, Q4_K, Q5_K, STAGE_DOWN, InvalidData, MoeLayer
 from test_expert_cache import Cache
 from util import check_layer
 
@@ -60,15 +60,20 @@ def test_cached_layer_parity_and_counters(gpu, oracle, slots):
     layer.destroy()
 
 
-def test_cached_equals_resident_bit_for_bit(gpu):
-    """Same kernels on both (prefill path, 160 pairs): each tile's products and
-    the combine are the same operations, so the outputs are identical."""
-    spec = CF.make_layer(32, 0, 2048, 32, 4, 512, Q4_K, Q4_K, shared_ffn=512)
+@pytest.mark.parametrize("gk,dk", [(Q4_K, Q4_K), (Q5_K, Q5_K), (IQ2_XS, IQ2_XS), (IQ2_S, IQ4_XS),
+                                   (IQ3_XXS, IQ4_NL), (IQ3_S, IQ3_S)])
+def test_cached_equals_resident_bit_for_bit(gpu, gk, dk):
+    """Prefill path, 160 pairs, merged shared expert. The resident layer's f16
+    GEMMs read the tiled weight copies, the cached layer's read its slots in
+    GGUF order; both decode the same operands and run the same products and
+    combine, so the outputs are identical (which pins each tiled layout)."""
+    spec = CF.make_layer(32, 0, 2048, 32, 4, 512, gk, dk, shared_ffn=512)
     x = CF.inputs(32, 40, 2048)
     res = MoeLayer(gpu, spec)
     cached = MoeLayer(gpu, spec, cache_slots=5)
     o1, i1, w1 = res(x)
     o2, i2, w2 = cached(x)
+    assert res.stage_kernel(STAGE_DOWN) == "k_gemm_f16<down>"
     assert np.array_equal(i1, i2) and np.array_equal(w1, w2)
     assert np.array_equal(o1, o2)
     assert cached.cache_stats()["misses"] == len(np.unique(i2))
