@@ -184,7 +184,7 @@ typedef struct ingot_layer_desc {
 } ingot_layer_desc;
 
 /* Copies the layer to device memory (every expert resident). A matrix in a
- * format the f16 prefill GEMM decodes (all but Q6_K; rows a multiple of 16)
+ * format the f16 prefill GEMM decodes (rows a multiple of 16)
  * also gets a second copy, reordered so that each of that GEMM's weight
  * loads reads one contiguous span; it doubles those matrices' device
  * memory. */

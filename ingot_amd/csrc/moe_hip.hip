@@ -184,12 +184,12 @@ int upload_scoped(ingot_ctx* ctx, DevScope& sc, const ingot_matrix* m, DevMatrix
 }
 
 // Formats with a tiled layout for the f16 GEMM (k_tile_weights): every f16
-// GEMM format but Q6_K, for the column counts the f16 GEMM takes them at, in
-// whole 16-row groups.
+// GEMM format, for the column counts the f16 GEMM takes them at, in whole
+// 16-row groups.
 bool tiled_kind(const DevMatrix& m) {
     bool cols_ok = false;
     switch (m.kind) {
-        case 12: case 13: case 23: cols_ok = m.cols % 256 == 0; break;
+        case 12: case 13: case 14: case 23: cols_ok = m.cols % 256 == 0; break;
         case 17: case 18: case 21: case 22: cols_ok = m.cols % 512 == 0; break;
         case 20: cols_ok = m.cols % 64 == 0; break;
         default: break;
@@ -363,11 +363,9 @@ template <bool GATEUP, typename... Args>
 bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, bool tl, dim3 grid, Args... args) {
 #define F16(KV, AO, TT)                                                                                      \
     do {                                                                                                     \
-        if constexpr (KV != 14) {                                                                            \
-            if (tl) {                                                                                        \
-                hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT, true>), grid, dim3(2 * TT), 0, s, args...); \
-                break;                                                                                       \
-            }                                                                                                \
+        if (tl) {                                                                                            \
+            hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT, true>), grid, dim3(2 * TT), 0, s, args...);   \
+            break;                                                                                           \
         }                                                                                                    \
         hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT>), grid, dim3(2 * TT), 0, s, args...);             \
     } while (0)

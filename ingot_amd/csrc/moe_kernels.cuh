@@ -1885,10 +1885,16 @@ constexpr uint32_t TILE_Q4K = 2304, TILE_IQ3XXS = 1568, TILE_IQ4NL = 576;
 //   IQ4_XS (2176): per slab sq, at 512 sq + 8 l the nibble bytes 4 kq .. + 3
 //     of blocks 2 sq and 2 sq + 1 of row ln; at 2048 + 8 ln the row's d,
 //     scales_h and scales_l.
-constexpr uint32_t TILE_Q5K = 2816, TILE_IQ2XS = 1184, TILE_IQ2S = 1312, TILE_IQ3S = 1760, TILE_IQ4XS = 2176;
+//   Q6_K (3360): per slab sq, at 512 sq + 8 l the ql bytes
+//     64 (sq / 2) + 32 (sq % 2) + 8 kq .. + 7 of row ln; per half n, at
+//     2048 + 512 n + 8 l its qh bytes 128 + 32 n + 8 kq .. + 7; at 3072 + 16 ln
+//     the row's 16 scale bytes; at 3328 + 2 ln its d.
+constexpr uint32_t TILE_Q5K = 2816, TILE_IQ2XS = 1184, TILE_IQ2S = 1312, TILE_IQ3S = 1760, TILE_IQ4XS = 2176,
+                   TILE_Q6K = 3360;
 __host__ __device__ constexpr uint32_t tile_record(int kind) {
     return kind == 12   ? TILE_Q4K
            : kind == 13 ? TILE_Q5K
+           : kind == 14 ? TILE_Q6K
            : kind == 17 ? TILE_IQ2XS
            : kind == 18 ? TILE_IQ3XXS
            : kind == 20 ? TILE_IQ4NL
@@ -1946,8 +1952,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 // as 8 x 2 MFMA tiles. Each decoded B fragment then feeds 16 MFMAs instead of
 // 8 and each weight byte is fetched once per 128 tokens instead of 64; the A
 // slab (128 rows) is shared by the 4 waves through LDS.
-//   TL: the weights are in the tiled layout of k_tile_weights (every format
-// here but Q6_K), where each B load instruction reads one contiguous span
+//   TL: the weights are in the tiled layout of k_tile_weights, where each B
+// load instruction reads one contiguous span
 // (every lane the bytes it decodes) instead of 16 rows' scattered pieces.
 template <int KIND, bool GATEUP, int AORD, int TT, bool TL = false>
 __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_f16(
@@ -2010,7 +2016,6 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // byte it uses sits in a dword past its superblock), and d comes from a
     // 16-bit load.
     constexpr bool Q6K = KIND == 14;
-    static_assert(!TL || (KIND != 14 && KIND != 0), "no tiled layout for Q6_K");
     // (two operand sets per fragment: TT 128's 2 row blocks per wave fit the registers, 4 do not)
     static_assert(!Q6K || TT == 128, "Q6_K runs on 128-token tiles (which also take tiles of 64)");
     constexpr uint32_t IQB = IQ2 ? 74u : IQ2S ? 82u : IQ3S ? 110u : Q6K ? 210u : 98u;
@@ -2182,6 +2187,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const uint2 a = buf_load8(rw, ao, u + 64u);
                 n3[nb] = make_uint3(a.x, a.y, buf_load4(rw, ao, u + 72u));
                 n_d[nb] = buf_load4(rw, boff[nb], u);
+            } else if constexpr (TL && Q6K) {
+                const uint32_t u = bsoff[nb] + sb * TREC;
+                nhdr[nb] = buf_load16(rw, 16u * ln, u + 3072u);  // the row's 16 scale bytes
+                n5[nb] = 0u;
+                n_d[nb] = buf_load4(rw, 4u * (ln >> 1), u + 3328u);
             } else if constexpr (Q6K) {
                 // the 16 scale bytes (192) in a 20-byte window, d (208)
                 const uint32_t b = q6r[nb] + sb * IQB, a = b & ~3u;
@@ -2201,7 +2211,19 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const __amdgpu_buffer_rsrc_t rw = GATEUP && nb >= (int)HB ? rw1 : rw0;
-            if constexpr (Q6K) {
+            if constexpr (TL && Q6K) {
+                // ql bytes of the slab, and at a half's first slab its qh bytes
+                const uint32_t u = bsoff[nb] + (s >> 2) * TREC, hn = (s >> 1) & 1u;
+                const uint2 l = buf_load8(rw, 8u * lane, u + 512u * (s & 3u));
+                nq[rs][nb].x = l.x;
+                nq[rs][nb].y = l.y;
+                nq[rs][nb].z = 0u;
+                if (ev) {
+                    const uint2 h = buf_load8(rw, 8u * lane, u + 2048u + 512u * hn);
+                    nq[rs][nb].w = h.x;
+                    nd[rs][nb] = make_uint2(h.y, 0u);
+                }
+            } else if constexpr (Q6K) {
                 const uint32_t a = (q6r[nb] + 8u * kq + (s >> 2) * IQB) & ~3u, hn = (s >> 1) & 1u;
                 const auto l = __builtin_amdgcn_raw_buffer_load_b96(rw, (int)a, (int)(64u * hn + 32u * (s & 1u)), 0);
                 nq[rs][nb].x = l[0];
@@ -2253,6 +2275,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     auto dbits = [&](int nb, uint32_t sb) -> uint32_t {
         if constexpr (TL && IQG) return (ln & 1u) ? n_d[nb] >> 16 : n_d[nb];
         if constexpr (IQG) return (sb & 1u) ? n_d[nb] >> 16 : n_d[nb];
+        if constexpr (TL && Q6K) return ((ln & 1u) ? n_d[nb] >> 16 : n_d[nb]) & 0xffffu;
         if constexpr (Q6K) return n_d[nb];
         return nhdr[nb].x;
     };
@@ -2351,7 +2374,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                 st.sc[nb][0] = half_bits_to_float(db) == 0.f ? 0u : 1u;
             } else if constexpr (Q6K) {
                 // gw: the 16 int8 scales (zero with d, which zeroes B)
-                st.sh[nb] = ((q6r[nb] + sb * IQB) & 2u) << 3;
+                st.sh[nb] = TL ? 0u : ((q6r[nb] + sb * IQB) & 2u) << 3;
                 const uint32_t w[5] = {nhdr[nb].x, nhdr[nb].y, nhdr[nb].z, nhdr[nb].w, n5[nb]};
                 const bool z = half_bits_to_float(db) == 0.f;
 #pragma unroll
@@ -2537,7 +2560,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                                   : IQ2S             ? (TL ? 3u : 7u) * NB
                                   : IQ3S             ? (TL ? 4u : 7u) * NB
                                   : IQG              ? (TL ? 3u : 5u) * NB
-                                  : Q6K              ? 3u * NB
+                                  : Q6K              ? (TL ? 2u : 3u) * NB
                                                      : 0u;
     auto run = [&](auto mbe_tag) {
         constexpr int MBE = decltype(mbe_tag)::value;
@@ -3071,6 +3094,23 @@ __device__ __forceinline__ uint64_t tiled_source(uint32_t kind, uint32_t r, uint
         }
         const uint32_t t = q - 768u, sq = t >> 9, u = t & 511u, l = u >> 3;
         return (l & 15u) * stride + 176u * sb + 48u + 32u * sq + 8u * (l >> 4) + (u & 7u);
+    }
+    if (kind == 14) {
+        const uint32_t sb = r / TILE_Q6K, q = r % TILE_Q6K;
+        if (q < 2048u) {
+            const uint32_t sq = q >> 9, u = q & 511u, l = u >> 3;
+            return (l & 15u) * stride + 210u * sb + 64u * (sq >> 1) + 32u * (sq & 1u) + 8u * (l >> 4) + (u & 7u);
+        }
+        if (q < 3072u) {
+            const uint32_t t = q - 2048u, n = t >> 9, u = t & 511u, l = u >> 3;
+            return (l & 15u) * stride + 210u * sb + 128u + 32u * n + 8u * (l >> 4) + (u & 7u);
+        }
+        if (q < 3328u) {
+            const uint32_t t = q - 3072u;
+            return (t >> 4) * stride + 210u * sb + 192u + (t & 15u);
+        }
+        const uint32_t t = q - 3328u;
+        return (t >> 1) * stride + 210u * sb + 208u + (t & 1u);
     }
     if (kind == 17) {
         const uint32_t sb = r / TILE_IQ2XS, q = r % TILE_IQ2XS;

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from ingot_amd import configs as CF
-from ingot_amd.moe import IQ2_S, IQ2_XS, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, Q4_K, Q5_K, STAGE_DOWN, InvalidData, MoeLayer
+from ingot_amd.moe import IQ2_S, IQ2_XS, IQ3_S, IQ3_XXS, IQ4_NL, IQ4_XS, Q4_K, Q5_K, Q6_K, STAGE_DOWN, InvalidData, MoeLayer
 from test_expert_cache import Cache
 from util import check_layer
 
@@ -60,8 +60,8 @@ def test_cached_layer_parity_and_counters(gpu, oracle, slots):
     layer.destroy()
 
 
-@pytest.mark.parametrize("gk,dk", [(Q4_K, Q4_K), (Q5_K, Q5_K), (IQ2_XS, IQ2_XS), (IQ2_S, IQ4_XS),
-                                   (IQ3_XXS, IQ4_NL), (IQ3_S, IQ3_S)])
+@pytest.mark.parametrize("gk,dk", [(Q4_K, Q4_K), (Q5_K, Q5_K), (Q6_K, Q6_K), (Q4_K, Q6_K), (IQ2_XS, IQ2_XS),
+                                   (IQ2_S, IQ4_XS), (IQ3_XXS, IQ4_NL), (IQ3_S, IQ3_S)])
 def test_cached_equals_resident_bit_for_bit(gpu, gk, dk):
     """Prefill path, 160 pairs, merged shared expert. The resident layer's f16
     GEMMs read the tiled weight copies, the cached layer's read its slots in
