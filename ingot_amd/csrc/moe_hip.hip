@@ -233,16 +233,17 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
     // wide (T x E / 4 blocks); from 64 tokens the 64-output transposed kernel.
     const bool decode = T < 64;
     if (!decode && E % 32u == 0 && (HB == 4 || HB == 8)) {
-        // 16 experts per block when 32 would leave fewer than two blocks per CU
-        const bool eb16 = (T + 7) / 8 * (E / 32) < 512;
-        const dim3 grid((T + 7) / 8, E / (eb16 ? 16 : 32));
-#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV>), grid, dim3(256), 0, s, x, addend, W, sgvec, gain, eps, T, E, logits, sgl, xn, xs, xstat)
+        // 4 tokens per wave (16 per block); 16 experts per block when that
+        // leaves at least two blocks per CU, else 8
+        const bool eb16 = (T + 15) / 16 * (E / 16) >= 512;
+        const dim3 grid((T + 15) / 16, E / (eb16 ? 16 : 8));
+#define RT(HBV, EBV) hipLaunchKernelGGL((k_router_t<HBV, EBV, 4>), grid, dim3(256), 0, s, x, addend, W, sgvec, gain, eps, T, E, logits, sgl, xn, xs, xstat)
         if (HB == 8) {
             if (eb16) RT(8, 16);
-            else RT(8, 32);
+            else RT(8, 8);
         } else {
             if (eb16) RT(4, 16);
-            else RT(4, 32);
+            else RT(4, 8);
         }
 #undef RT
         return true;

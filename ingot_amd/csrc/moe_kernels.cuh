@@ -605,19 +605,21 @@ __device__ __forceinline__ float transpose_sum64(float (&v)[64], uint32_t lane) 
     return v[0];
 }
 
-// Prefill router: grid (ceil(T / 8), E / EB), 256 threads, EB = 32 or 16
-// experts per block (16: twice the blocks, two per CU, for short inputs).
-// Wave w of block (bx, by) computes the logits of tokens 8 bx + 2 w, +1 for
-// experts EB by .. +EB-1: lane l keeps the fixed-order FMA chain of its
-// columns 4 l + 256 i + c (as k_router) for each of the 2 EB (token, expert)
-// pairs, and one transposed butterfly leaves pair (t, e) = (l / 32, l % 32)
-// (EB = 32) or (l / 32, (l / 2) % 16) (EB = 16) in lane l.
+// Prefill router: grid (ceil(T / (4 TPW)), E / EB), 256 threads, TPW tokens
+// per wave and EB experts per block, TPW EB = 32 or 64 (the launcher takes
+// TPW = 4: each router value read from LDS feeds four FMAs; EB = 16, or 8 when
+// 16 would leave fewer than two blocks per CU). Wave w of block (bx, by)
+// computes the logits of tokens 4 TPW bx + TPW w .. + TPW - 1 for experts
+// EB by .. + EB - 1: lane l keeps the fixed-order FMA chain of its columns
+// 4 l + 256 i + c (as k_router) for each of the TPW EB (token, expert) pairs,
+// and one transposed butterfly leaves pair i = TPW EB == 64 ? l : l / 2,
+// (t, e) = (i / EB, i % EB), in lane l.
 // The block's router rows pass through LDS in double-buffered chunks of 4.
 // The residual add (addend: s written to xs by the by == 0 blocks), RMSNorm
 // (gain: written to xn by the by == 0 blocks) and the shared-expert gate logit
 // (sgvec: by == 0 blocks, wave_sum) and the per-token input statistics (xstat:
 // by == 0 blocks) are computed as in k_router.
-template <int HB, int EB>
+template <int HB, int EB, int TPW>
 __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, const float* __restrict__ addend,
                                                   const float* __restrict__ W, const float* __restrict__ sgvec,
                                                   const float* __restrict__ gain, float eps, uint32_t T, uint32_t E,
@@ -630,10 +632,10 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
     __shared__ float4 sw[2][CH][Q];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
     constexpr uint32_t NC = EB / CH;  // chunks
-    const uint32_t t0 = blockIdx.x * 8u + 2u * wave, e0 = blockIdx.y * (uint32_t)EB;
-    float xr[2][HB * 4];
+    const uint32_t t0 = blockIdx.x * (4u * TPW) + TPW * wave, e0 = blockIdx.y * (uint32_t)EB;
+    float xr[TPW][HB * 4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < TPW; ++t) {
         const uint32_t tt = min(t0 + t, T - 1);
 #pragma unroll
         for (int i = 0; i < HB; ++i) {
@@ -641,7 +643,7 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             xr[t][4 * i] = v.x; xr[t][4 * i + 1] = v.y; xr[t][4 * i + 2] = v.z; xr[t][4 * i + 3] = v.w;
         }
     }
-    if (addend) add_residual<2, HB>(xr, addend, xs, t0, T, lane, blockIdx.y == 0);
+    if (addend) add_residual<TPW, HB>(xr, addend, xs, t0, T, lane, blockIdx.y == 0);
     if (gain) {
         float g[HB * 4];
 #pragma unroll
@@ -650,7 +652,7 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             g[4 * i] = v.x; g[4 * i + 1] = v.y; g[4 * i + 2] = v.z; g[4 * i + 3] = v.w;
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < TPW; ++t) {
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < HB * 4; ++j) ss = __builtin_fmaf(xr[t][j], xr[t][j], ss);
@@ -675,7 +677,7 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
         }
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < TPW; ++t) {
             float acc = 0.f;
 #pragma unroll
             for (int j = 0; j < HB * 4; ++j) acc = __builtin_fmaf(wv[j], xr[t][j], acc);
@@ -685,14 +687,14 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
     }
     if (xstat && blockIdx.y == 0) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) token_stats<HB>(xr[t], xstat, t0 + t, T, lane);
+        for (int t = 0; t < TPW; ++t) token_stats<HB>(xr[t], xstat, t0 + t, T, lane);
     }
     // Router rows e0 .. e0 + EB - 1 in NC chunks of 4 through LDS.
     constexpr uint32_t PER = CH * Q / 256u;  // float4 per thread per chunk
     float4 stage[PER];
-    float p[2 * EB];
+    float p[TPW * EB];
 #pragma unroll
-    for (int i = 0; i < 2 * EB; ++i) p[i] = 0.f;
+    for (int i = 0; i < TPW * EB; ++i) p[i] = 0.f;
 #pragma unroll
     for (uint32_t k = 0; k < PER; ++k) {
         const uint32_t idx = tid + 256u * k;
@@ -717,7 +719,7 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
                 wv[4 * i] = v.x; wv[4 * i + 1] = v.y; wv[4 * i + 2] = v.z; wv[4 * i + 3] = v.w;
             }
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < TPW; ++t) {
                 float acc = 0.f;
 #pragma unroll
                 for (int j = 0; j < HB * 4; ++j) acc = __builtin_fmaf(wv[j], xr[t][j], acc);
@@ -733,13 +735,14 @@ __global__ __launch_bounds__(256) void k_router_t(const float* __restrict__ x, c
             __syncthreads();
         }
     }
-    if constexpr (EB == 32) {
+    static_assert(TPW * EB == 32 || TPW * EB == 64, "32 or 64 logits per wave");
+    if constexpr (TPW * EB == 64) {
         const float v = transpose_sum64(p, lane);
-        const uint32_t t = t0 + (lane >> 5), e = e0 + (lane & 31u);
+        const uint32_t t = t0 + lane / EB, e = e0 + lane % EB;
         if (t < T) logits[(uint64_t)t * E + e] = v;
     } else {
         const float v = transpose_sum32(p, lane);
-        const uint32_t t = t0 + (lane >> 5), e = e0 + ((lane >> 1) & 15u);
+        const uint32_t t = t0 + (lane >> 1) / EB, e = e0 + (lane >> 1) % EB;
         if (t < T && (lane & 1u) == 0) logits[(uint64_t)t * E + e] = v;
     }
 }
