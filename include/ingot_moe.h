@@ -184,10 +184,11 @@ typedef struct ingot_layer_desc {
 } ingot_layer_desc;
 
 /* Copies the layer to device memory (every expert resident). A matrix in a
- * format the f16 prefill GEMM decodes (rows a multiple of 16)
- * also gets a second copy, reordered so that each of that GEMM's weight
- * loads reads one contiguous span; it doubles those matrices' device
- * memory. */
+ * format the f16 prefill GEMM decodes (rows a multiple of 16) gets a second
+ * copy at the first ingot_layer_reserve (or forward) of a batch that takes
+ * the prefill path: the same bytes reordered so that each of that GEMM's
+ * weight loads reads one contiguous span. It doubles those matrices' device
+ * memory; a layer that only decodes never makes it. */
 int ingot_layer_create(ingot_ctx* ctx, const ingot_layer_desc* desc, ingot_layer** out);
 /* A second resident copy of the same weights at new device addresses (not for
  * cached layers). */
@@ -226,8 +227,9 @@ int ingot_expert_cache_claim(ingot_expert_cache* cache, uint32_t id, const uint3
 int ingot_expert_cache_commit(ingot_expert_cache* cache, uint32_t slot, uint32_t id);
 int ingot_expert_cache_state(const ingot_expert_cache* cache, int64_t* ids, uint64_t* hits, uint64_t* misses);
 void ingot_layer_destroy(ingot_layer* layer);
-/* Reserve workspace for up to T tokens (done implicitly by forward; call it
- * before graph capture, which must not allocate). */
+/* Reserve workspace for up to T tokens, and make the prefill GEMM's weight
+ * copies when T tokens take the prefill path (done implicitly by forward;
+ * call it before graph capture, which must not allocate). */
 int ingot_layer_reserve(ingot_layer* layer, uint32_t T);
 /* out[T][H] = layer(x[T][H]); device pointers, asynchronous on the context
  * stream. d_ids [T][K] / d_weights [T][K] receive the routing when non-NULL.

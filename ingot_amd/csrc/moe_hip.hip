@@ -197,10 +197,11 @@ bool tiled_kind(const DevMatrix& m) {
     return cols_ok && m.rows % 16 == 0;
 }
 
-// m->t = m->d in the tiled layout (resident layers; the decode kernels and the
-// fp32 GEMM keep reading m->d).
+// m->t = m->d in the tiled layout (resident layers, at the first reserve of a
+// batch that takes the prefill path; the decode kernels and the fp32 GEMM
+// keep reading m->d).
 int make_tiled(ingot_ctx* ctx, DevMatrix* m) {
-    if (!m->d || !tiled_kind(*m)) return INGOT_OK;
+    if (!m->d || m->t || !tiled_kind(*m)) return INGOT_OK;
     HIP_TRY(ctx, hipMalloc(reinterpret_cast<void**>(&m->t), m->nbytes));
     const uint64_t blocks = std::min<uint64_t>((m->nbytes + 255) / 256, 1u << 20);
     hipLaunchKernelGGL(k_tile_weights, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, m->d, m->t, m->nbytes,
@@ -587,6 +588,7 @@ struct ingot_layer {
     uint32_t gemm_mode = INGOT_GEMM_AUTO;
     float *router = nullptr, *bias = nullptr, *sgvec = nullptr, *gain = nullptr;
     DevMatrix gate, up, down, sgate, sup, sdown;
+    bool tiled = false;  // the tiled copies (DevMatrix::t) are made
     // the layer's own workspace, for up to cap_T tokens
     uint32_t cap_T = 0;
     void* ws = nullptr;
@@ -659,8 +661,38 @@ static uint64_t carve(const ingot_layer* L, uint32_t T, void* base, Ws* out) {
     return off;
 }
 
+// Pairs up to this count take the GEMV (decode) kernels; more take the
+// dispatch + grouped MFMA GEMM (prefill) kernels.
+static const uint32_t GEMV_MAX_PAIRS = 64;
+
+// Whether a forward of T tokens takes the decode kernels (else routing,
+// dispatch and the grouped GEMMs). A cached layer reads the routing back to
+// the host before its expert products, so it always takes the GEMM path.
+static bool takes_decode(const ingot_layer* L, uint32_t T) {
+    const uint32_t K = L->K, F = L->F, SF = L->SF, P = T * K;
+    const bool hs = L->has_shared;
+    const int ks = hs ? (int)L->sdown.kind : -1;
+    const bool fuse_shared = hs && can_fuse_shared(L->down.kind, ks);
+    const uint32_t nv = K * (F / 32) + (fuse_shared ? SF / 32 : 0);
+    return !L->cached && P <= GEMV_MAX_PAIRS && K <= 2 * GU_WAVES && (uint64_t)K * F + (hs ? SF : 0) <= DOWN_LDS_FLOATS &&
+           (nv + 63) / 64 <= 8 && (!hs || fuse_shared || (SF / 32 + 63) / 64 <= 2) && L->H <= 4096;
+}
+
 static int reserve(ingot_layer* L, uint32_t T) {
     ingot_ctx* ctx = L->ctx;
+    // The f16 GEMM's tiled weight copies, made by the first reserve (or
+    // forward) of a batch that takes the prefill path: a layer that only
+    // decodes never holds them. Until they exist (and under graph capture,
+    // which cannot allocate) the GEMM reads GGUF order.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (!L->cached && !L->tiled && cs == hipStreamCaptureStatusNone && !takes_decode(L, T)) {
+        for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) {
+            const int st = make_tiled(ctx, m);
+            if (st != INGOT_OK) return st;
+        }
+        L->tiled = true;
+    }
     if (T <= L->cap_T) return INGOT_OK;
     const uint64_t total = carve(L, T, nullptr, nullptr);
     void* ws = nullptr;
@@ -1044,9 +1076,6 @@ static int create_layer(ingot_ctx* ctx, const ingot_layer_desc* d, uint32_t slot
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_gate, &L->sgate);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_up, &L->sup);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_down, &L->sdown);
-    if (slots == 0)
-        for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown})
-            if (st == INGOT_OK) st = make_tiled(ctx, m);
     if (st != INGOT_OK) {
         free_dev(L);
         delete L;
@@ -1113,6 +1142,7 @@ int ingot_layer_clone(const ingot_layer* src, ingot_layer** out) {
     L->has_shared = src->has_shared; L->has_sgvec = src->has_sgvec; L->has_norm = src->has_norm;
     L->has_bias = src->has_bias;
     L->gemm_mode = src->gemm_mode;
+    L->tiled = src->tiled;
     auto dup = [&](const void* s, uint64_t bytes, void** dst) -> int {
         if (!s) return INGOT_OK;
         HIP_TRY(ctx, hipMalloc(dst, bytes));
@@ -1168,9 +1198,6 @@ int ingot_layer_reserve(ingot_layer* L, uint32_t T) {
     return reserve(L, T);
 }
 
-// Pairs up to this count take the GEMV (decode) kernels; more take the
-// dispatch + grouped MFMA GEMM (prefill) kernels.
-static const uint32_t GEMV_MAX_PAIRS = 64;
 
 // The f16 GEMM addresses its A operands (x split: T rows of H; act split: P + T
 // rows of F) and their group sums with 32-bit byte offsets.
@@ -1302,11 +1329,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
     const bool hs_ = L->has_shared;
     const int ks_ = hs_ ? (int)L->sdown.kind : -1;
     const bool fuse_shared = hs_ && can_fuse_shared(L->down.kind, ks_);
-    const uint32_t nv_ = K * (F / 32) + (fuse_shared ? SF / 32 : 0);
-    // A cached layer reads the routing back to the host before its expert
-    // products, so it always takes the route / dispatch / grouped GEMM path.
-    const bool decode = !L->cached && P <= GEMV_MAX_PAIRS && K <= 2 * GU_WAVES && (uint64_t)K * F + (hs_ ? SF : 0) <= DOWN_LDS_FLOATS &&
-                        (nv_ + 63) / 64 <= 8 && (!hs_ || fuse_shared || (SF / 32 + 63) / 64 <= 2) && H <= 4096;
+    const bool decode = takes_decode(L, T);
     uint32_t* flags = ctx->d_flags;
     float* xstat = w.xstat;
 

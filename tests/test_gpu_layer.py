@@ -446,6 +446,27 @@ def test_decode_route_many_experts_ties(gpu, oracle, E, K):
     layer.destroy()
 
 
+def test_tiled_copies_made_for_prefill_only(gpu, oracle):
+    """The prefill GEMM's tiled weight copies appear at the first batch that
+    takes the prefill path (never for decode), travel with clones, and leave
+    the outputs as they were."""
+    spec = small_layer(Q4_K, Q4_K)
+    layer = MoeLayer(gpu, spec)
+    gguf = layer.weight_bytes()
+    x1, x40 = CF.inputs(16, 1, 2048), CF.inputs(16, 40, 2048)
+    out1, _, _ = check_layer(layer, spec, x1, oracle, "decode before any prefill")
+    assert layer.weight_bytes() == gguf
+    check_layer(layer, spec, x40, oracle, "first prefill")
+    routed = sum(m.data.nbytes for m in (spec.gate, spec.up, spec.down))
+    assert layer.weight_bytes() == gguf + routed
+    assert np.array_equal(layer(x1)[0], out1)
+    clone = layer.clone()
+    assert clone.weight_bytes() == layer.weight_bytes()
+    assert np.array_equal(clone(x40)[0], layer(x40)[0])
+    clone.destroy()
+    layer.destroy()
+
+
 # ----------------------------------------------------------- errors, graphs
 def test_nonfinite_input_rejected(gpu):
     spec = small_layer(Q4_K, Q4_K)
