@@ -126,7 +126,53 @@ bool launch_dec_down_k(hipStream_t s, uint32_t vpl, dim3 grid, const DownArgs& a
 #undef DD
 }
 
+template <int KIND, bool GATEUP>
+bool launch_gemm_f16_k(hipStream_t s, int aord, bool tt128, bool tl, dim3 grid, const GemmF16Args& a) {
+    // Q4_K and Q5_K have both tile sizes, Q6_K only TT 128, the others only TT 64.
+    constexpr bool T128 = KIND == 12 || KIND == 13 || KIND == 14, T64 = KIND != 14;
+#define F16L(AO, TT, TLV)                                                                                        \
+    hipLaunchKernelGGL((k_gemm_f16<KIND, GATEUP, AO, TT, TLV>), grid, dim3(2 * TT), 0, s, a.w0, a.w1, a.ws0,     \
+                       a.ws1, a.e_shared, a.stride0, a.stride1, a.rows_per_expert, a.kdim, a.ah, a.al, a.gs,     \
+                       a.pairs, a.K, a.tiles, a.ldo, a.limit, a.out, a.out_h, a.out_l, a.out_gs, a.nblk,        \
+                       a.a_rows, a.xstat, a.rowmax, a.flags, a.slot_of)
+#define F16T(AO, TT)                    \
+    do {                                \
+        if (tl) F16L(AO, TT, true);     \
+        else F16L(AO, TT, false);       \
+        return true;                    \
+    } while (0)
+#define F16A(TT)                                  \
+    do {                                          \
+        if constexpr (GATEUP) {                   \
+            switch (aord) {                       \
+                case A_IQ4NL: F16T(A_IQ4NL, TT);  \
+                case A_IQ3XXS: F16T(A_IQ3XXS, TT); \
+                case A_Q6K: F16T(A_Q6K, TT);      \
+                case A_F32: F16T(A_F32, TT);      \
+                default: F16T(A_NATURAL, TT);     \
+            }                                     \
+        } else {                                  \
+            F16T(A_NATURAL, TT);                  \
+        }                                         \
+    } while (0)
+    if (tt128 || !T64) {
+        if constexpr (T128) F16A(128);
+        return false;
+    }
+    if constexpr (T64) F16A(64);
+    return false;
+#undef F16A
+#undef F16T
+#undef F16L
+}
+
 }  // namespace ingot
+
+#define INGOT_INSTANTIATE_F16(K)                                                                          \
+    namespace ingot {                                                                                     \
+    template bool launch_gemm_f16_k<K, true>(hipStream_t, int, bool, bool, dim3, const GemmF16Args&);  \
+    template bool launch_gemm_f16_k<K, false>(hipStream_t, int, bool, bool, dim3, const GemmF16Args&); \
+    }
 
 #define INGOT_INSTANTIATE_KIND(K)                                                                                \
     namespace ingot {                                                                                            \

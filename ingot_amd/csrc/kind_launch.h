@@ -105,6 +105,39 @@ bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32
                                 const DecGateUpArgs& a, const uint8_t* sg, const uint8_t* su, uint64_t sgs,
                                 uint64_t sus, float* sact);
 
+// Arguments of k_gemm_f16 (its parameters, in order).
+struct GemmF16Args {
+    const uint8_t *w0, *w1, *ws0, *ws1;
+    uint32_t e_shared;
+    uint64_t stride0, stride1;
+    uint32_t rows_per_expert, kdim;
+    const _Float16 *ah, *al;
+    const float* gs;
+    const uint32_t* pairs;
+    uint32_t K;
+    const uint32_t* tiles;
+    uint32_t ldo;
+    float limit;
+    float* out;
+    _Float16 *out_h, *out_l;
+    float* out_gs;
+    uint32_t nblk, a_rows;
+    const float* xstat;
+    uint32_t* rowmax;
+    uint32_t* flags;
+    const uint32_t* slot_of;
+};
+// The formats of the f16 grouped GEMM.
+#define INGOT_F16_KINDS(X) X(12) X(13) X(14) X(17) X(18) X(20) X(21) X(22) X(23)
+// k_gemm_f16<KIND, GATEUP, aord, TT, tl>: TT 128 when tt128 (Q4_K, Q5_K; Q6_K
+// always), else 64; false if no instantiation covers the arguments.
+template <int KIND, bool GATEUP>
+bool launch_gemm_f16_k(hipStream_t s, int aord, bool tt128, bool tl, dim3 grid, const GemmF16Args& a);
+
+#define INGOT_DECLARE_F16(K)                                                                                \
+    extern template bool launch_gemm_f16_k<K, true>(hipStream_t, int, bool, bool, dim3, const GemmF16Args&); \
+    extern template bool launch_gemm_f16_k<K, false>(hipStream_t, int, bool, bool, dim3, const GemmF16Args&);
+
 #define INGOT_DECLARE_KIND(K)                                                                               \
     extern template bool launch_gemv_gate_up_k<K>(hipStream_t, uint32_t, uint32_t, dim3, const GateUpArgs&); \
     extern template bool launch_shared_add_k<K>(hipStream_t, uint32_t, dim3, const uint8_t*, uint64_t,      \
@@ -127,5 +160,6 @@ INGOT_FUSED_DOWN(INGOT_DECLARE_FUSED)
                                                             uint64_t, uint64_t, float*);
 INGOT_FUSED_GATE_UP(INGOT_DECLARE_FUSED_GU)
 #undef INGOT_DECLARE_FUSED_GU
+INGOT_F16_KINDS(INGOT_DECLARE_F16)
 
 }  // namespace ingot

@@ -3,3 +3,4 @@
 
 INGOT_INSTANTIATE_KIND(12)
 INGOT_INSTANTIATE_FUSED(12, 12)
+INGOT_INSTANTIATE_F16(12)

@@ -360,70 +360,17 @@ bool f16_tt128_kind(uint32_t kind) { return kind == 12 || kind == 13 || kind == 
 
 // gate/up: `kind` its weights, `aord` the order it writes act in (the down
 // projection's a_order); tt128: tiles of up to 128 tokens (f16_tt128_kind).
-// tl: the weights are the tiled copies (tiled_kind).
+// tl: the weights are the tiled copies (tiled_kind). The kernels are
+// instantiated per format in the kinds_*.hip units (launch_gemm_f16_k).
 template <bool GATEUP, typename... Args>
 bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, bool tl, dim3 grid, Args... args) {
-#define F16(KV, AO, TT)                                                                                      \
-    do {                                                                                                     \
-        if (tl) {                                                                                            \
-            hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT, true>), grid, dim3(2 * TT), 0, s, args...);   \
-            break;                                                                                           \
-        }                                                                                                    \
-        hipLaunchKernelGGL((k_gemm_f16<KV, GATEUP, AO, TT>), grid, dim3(2 * TT), 0, s, args...);             \
-    } while (0)
-#define F16_GU(KV, TT)                                          \
-    switch (aord) {                                             \
-        case A_IQ4NL: F16(KV, A_IQ4NL, TT); return true;        \
-        case A_IQ3XXS: F16(KV, A_IQ3XXS, TT); return true;      \
-        case A_Q6K: F16(KV, A_Q6K, TT); return true;            \
-        case A_F32: F16(KV, A_F32, TT); return true;            \
-        default: F16(KV, A_NATURAL, TT); return true;           \
+    const GemmF16Args a{args...};
+    switch (kind) {
+#define K_(KV) case KV: return launch_gemm_f16_k<KV, GATEUP>(s, aord, tt128, tl, grid, a);
+        INGOT_F16_KINDS(K_)
+#undef K_
+        default: return false;
     }
-    if constexpr (GATEUP) {
-        if (tt128) {
-            switch (kind) {
-                case 12: F16_GU(12, 128)
-                case 13: F16_GU(13, 128)
-                case 14: F16_GU(14, 128)
-                default: return false;
-            }
-        }
-        switch (kind) {
-            case 12: F16_GU(12, 64)
-            case 13: F16_GU(13, 64)
-            case 14: F16_GU(14, 128)
-            case 17: F16_GU(17, 64)
-            case 18: F16_GU(18, 64)
-            case 20: F16_GU(20, 64)
-            case 21: F16_GU(21, 64)
-            case 22: F16_GU(22, 64)
-            case 23: F16_GU(23, 64)
-            default: return false;
-        }
-    } else {
-        if (tt128) {
-            switch (kind) {
-                case 12: F16(12, A_NATURAL, 128); return true;
-                case 13: F16(13, A_NATURAL, 128); return true;
-                case 14: F16(14, A_NATURAL, 128); return true;
-                default: return false;
-            }
-        }
-        switch (kind) {
-            case 12: F16(12, A_NATURAL, 64); return true;
-            case 13: F16(13, A_NATURAL, 64); return true;
-            case 14: F16(14, A_NATURAL, 128); return true;
-            case 17: F16(17, A_NATURAL, 64); return true;
-            case 18: F16(18, A_NATURAL, 64); return true;
-            case 20: F16(20, A_NATURAL, 64); return true;
-            case 21: F16(21, A_NATURAL, 64); return true;
-            case 22: F16(22, A_NATURAL, 64); return true;
-            case 23: F16(23, A_NATURAL, 64); return true;
-            default: return false;
-        }
-    }
-#undef F16_GU
-#undef F16
 }
 
 }  // namespace
