@@ -202,7 +202,12 @@ bool tiled_kind(const DevMatrix& m) {
 // keep reading m->d).
 int make_tiled(ingot_ctx* ctx, DevMatrix* m) {
     if (!m->d || m->t || !tiled_kind(*m)) return INGOT_OK;
-    HIP_TRY(ctx, hipMalloc(reinterpret_cast<void**>(&m->t), m->nbytes));
+    // The copy is optional: without room for it the GEMM keeps reading GGUF order.
+    if (hipMalloc(reinterpret_cast<void**>(&m->t), m->nbytes) != hipSuccess) {
+        (void)hipGetLastError();
+        m->t = nullptr;
+        return INGOT_OK;
+    }
     const uint64_t blocks = std::min<uint64_t>((m->nbytes + 255) / 256, 1u << 20);
     hipLaunchKernelGGL(k_tile_weights, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, m->d, m->t, m->nbytes,
                        m->kind, m->stride);
