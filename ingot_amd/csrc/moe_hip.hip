@@ -236,7 +236,8 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
                    float* logits, float* sgl, float* xn, float* xs, float* xstat) {
     const uint32_t rows = E + (has_sg ? 1u : 0u);
     // Below 64 tokens one token and one router row per wave keeps the grid
-    // wide (T x E / 4 blocks); from 64 tokens the 64-output transposed kernel.
+    // wide (T x E / 4 blocks); from 64 tokens the transposed kernel (H of
+    // 1024 or 2048).
     const bool decode = T < 64;
     if (!decode && E % 32u == 0 && (HB == 4 || HB == 8)) {
         // 4 tokens per wave (16 per block); 16 experts per block when that
