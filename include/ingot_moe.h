@@ -122,9 +122,14 @@ const char* ingot_status_string(int status);
 /* 1 if the kernels decode `kind`, else 0. */
 int ingot_kind_supported(uint32_t kind);
 
-/* ---- context ---- */
+/* ---- context ----
+ * Lifetime: every layer created on a context (ingot_layer_create, _clone,
+ * _create_cached) holds a pointer to it and must be destroyed before it.
+ * ingot_ctx_destroy refuses, with INGOT_INVALID and the context left intact,
+ * while layers are alive on it (the reference gets the same order from
+ * ownership: Gpu owns its buffers, src/metal.rs:46-63). */
 int ingot_ctx_create(int device, ingot_ctx** out);
-void ingot_ctx_destroy(ingot_ctx* ctx);
+int ingot_ctx_destroy(ingot_ctx* ctx);
 const char* ingot_last_error(const ingot_ctx* ctx);
 /* Launch on a caller-owned hipStream_t (NULL: the context's own stream). */
 int ingot_ctx_set_stream(ingot_ctx* ctx, void* hip_stream);
@@ -155,12 +160,25 @@ int ingot_moe(ingot_ctx* ctx, const ingot_matrix routed[3], const ingot_matrix* 
  * ingot_ctx_check_device_flags). */
 int ingot_route_batch(ingot_ctx* ctx, const float* d_logits, const float* d_bias, uint32_t T, uint32_t E,
                       uint32_t K, uint32_t routing, float scale, uint32_t* d_ids, float* d_weights);
-/* Synchronizes, reads and clears the device flags; INGOT_NONFINITE if a
- * kernel met a non-finite router logit since the last check, else INGOT_RANGE
- * if a prefill forward's activations left the split-f16 range, else
- * INGOT_NONFINITE if a layer forward wrote a non-finite output value (the
- * device-side form of the reference's read-back check, src/metal.rs:1575-1577). */
+/* Synchronizes, reads and clears the device flags of the context and of every
+ * layer on it. Each layer's kernels raise flags in a word of its own; the
+ * check records per layer what its forwards raised (ingot_layer_flag_status)
+ * and returns the status of the earliest-created flagged layer (else of the
+ * context's own ingot_route_batch calls), its message naming that layer:
+ * INGOT_NONFINITE if a kernel met a non-finite router logit since the last
+ * check, else INGOT_RANGE if a prefill forward's activations left the
+ * split-f16 range, else INGOT_NONFINITE if a layer forward wrote a non-finite
+ * output value (the device-side form of the reference's read-back check,
+ * src/metal.rs:1575-1577). An engine with several layers in one graph
+ * recomputes from the first flagged layer of its stack onward (later layers
+ * may be flagged only because their input came from it) instead of the whole
+ * stack. */
 int ingot_ctx_check_device_flags(ingot_ctx* ctx);
+/* What the layer's own forwards raised before the last
+ * ingot_ctx_check_device_flags (INGOT_OK, INGOT_NONFINITE or INGOT_RANGE; the
+ * reference fails the one command whose output is non-finite,
+ * src/metal.rs:1575-1577). */
+int ingot_layer_flag_status(const ingot_layer* layer);
 
 /* ---- resident layer ---- */
 typedef struct ingot_layer_desc {
@@ -287,11 +305,14 @@ void ingot_graph_destroy(ingot_graph* g);
 int ingot_graph_time(ingot_ctx* ctx, ingot_graph* g, uint32_t launches, float* ms);
 
 /* Kernel-level timing for roofline reporting: captures `reps` replays of one
- * stage of the last forward of `layer` (same inputs) in a HIP graph, launches
- * it once to warm up, then times one launch between HIP events on the context
- * stream and returns the mean milliseconds per stage launch.
+ * stage of the last forward of `layer` (same inputs, which must still be
+ * allocated) in a HIP graph, launches it once to warm up, then times one
+ * launch between HIP events on the context stream and returns the mean
+ * milliseconds per stage launch.
  * stage: 0 router, 1 route, 2 gate/up, 3 down (+combine at decode), 4 combine,
- * 5 dispatch. Returns INGOT_INVALID if the stage did not run in that forward. */
+ * 5 dispatch. Returns INGOT_INVALID if the stage did not run in that forward,
+ * if a reserve has reallocated the workspace since, and for cached layers
+ * (their GEMM stages exist only inside a forward's expert passes). */
 int ingot_layer_time_stage(ingot_layer* layer, uint32_t stage, uint32_t reps, float* ms);
 /* The same over n layers (resident copies) replayed round-robin, so that
  * consecutive launches read weights at different addresses. */
@@ -299,7 +320,8 @@ int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t sta
 /* Name of the HIP kernel that implements `stage` in the last forward. */
 const char* ingot_layer_stage_kernel(const ingot_layer* layer, uint32_t stage);
 /* The prefill dispatch of the last forward (synchronizes; INGOT_INVALID if that
- * forward ran the decode kernels), P = T * K pairs: counts[E] and first[E]
+ * forward ran the decode kernels, was a static forward, or a reserve has
+ * reallocated the workspace since), P = T * K pairs: counts[E] and first[E]
  * (expert_layout), pairs[P + S] (expert_pairs; S = T when the shared expert ran
  * in the same GEMM launches, its rows P + t naming token t as t K, else 0),
  * inverse[P], tiles[min(tiles_cap, info[2])][4] = {expert (E: the shared
@@ -318,11 +340,20 @@ int ingot_malloc(ingot_ctx* ctx, uint64_t bytes, void** d_ptr);
 int ingot_free(ingot_ctx* ctx, void* d_ptr);
 int ingot_memcpy_h2d(ingot_ctx* ctx, void* d_dst, const void* h_src, uint64_t bytes);
 int ingot_memcpy_d2h(ingot_ctx* ctx, void* h_dst, const void* d_src, uint64_t bytes);
+/* Free and total device memory of the context's GPU (hipMemGetInfo). */
+int ingot_device_mem_info(ingot_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes);
 /* Device-to-device copy by a plain streaming HIP kernel (16 bytes per lane,
  * bytes a multiple of 16). No counterpart in the reference: it is the known-size
  * workload against which hardware byte counters (FETCH_SIZE, WRITE_SIZE) are
  * calibrated. */
 int ingot_device_copy(ingot_ctx* ctx, void* d_dst, const void* d_src, uint64_t bytes);
+/* Streaming read of `bytes` (a multiple of 16) at d_src by a plain HIP kernel,
+ * asynchronous on the context stream (graph-capturable); d_sink must hold
+ * max(1, ceil(bytes / 16384)) words, which the kernel almost never writes.
+ * bytes == 0 launches an empty kernel. No counterpart in the reference's MoE
+ * path: it is the floor of a decode stage reading the same bytes from HBM,
+ * like the reference's STREAM bench (src/expert_bench.rs:203-290). */
+int ingot_device_read(ingot_ctx* ctx, const void* d_src, uint64_t bytes, uint32_t* d_sink);
 
 #ifdef __cplusplus
 }

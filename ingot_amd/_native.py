@@ -75,7 +75,7 @@ MOE_SYMBOLS = {
     "ingot_status_string": (C.c_char_p, [I32]),
     "ingot_kind_supported": (I32, [U32]),
     "ingot_ctx_create": (I32, [I32, C.POINTER(P)]),
-    "ingot_ctx_destroy": (None, [P]),
+    "ingot_ctx_destroy": (I32, [P]),
     "ingot_last_error": (C.c_char_p, [P]),
     "ingot_ctx_set_stream": (I32, [P, P]),
     "ingot_ctx_stream": (P, [P]),
@@ -87,6 +87,7 @@ MOE_SYMBOLS = {
     "ingot_moe": (I32, [P, C.POINTER(Matrix_t), C.POINTER(Matrix_t), C.POINTER(Matrix_t), P, P, U32, P]),
     "ingot_route_batch": (I32, [P, P, P, U32, U32, U32, U32, F32, P, P]),
     "ingot_ctx_check_device_flags": (I32, [P]),
+    "ingot_layer_flag_status": (I32, [P]),
     "ingot_layer_create": (I32, [P, C.POINTER(LayerDesc_t), C.POINTER(P)]),
     "ingot_layer_clone": (I32, [P, C.POINTER(P)]),
     "ingot_layer_create_cached": (I32, [P, C.POINTER(LayerDesc_t), U32, C.POINTER(P)]),
@@ -118,7 +119,9 @@ MOE_SYMBOLS = {
     "ingot_free": (I32, [P, P]),
     "ingot_memcpy_h2d": (I32, [P, P, P, U64]),
     "ingot_memcpy_d2h": (I32, [P, P, P, U64]),
+    "ingot_device_mem_info": (I32, [P, C.POINTER(U64), C.POINTER(U64)]),
     "ingot_device_copy": (I32, [P, P, P, U64]),
+    "ingot_device_read": (I32, [P, P, U64, P]),
 }
 
 SYNTH_SYMBOLS = {

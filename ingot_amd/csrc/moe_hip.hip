@@ -19,6 +19,11 @@
 
 using namespace ingot;
 
+// Device flag words of a context: word 0 belongs to the context's own calls
+// (ingot_route, ingot_route_batch), word i >= 1 to the layer attached to slot
+// i, so that a check can name the layer whose kernels raised a flag.
+constexpr uint32_t FLAG_WORDS = 1024;
+
 struct ingot_ctx {
     int device = 0;
     hipStream_t own = nullptr;
@@ -26,9 +31,12 @@ struct ingot_ctx {
     bool poisoned = false;
     std::string err;
     std::string name;
-    uint32_t* d_flags = nullptr;
+    uint32_t* d_flags = nullptr;  // FLAG_WORDS words
     void* scratch = nullptr;  // this device's copy of `scratch` (hipGetSymbolAddress)
     hipStream_t copy = nullptr;  // cached layers' expert copies (created with the first one)
+    std::vector<ingot_layer*> slot{nullptr};  // slot[i]: the live layer owning flag word i (slot 0 unused)
+    uint32_t live = 0;                         // live layers on this context
+    uint32_t next_seq = 0;                     // creation number of the next layer
 };
 
 // Workspace of the allocation-free forward (ingot_layer_forward_static): one
@@ -561,11 +569,43 @@ struct ingot_layer {
         const uint32_t* slot_of = nullptr;
         bool first = true;
     } pass;
-    // the dispatch buffers of the last prefill forward (ingot_layer_dispatch_debug)
+    // the dispatch buffers of the last prefill forward (ingot_layer_dispatch_debug);
+    // last_static: that forward used the shared static array
     uint32_t last_T = 0, last_P = 0, last_S = 0, last_cap = 0, last_tm = 0;
-    bool last_prefill = false;
+    bool last_prefill = false, last_static = false;
     Ws last;
+    // flag word ctx->d_flags[slot]; seq: creation number on the context;
+    // flag_status: what its kernels raised before the last flag check
+    uint32_t slot = 0, seq = 0;
+    int flag_status = INGOT_OK;
 };
+
+// The layer's device flag word.
+static uint32_t* layer_flags(const ingot_layer* L) { return L->ctx->d_flags + L->slot; }
+
+// Gives L a flag word (the lowest free slot) and its creation number.
+static int attach(ingot_ctx* ctx, ingot_layer* L) {
+    uint32_t i = 1;
+    while (i < ctx->slot.size() && ctx->slot[i]) ++i;
+    if (i >= FLAG_WORDS) return fail(ctx, INGOT_UNSUPPORTED, "more than 1023 live layers on one context");
+    if (i == ctx->slot.size()) ctx->slot.push_back(nullptr);
+    ctx->slot[i] = L;
+    L->slot = i;
+    L->seq = ctx->next_seq++;
+    ++ctx->live;
+    return INGOT_OK;
+}
+
+// Releases L's flag word, cleared so that the next layer in the slot starts clean.
+static void detach(ingot_layer* L) {
+    ingot_ctx* ctx = L->ctx;
+    if (!L->slot || L->slot >= ctx->slot.size() || ctx->slot[L->slot] != L) return;
+    const uint32_t zero = 0;
+    (void)hipMemcpy(layer_flags(L), &zero, 4, hipMemcpyHostToDevice);
+    ctx->slot[L->slot] = nullptr;
+    L->slot = 0;
+    --ctx->live;
+}
 
 static void free_dev(ingot_layer* L) {
     for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) {
@@ -633,32 +673,71 @@ static bool takes_decode(const ingot_layer* L, uint32_t T) {
            (nv + 63) / 64 <= 8 && (!hs || fuse_shared || (SF / 32 + 63) / 64 <= 2) && L->H <= 4096;
 }
 
+// The f16 GEMM addresses its A operands (x split: T rows of H; act split: P + T
+// rows of F) and their group sums with 32-bit byte offsets.
+static bool f16_gemm_fits(uint64_t kdim, uint64_t rows) { return 2ull * kdim * rows < (1ull << 32); }
+
+// Which prefill GEMMs a batch of T tokens runs. f16gu: gate/up on the f16 GEMM
+// (both projections' formats allow it, or only gate/up's, which then writes
+// fp32 act for the fp32 down GEMM); f16: down too; merge: the shared expert
+// joins the same launches (its formats and width equal the routed experts').
+struct PrefillPlan {
+    bool f16gu = false, f16 = false, merge = false;
+};
+
+static PrefillPlan prefill_plan(const ingot_layer* L, uint32_t T) {
+    PrefillPlan p;
+    const uint64_t P = (uint64_t)T * L->K, PS = P + (L->has_shared ? T : 0u);
+    p.f16gu = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(L->gate.kind, L->H, true) && f16_gemm_fits(L->H, T) &&
+              f16_gemm_fits(L->F, PS);
+    p.f16 = p.f16gu && f16_gemm_kind(L->down.kind, L->F, false);
+    p.merge = p.f16 && L->has_shared && L->SF == L->F && L->sgate.kind == L->gate.kind &&
+              L->sup.kind == L->up.kind && L->sdown.kind == L->down.kind && L->sgate.stride == L->gate.stride &&
+              L->sup.stride == L->up.stride && L->sdown.stride == L->down.stride;
+    return p;
+}
+
 static int reserve(ingot_layer* L, uint32_t T) {
     ingot_ctx* ctx = L->ctx;
+    // The workspace first: it is required, the tiled copies below are not.
+    if (T > L->cap_T) {
+        const uint64_t total = carve(L, T, nullptr, nullptr);
+        void* ws = nullptr;
+        if (L->ws) (void)hipFree(L->ws);
+        L->ws = nullptr;
+        L->cap_T = 0;
+        L->w = Ws();
+        // the last forward's dispatch buffers and stage closures pointed into the freed block
+        if (!L->last_static) {
+            L->last_prefill = false;
+            for (auto& f : L->stage) f = nullptr;
+        }
+        HIP_TRY(ctx, hipMalloc(&ws, total));
+        L->ws = ws;
+        carve(L, T, ws, &L->w);
+        L->cap_T = T;
+    }
     // The f16 GEMM's tiled weight copies, made by the first reserve (or
-    // forward) of a batch that takes the prefill path: a layer that only
-    // decodes never holds them. Until they exist (and under graph capture,
-    // which cannot allocate) the GEMM reads GGUF order.
+    // forward) of a batch that runs that GEMM, only for the matrices it reads
+    // at this batch size: a layer that only decodes, or runs the fp32 GEMM,
+    // never holds them. Until they exist (and under graph capture, which
+    // cannot allocate) the GEMM reads GGUF order; a copy without room is
+    // skipped (make_tiled), and the GEMM then reads that matrix in GGUF order.
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIP_TRY(ctx, hipStreamIsCapturing(ctx->stream, &cs));
     if (!L->cached && !L->tiled && cs == hipStreamCaptureStatusNone && !takes_decode(L, T)) {
-        for (DevMatrix* m : {&L->gate, &L->up, &L->down, &L->sgate, &L->sup, &L->sdown}) {
-            const int st = make_tiled(ctx, m);
-            if (st != INGOT_OK) return st;
+        const PrefillPlan p = prefill_plan(L, T);
+        if (p.f16gu) {
+            std::vector<DevMatrix*> ms{&L->gate, &L->up};
+            if (p.f16) ms.push_back(&L->down);
+            if (p.merge) ms.insert(ms.end(), {&L->sgate, &L->sup, &L->sdown});
+            for (DevMatrix* m : ms) {
+                const int st = make_tiled(ctx, m);
+                if (st != INGOT_OK) return st;
+            }
+            L->tiled = true;
         }
-        L->tiled = true;
     }
-    if (T <= L->cap_T) return INGOT_OK;
-    const uint64_t total = carve(L, T, nullptr, nullptr);
-    void* ws = nullptr;
-    if (L->ws) (void)hipFree(L->ws);
-    L->ws = nullptr;
-    L->cap_T = 0;
-    L->w = Ws();
-    HIP_TRY(ctx, hipMalloc(&ws, total));
-    L->ws = ws;
-    carve(L, T, ws, &L->w);
-    L->cap_T = T;
     return INGOT_OK;
 }
 
@@ -704,8 +783,8 @@ int ingot_ctx_create(int device, ingot_ctx** out) {
     ctx->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
     if (bad(hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking))) return INGOT_DEVICE;
     ctx->stream = ctx->own;
-    if (bad(hipMalloc(&ctx->d_flags, 256))) return INGOT_DEVICE;
-    if (bad(hipMemset(ctx->d_flags, 0, 256))) return INGOT_DEVICE;
+    if (bad(hipMalloc(&ctx->d_flags, 4ull * FLAG_WORDS))) return INGOT_DEVICE;
+    if (bad(hipMemset(ctx->d_flags, 0, 4ull * FLAG_WORDS))) return INGOT_DEVICE;
     void* sp = nullptr;
     if (bad(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch))) || !sp) return INGOT_DEVICE;
     ctx->scratch = sp;
@@ -713,8 +792,13 @@ int ingot_ctx_create(int device, ingot_ctx** out) {
     return INGOT_OK;
 }
 
-void ingot_ctx_destroy(ingot_ctx* ctx) {
-    if (!ctx) return;
+int ingot_ctx_destroy(ingot_ctx* ctx) {
+    if (!ctx) return INGOT_INVALID;
+    // A layer keeps a pointer to its context (stream, flags): destroying the
+    // context under it would leave the layer's later calls on freed memory.
+    if (ctx->live)
+        return fail(ctx, INGOT_INVALID,
+                    std::to_string(ctx->live) + " layer(s) still alive on this context: destroy them first");
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->copy) {
@@ -724,6 +808,7 @@ void ingot_ctx_destroy(ingot_ctx* ctx) {
     if (ctx->d_flags) (void)hipFree(ctx->d_flags);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
+    return INGOT_OK;
 }
 
 const char* ingot_last_error(const ingot_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
@@ -743,17 +828,58 @@ int ingot_ctx_synchronize(ingot_ctx* ctx) {
 
 const char* ingot_device_name(ingot_ctx* ctx) { return ctx ? ctx->name.c_str() : ""; }
 
+// The status a set of flag bits reports, most severe first.
+static int flag_status(uint32_t f) {
+    if (f & FLAG_NONFINITE) return INGOT_NONFINITE;
+    if (f & FLAG_RANGE) return INGOT_RANGE;
+    if (f & FLAG_OUT_NONFINITE) return INGOT_NONFINITE;
+    return INGOT_OK;
+}
+
 int ingot_ctx_check_device_flags(ingot_ctx* ctx) {
     CHECK_CTX(ctx);
-    uint32_t flags = 0, zero = 0;
+    const uint32_t n = (uint32_t)ctx->slot.size();
+    std::vector<uint32_t> f(n, 0u);
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    HIP_TRY(ctx, hipMemcpy(&flags, ctx->d_flags, 4, hipMemcpyDeviceToHost));
-    HIP_TRY(ctx, hipMemcpy(ctx->d_flags, &zero, 4, hipMemcpyHostToDevice));
-    if (flags & FLAG_NONFINITE) return fail(ctx, INGOT_NONFINITE, "non-finite router logits");
-    if (flags & FLAG_RANGE)
-        return fail(ctx, INGOT_RANGE,
-                    "prefill activations outside the range of the split-f16 GEMM: re-run with INGOT_GEMM_FP32");
-    if (flags & FLAG_OUT_NONFINITE) return fail(ctx, INGOT_NONFINITE, "layer output contains non-finite values");
+    HIP_TRY(ctx, hipMemcpy(f.data(), ctx->d_flags, 4ull * n, hipMemcpyDeviceToHost));
+    HIP_TRY(ctx, hipMemset(ctx->d_flags, 0, 4ull * n));
+    // Each layer keeps what its own kernels raised. The status returned is
+    // that of the earliest-created flagged layer (in a stack built in order,
+    // the root cause: a later layer may only have inherited its bad input),
+    // else that of the context's own calls.
+    uint32_t nflagged = 0, fl = f[0];
+    const ingot_layer* first = nullptr;
+    for (uint32_t i = 1; i < n; ++i) {
+        ingot_layer* L = ctx->slot[i];
+        if (!L) continue;
+        L->flag_status = flag_status(f[i]);
+        if (f[i]) {
+            ++nflagged;
+            if (!first || L->seq < first->seq) {
+                first = L;
+                fl = f[i];
+            }
+        }
+    }
+    const int st = flag_status(fl);
+    if (st == INGOT_OK) return INGOT_OK;
+    std::string msg = (fl & FLAG_NONFINITE) ? "non-finite router logits"
+                      : (fl & FLAG_RANGE)
+                          ? "prefill activations outside the range of the split-f16 GEMM: re-run with INGOT_GEMM_FP32"
+                          : "layer output contains non-finite values";
+    if (first)
+        msg = "layer " + std::to_string(first->seq) + " (creation order; " + std::to_string(nflagged) +
+              " layer(s) flagged): " + msg;
+    return fail(ctx, st, msg);
+}
+
+int ingot_device_mem_info(ingot_ctx* ctx, uint64_t* free_bytes, uint64_t* total_bytes) {
+    CHECK_CTX(ctx);
+    if (!free_bytes || !total_bytes) return INGOT_INVALID;
+    size_t fr = 0, to = 0;
+    HIP_TRY(ctx, hipMemGetInfo(&fr, &to));
+    *free_bytes = fr;
+    *total_bytes = to;
     return INGOT_OK;
 }
 
@@ -791,6 +917,19 @@ int ingot_device_copy(ingot_ctx* ctx, void* d_dst, const void* d_src, uint64_t b
                        static_cast<const uint4*>(d_src), n16);
     LAUNCH_CHECK(ctx);
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return INGOT_OK;
+}
+
+int ingot_device_read(ingot_ctx* ctx, const void* d_src, uint64_t bytes, uint32_t* d_sink) {
+    CHECK_CTX(ctx);
+    if ((bytes & 15u) || !d_sink || (bytes && !d_src))
+        return fail(ctx, INGOT_INVALID, "device_read: bytes must be a multiple of 16, sink non-null");
+    const uint64_t n16 = bytes / 16u;
+    const uint64_t blocks = std::max<uint64_t>(1u, (n16 + READ_BLOCK_WORDS - 1) / READ_BLOCK_WORDS);
+    if (blocks > 0x7fffffffu) return fail(ctx, INGOT_INVALID, "device_read: too many bytes for one launch");
+    hipLaunchKernelGGL(k_read16, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, static_cast<const uint4*>(d_src),
+                       n16, d_sink);
+    LAUNCH_CHECK(ctx);
     return INGOT_OK;
 }
 
@@ -1031,6 +1170,7 @@ static int create_layer(ingot_ctx* ctx, const ingot_layer_desc* d, uint32_t slot
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_gate, &L->sgate);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_up, &L->sup);
     if (st == INGOT_OK && has_shared) st = upload_matrix(ctx, &d->shared_down, &L->sdown);
+    if (st == INGOT_OK) st = attach(ctx, L);
     if (st != INGOT_OK) {
         free_dev(L);
         delete L;
@@ -1116,6 +1256,7 @@ int ingot_layer_clone(const ingot_layer* src, ingot_layer** out) {
         st = dup(sm[i]->d, sm[i]->nbytes, (void**)&dm[i]->d);
         if (st == INGOT_OK) st = dup(sm[i]->t, sm[i]->nbytes, (void**)&dm[i]->t);
     }
+    if (st == INGOT_OK) st = attach(ctx, L);
     if (st != INGOT_OK) {
         free_dev(L);
         delete L;
@@ -1129,9 +1270,12 @@ void ingot_layer_destroy(ingot_layer* L) {
     if (!L) return;
     (void)hipSetDevice(L->ctx->device);
     (void)hipStreamSynchronize(L->ctx->stream);
+    detach(L);
     free_dev(L);
     delete L;
 }
+
+int ingot_layer_flag_status(const ingot_layer* L) { return L ? L->flag_status : INGOT_INVALID; }
 
 int ingot_layer_set_gemm_mode(ingot_layer* L, uint32_t mode) {
     if (!L || mode > INGOT_GEMM_FP32) return INGOT_INVALID;
@@ -1152,11 +1296,6 @@ int ingot_layer_reserve(ingot_layer* L, uint32_t T) {
     CHECK_CTX(L->ctx);
     return reserve(L, T);
 }
-
-
-// The f16 GEMM addresses its A operands (x split: T rows of H; act split: P + T
-// rows of F) and their group sums with 32-bit byte offsets.
-static bool f16_gemm_fits(uint64_t kdim, uint64_t rows) { return 2ull * kdim * rows < (1ull << 32); }
 
 // The stages of a cached layer's forward (src/qwen.rs:1171-1253): routing and
 // dispatch, then the routing is read back to the host; the routed experts, in
@@ -1285,7 +1424,7 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
     const int ks_ = hs_ ? (int)L->sdown.kind : -1;
     const bool fuse_shared = hs_ && can_fuse_shared(L->down.kind, ks_);
     const bool decode = takes_decode(L, T);
-    uint32_t* flags = ctx->d_flags;
+    uint32_t* flags = layer_flags(L);
     float* xstat = w.xstat;
 
     // 1. router (+ RMSNorm, + shared gate logit, + per-token input maximum)
@@ -1371,13 +1510,8 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         // format allows it (a Q4_K_M layer's Q6_K down), gate/up runs on the
         // f16 GEMM writing fp32 act and the down projection on the fp32 GEMM,
         // over the same 64-token tiles.
-        const uint64_t PS = (uint64_t)P + (hs ? T : 0u);
-        const bool f16gu = L->gemm_mode == INGOT_GEMM_AUTO && f16_gemm_kind(gate.kind, H, true) &&
-                           f16_gemm_fits(H, T) && f16_gemm_fits(F, PS);
-        const bool f16 = f16gu && f16_gemm_kind(down.kind, F, false);
-        const bool merge = f16 && hs && SF == F && sgate.kind == gate.kind && sup.kind == up.kind &&
-                           sdown.kind == down.kind && sgate.stride == gate.stride && sup.stride == up.stride &&
-                           sdown.stride == down.stride;
+        const PrefillPlan plan = prefill_plan(L, T);
+        const bool f16gu = plan.f16gu, f16 = plan.f16, merge = plan.merge;
         const int aord = f16 ? a_order(down.kind) : A_F32, xord = a_order(gate.kind);
         const bool mins = f16 && (down.kind == 12 || down.kind == 13);
         // 128-token tiles when an expert can take more than 64 pairs (each takes at
@@ -1479,6 +1613,7 @@ int ingot_layer_forward(ingot_layer* L, const float* d_x, uint32_t T, float* d_o
     if (!d_x || !d_out || T == 0) return fail(L->ctx, INGOT_INVALID, "MoE input shape mismatch");
     const int st = reserve(L, T);
     if (st != INGOT_OK) return st;
+    L->last_static = false;
     return layer_forward(L, L->w, d_x, nullptr, T, d_out, d_ids, d_weights);
 }
 
@@ -1495,6 +1630,7 @@ int ingot_layer_forward_static(ingot_layer* L, const float* d_x, uint32_t T, flo
                         " bytes of workspace; the static scratch holds " + std::to_string(STATIC_SCRATCH_BYTES));
     Ws w;
     carve(L, T, L->ctx->scratch, &w);
+    L->last_static = true;
     return layer_forward(L, w, d_x, nullptr, T, d_out, d_ids, d_weights);
 }
 
@@ -1510,6 +1646,7 @@ int ingot_layer_forward_add(ingot_layer* L, const float* d_x, const float* d_a, 
     if (!L->has_norm) return fail(L->ctx, INGOT_INVALID, "the residual add needs the layer's RMSNorm gain");
     const int st = reserve(L, T);
     if (st != INGOT_OK) return st;
+    L->last_static = false;
     return layer_forward(L, L->w, d_x, d_a, T, d_out, d_ids, d_weights);
 }
 
@@ -1517,9 +1654,13 @@ int ingot_layers_time_stage(ingot_layer* const* layers, uint32_t n, uint32_t sta
     if (!layers || n == 0 || !ms || stage >= ST_N || reps == 0) return INGOT_INVALID;
     ingot_ctx* ctx = layers[0]->ctx;
     CHECK_CTX(ctx);
-    for (uint32_t i = 0; i < n; ++i)
-        if (!layers[i] || layers[i]->ctx != ctx || !layers[i]->stage[stage])
-            return fail(ctx, INGOT_INVALID, "stage did not run in the last forward");
+    for (uint32_t i = 0; i < n; ++i) {
+        if (!layers[i] || layers[i]->ctx != ctx) return fail(ctx, INGOT_INVALID, "layers of different contexts");
+        // A cached layer's GEMM stages read the expert -> slot table of a pass,
+        // which exists only inside its forward.
+        if (layers[i]->cached) return fail(ctx, INGOT_INVALID, "a cached layer's stages cannot be replayed");
+        if (!layers[i]->stage[stage]) return fail(ctx, INGOT_INVALID, "stage did not run in the last forward");
+    }
     hipStream_t s = ctx->stream;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -1567,6 +1708,10 @@ int ingot_layer_dispatch_debug(ingot_layer* L, uint32_t* counts, uint32_t* first
     CHECK_CTX(ctx);
     if (!L->last_prefill || !L->stage[ST_DISPATCH])
         return fail(ctx, INGOT_INVALID, "the last forward did not run the prefill dispatch");
+    // A static forward's buffers are in the shared array, which any later static
+    // forward on this GPU overwrites.
+    if (L->last_static)
+        return fail(ctx, INGOT_INVALID, "the last forward used the shared static workspace: its buffers are not kept");
     if (!counts || !first || !pairs || !inverse || !tiles || !info)
         return fail(ctx, INGOT_INVALID, "null output buffer");
     const Ws& w = L->last;

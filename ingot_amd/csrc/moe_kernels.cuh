@@ -2956,6 +2956,29 @@ __global__ __launch_bounds__(256) void k_copy16(uint4* __restrict__ dst, const u
         dst[i] = src[i];
 }
 
+// Streaming read of n16 16-byte words, the floor a decode stage of the same
+// bytes cannot beat: a block of 256 lanes reads READ_BLOCK_WORDS consecutive
+// words (16 KiB), each lane READ_UNROLL of them 4 KiB apart with every load in flight,
+// and folds them with XOR. Nothing is stored unless a lane's fold equals an
+// arbitrary constant (the stores keep the loads live; sink holds one word per
+// block). n16 == 0 gives an empty kernel node: a dependent launch doing nothing.
+constexpr uint32_t READ_UNROLL = 4;
+constexpr uint64_t READ_BLOCK_WORDS = 256ull * READ_UNROLL;
+__global__ __launch_bounds__(256) void k_read16(const uint4* __restrict__ src, uint64_t n16,
+                                                uint32_t* __restrict__ sink) {
+    const uint64_t base = (uint64_t)blockIdx.x * READ_BLOCK_WORDS + threadIdx.x;
+    uint4 v[READ_UNROLL];
+#pragma unroll
+    for (uint32_t j = 0; j < READ_UNROLL; ++j) {
+        const uint64_t i = base + 256ull * j;
+        v[j] = i < n16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < READ_UNROLL; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
 // Dense token tiles for the shared expert: tile t = {0, 64 t, min(64, T - 64 t), 0}.
 __global__ void k_dense_tiles(uint32_t T, uint32_t cap, uint32_t* __restrict__ tiles) {
     uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;

@@ -168,8 +168,12 @@ class Gpu:
         self.ctx = ctx.value
 
     def close(self) -> None:
+        """Destroys the context. Refused (InvalidData, the context kept) while
+        layers created on it are alive: destroy them first."""
         if getattr(self, "ctx", None):
-            self.lib.ingot_ctx_destroy(self.ctx)
+            st = self.lib.ingot_ctx_destroy(self.ctx)
+            if st != OK:
+                _raise(st, self.lib.ingot_last_error(self.ctx).decode())
             self.ctx = None
 
     def __del__(self):
@@ -190,6 +194,18 @@ class Gpu:
 
     def check_device_flags(self) -> None:
         self._check(self.lib.ingot_ctx_check_device_flags(self.ctx))
+
+    def stream_read(self, buf: DeviceBuffer, nbytes: int, sink: DeviceBuffer, offset: int = 0) -> None:
+        """Asynchronous streaming read of nbytes at buf + offset by a plain
+        kernel (ingot_device_read; nbytes == 0: an empty kernel node)."""
+        assert offset + nbytes <= buf.nbytes and sink.nbytes >= 4 * max(1, -(-nbytes // 16384))
+        self._check(self.lib.ingot_device_read(self.ctx, buf.ptr + offset, int(nbytes), sink.ptr))
+
+    def mem_info(self) -> tuple[int, int]:
+        """(free, total) bytes of device memory."""
+        fr, to = C.c_uint64(), C.c_uint64()
+        self._check(self.lib.ingot_device_mem_info(self.ctx, C.byref(fr), C.byref(to)))
+        return fr.value, to.value
 
     def buffer(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)
@@ -444,6 +460,11 @@ class MoeLayer:
         if not np.isfinite(out).all():
             raise NonFinite("output contains non-finite values")
         return out, dids.download(np.uint32, T * K).reshape(T, K), dw.download(np.float32, T * K).reshape(T, K)
+
+    def flag_status(self) -> int:
+        """What this layer's own forwards raised before the last
+        Gpu.check_device_flags (OK, NONFINITE or RANGE)."""
+        return int(self.gpu.lib.ingot_layer_flag_status(self.handle))
 
     def time_stage(self, stage: int, reps: int) -> float:
         ms = C.c_float()

@@ -22,8 +22,10 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def gpu():
     from ingot_amd.moe import Gpu
+    import gc
     g = Gpu(0)
     yield g
+    gc.collect()  # layers the tests dropped are destroyed before their context
     g.close()
 
 

@@ -46,6 +46,38 @@ def test_static_forward_matches_forward(gpu, name, Ts):
     layer.destroy()
 
 
+@pytest.mark.parametrize("name,T", [("c0", 8), ("c1", 128)])
+def test_static_forward_first_on_a_fresh_layer_allocates_nothing(gpu, name, T):
+    """A layer that has never reserved: the static forward makes no workspace
+    and no tiled weight copies (device free memory and the layer's weight
+    bytes unchanged), and equals a later forward() bit for bit."""
+    spec = {"c0": CF.c0_layer, "c1": CF.c1_layer}[name]()
+    warm = MoeLayer(gpu, spec)  # loads the code objects and runtime state the static path uses
+    x = CF.inputs(32, T, spec.hidden, seed=T)
+    run(warm, gpu, x, static=True)
+    warm.destroy()
+    layer = MoeLayer(gpu, spec)
+    wb = layer.weight_bytes()
+    dx = gpu.to_device(x)
+    H, K = spec.hidden, spec.top_k
+    out, ids, w = gpu.buffer(4 * T * H), gpu.buffer(4 * T * K), gpu.buffer(4 * T * K)
+    gpu.synchronize()
+    free0, _ = gpu.mem_info()
+    layer.forward_static(dx, T, out, ids, w)
+    gpu.synchronize()
+    free1, _ = gpu.mem_info()
+    gpu.check_device_flags()
+    got = (out.download(np.float32, T * H), ids.download(np.uint32, T * K), w.download(np.float32, T * K))
+    assert layer.weight_bytes() == wb, "the static forward made weight copies"
+    assert free0 - free1 < layer.static_bytes(T) // 2, f"device free memory fell by {free0 - free1} bytes"
+    ref = run(layer, gpu, x, static=False)
+    for a, b, what in zip(got, ref, ("outputs", "ids", "routing weights")):
+        assert np.array_equal(a, b), f"{name} T={T}: {what}"
+    print(f"{name} T={T}: fresh static forward allocated nothing ({free0 - free1} bytes of free memory moved), "
+          f"bit-equal to forward()", flush=True)
+    layer.destroy()
+
+
 def test_static_forward_refuses_oversized_batches(gpu):
     spec = CF.c1_layer()
     layer = MoeLayer(gpu, spec)
