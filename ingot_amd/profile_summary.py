@@ -35,6 +35,10 @@ WORKLOADS = {
     "c3": ("c3 T=64", "configs[3] 64 tokens: 2 eager forwards over each of 2 copies"),
     "c4b1": ("c4 b=1", "configs[4] 48-layer stack at b=1: 2 eager passes"),
     "c4b8": ("c4 b=8", "configs[4] 48-layer stack at b=8: 2 eager passes"),
+    "mix46b1": ("mix46 b=1", "Q4_K gate/up + Q6_K down (Qwen3-30B-A3B Q4_K_M mix) decode b=1: 2 eager forwards "
+                             "over each of 32 copies"),
+    "mix46p": ("mix46 prefill512", "the same mix at prefill 512 (Zipf router bias): 2 eager forwards over each of "
+                                   "8 copies"),
 }
 SQ_PASS = ("SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_WAVES "
            "SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_INSTS_SALU GRBM_GUI_ACTIVE")
