@@ -236,15 +236,21 @@ __device__ __forceinline__ uint32_t route_threshold(const uint32_t (&key)[NE], u
 }
 
 // Top-K selection of one token by one wave (route_keys order):
-//   1. T = route_threshold(K);
-//   2. the selected set: the K keys >= T when exact; else keys above T, then
-//      keys equal to T by ascending id until there are K;
-//   3. the K candidates are compacted in id order into LDS, lane m < K takes
-//      candidate m, reads all K keys (LDS broadcast) and counts those that
+//   1. candidates, a superset of the top K of at most 64 keys: with several
+//      keys per lane (NE > 1), every key >= M, M the K-th highest of the
+//      lanes' maxima (the K lanes with the highest maxima hold K keys >= M, so
+//      the K-th highest key is >= M and so is every key of the top K; finding
+//      M costs one ballot per bit instead of NE). Otherwise (one key per lane,
+//      or more than 64 keys >= M, as when many keys are equal) exactly the top
+//      K: T = route_threshold(K); the K keys >= T when exact, else the keys
+//      above T, then keys equal to T by ascending id until there are K;
+//   2. the C candidates are compacted in id order into LDS, lane m < C takes
+//      candidate m, reads all C keys (LDS broadcast) and counts those that
 //      precede it (higher key, or equal key and lower id: an earlier
-//      position), and puts itself at that rank.
-// Lane k < K ends with selection k's id and weight input. Returns whether
-// this lane saw a non-finite logit or bias.
+//      position), and a candidate of rank < K puts itself at that rank.
+// Every key that precedes a candidate is itself a candidate, so these ranks
+// are the ranks among all keys. Lane k < K ends with selection k's id and
+// weight input. Returns whether this lane saw a non-finite logit or bias.
 template <int NE>
 __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
                                   uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
@@ -253,9 +259,25 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
     float wv[NE];
     bool ok[NE];
     const bool bad = route_keys<NE>(l, bias, E, sigmoid_mode, key, wv, ok);
+    uint64_t sel[NE];
+    uint32_t C = 0;  // candidates (0: not formed yet)
+    if constexpr (NE > 1) {
+        uint32_t mk[1] = {key[0]};
+#pragma unroll
+        for (int j = 1; j < NE; ++j) mk[0] = max(mk[0], key[j]);
+        bool ex1;
+        const uint32_t M = route_threshold<1>(mk, K, ex1);
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            sel[j] = __ballot(ok[j] && key[j] >= M);
+            C += (uint32_t)__popcll(sel[j]);
+        }
+        if (C > 64u) C = 0;
+    }
+    if (C == 0) {
+    C = K;
     bool exact;
     const uint32_t T = route_threshold<NE>(key, K, exact);
-    uint64_t sel[NE];
     if (exact) {  // T > 0: absent candidates excluded
 #pragma unroll
         for (int j = 0; j < NE; ++j) sel[j] = __ballot(key[j] >= T);
@@ -278,7 +300,8 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
             }
         }
     }
-    // 3. compaction in id order (slot j, then lane), ranking, placement
+    }
+    // 2. compaction in id order (slot j, then lane), ranking, placement
     uint32_t* r = route_lds();
     uint32_t before = 0;
 #pragma unroll
@@ -293,25 +316,26 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
         before += (uint32_t)__popcll(sel[j]);
     }
     wave_sync();
-    const bool cand = lane < K;
+    const bool cand = lane < C;
     const uint32_t ck = cand ? r[lane] : 0u, cid = cand ? r[64 + lane] : 0u;
     const float cv = cand ? __uint_as_float(r[128 + lane]) : 0.f;
     uint32_t rank = 0;
-    for (uint32_t m = 0; m < K; m += 4) {
+    for (uint32_t m = 0; m < C; m += 4) {
         const uint4 k4 = *reinterpret_cast<const uint4*>(r + m);
         const uint32_t km[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
         for (uint32_t q = 0; q < 4; ++q)
-            rank += (m + q < K && (km[q] > ck || (km[q] == ck && m + q < lane))) ? 1u : 0u;
+            rank += (m + q < C && (km[q] > ck || (km[q] == ck && m + q < lane))) ? 1u : 0u;
     }
     wave_sync();
-    if (cand) {
+    if (cand && rank < K) {
         r[64 + rank] = cid;
         r[128 + rank] = __float_as_uint(cv);
     }
     wave_sync();
-    my_id = cand ? min(r[64 + lane], E - 1u) : 0u;  // (always below E: a guard for the weight addresses)
-    my_v = cand ? __uint_as_float(r[128 + lane]) : 0.f;
+    const bool sel_k = lane < K;
+    my_id = sel_k ? min(r[64 + lane], E - 1u) : 0u;  // (always below E: a guard for the weight addresses)
+    my_v = sel_k ? __uint_as_float(r[128 + lane]) : 0.f;
     wave_sync();  // the scratch is reused by the next call
     return bad;
 }
