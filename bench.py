@@ -6,8 +6,10 @@ decode b=1 and prefill 512; % of HBM / MFMA roofline).
 A step is one forward of the MoE layer (configs[4]: of the 48-layer stack) over
 one batch of synthetic input already resident in HBM. Every configuration of
 BASELINE.json is measured and reported under "configs", with the real
-Qwen3-30B-A3B Q4_K_M format mix (Q4_K gate/up, Q6_K down) at the C0/C1 shapes
-and the C1 layer at the reference's 4096-token prefill block:
+Qwen3-30B-A3B Q4_K_M format mix (Q4_K gate/up, Q6_K down) at the C0/C1 shapes,
+the Qwen3.8 IQ2_XS checkpoint's mix (IQ2_S gate/up, IQ3_S down, IQ4_XS/Q2_0
+shared expert) at the C2 shape, and the C1 layer at the reference's 4096-token
+prefill block:
 
     configs[0]  decode b=1        (32 resident weight copies)
     configs[1]  prefill 512       (8 copies)  <- the headline `value`
@@ -15,6 +17,7 @@ and the C1 layer at the reference's 4096-token prefill block:
     configs[3]  64 tokens         (2 copies, 980 MB each)
     configs[4]  48 layers, b=1 and b=8
     Q4_K/Q6_K mix b=1 (32 copies) and prefill 512 (8 copies)
+    IQ2_S/IQ3_S mix b=1 (32 copies) and prefill 512 (4 copies)
     configs[1] layer at prefill 4096 (2 copies)
 
 Timing: W untimed warm-up steps in one HIP graph, then
@@ -398,24 +401,17 @@ def run_c4(gpu, steps, warmup, cpu_s):
 
 
 def extra_configs(gpu, args):
-    """More of the real checkpoints' format mixes at the graded shapes (for the
-    record): Q5_K_M-style, the Qwen3.8 IQ2_XS mix
-    (validation/rust-moe-layer-0.json:9-16), and configs[2]'s layer at prefill."""
+    """More format mixes at the graded shapes (for the record): Q5_K_M-style,
+    the Qwen3.8 mix on the fp32 GEMM, and configs[2]'s layer at prefill."""
     from ingot_amd import configs as CF
-    from ingot_amd.moe import GEMM_FP32, IQ2_S, IQ3_S, IQ4_XS, Q2_0, Q5_K
+    from ingot_amd.moe import GEMM_FP32, Q5_K
     out = {}
     S = args.extra_steps
     spec5 = CF.make_layer(0, 0, 2048, 128, 8, 768, Q5_K, Q5_K, bias="zipf")
     out["Q5_K prefill 512"] = run_layer_config(gpu, "Q5_K prefill 512", "Q5_K gate/up and down, prefill 512",
                                                spec5, 512, 8, CF.inputs(0, 512, 2048), S, 10, "mfma", "q5k prefill512")
     del spec5
-    specq = CF.make_layer(2, 0, 2048, 512, 10, 512, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
-                          shared_down_kind=Q2_0, shared_gated=True)
-    out["IQ2_S/IQ3_S mix b=1"] = run_layer_config(gpu, "IQ2_S/IQ3_S mix b=1", "IQ2_S/IQ3_S + IQ4_XS/Q2_0 shared, b=1",
-                                                  specq, 1, 32, CF.inputs(2, 1, 2048), S, 10, "hbm", "mixiq b=1")
-    out["IQ2_S/IQ3_S mix prefill 512"] = run_layer_config(gpu, "IQ2_S/IQ3_S mix prefill 512", "the same, prefill 512",
-                                                          specq, 512, 4, CF.inputs(2, 512, 2048), S, 10, "mfma",
-                                                          "mixiq prefill512")
+    specq = qwen38_mix(CF)
     out["IQ2_S/IQ3_S mix prefill 512, fp32 GEMM"] = run_layer_config(
         gpu, "IQ2_S/IQ3_S mix prefill 512, fp32 GEMM", "the same on the fp32 GEMM", specq, 512, 4,
         CF.inputs(2, 512, 2048), S, 10, "mfma", "mixiq prefill512 fp32", mode=GEMM_FP32)
@@ -425,6 +421,14 @@ def extra_configs(gpu, args):
                                                             "configs[2]'s layer at prefill 512", spec2, 512, 4,
                                                             CF.inputs(2, 512, 2048), S, 10, "mfma", "c2 prefill512")
     return out
+
+
+def qwen38_mix(CF):
+    """The Qwen3.8 IQ2_XS checkpoint's expert formats (validation/rust-moe-layer-0.json:9-16) at configs[2]'s
+    shape: IQ2_S gate/up, IQ3_S down, a gated shared expert in IQ4_XS (gate/up) and Q2_0 (down)."""
+    from ingot_amd.moe import IQ2_S, IQ3_S, IQ4_XS, Q2_0
+    return CF.make_layer(2, 0, 2048, 512, 10, 512, IQ2_S, IQ3_S, shared_ffn=512, shared_gate_kind=IQ4_XS,
+                         shared_down_kind=Q2_0, shared_gated=True)
 
 
 def profile_workload(args):
@@ -460,6 +464,8 @@ def profile_workload(args):
     elif w in ("mix46b1", "mix46p"):
         spec = CF.make_layer(0, 0, 2048, 128, 8, 768, Q4_K, Q6_K, bias=None if w == "mix46b1" else "zipf")
         run(spec, 1 if w == "mix46b1" else 512, 32 if w == "mix46b1" else 8, 0, 2048)
+    elif w in ("mixiqb1", "mixiqp"):
+        run(qwen38_mix(CF), 1 if w == "mixiqb1" else 512, 32 if w == "mixiqb1" else 4, 2, 2048)
     elif w in ("c4b1", "c4b8"):
         T = 1 if w == "c4b1" else 8
         layers = [MoeLayer(gpu, CF.c4_layer(l)) for l in range(48)]
@@ -561,6 +567,15 @@ def main():
             specm, 512, 8, CF.inputs(1, 512, 2048), args.steps, args.warmup, "mfma", "mix46 prefill512",
             cpu_s=small)
         del specm
+        specq = qwen38_mix(CF)
+        configs["mix IQ2_S/IQ3_S b=1"] = run_layer_config(
+            gpu, "mix IQ2_S/IQ3_S b=1", "Qwen3.8 IQ2_XS checkpoint mix at configs[2]'s shape (IQ2_S gate/up, IQ3_S "
+            "down, gated IQ4_XS/Q2_0 shared expert), decode batch 1", specq, 1, 32, CF.inputs(2, 1, 2048),
+            args.decode_steps, args.warmup, "hbm", "mixiq b=1", cpu_s=small, floor=True)
+        configs["mix IQ2_S/IQ3_S prefill 512"] = run_layer_config(
+            gpu, "mix IQ2_S/IQ3_S prefill 512", "the same mix, prefill 512", specq, 512, 4, CF.inputs(2, 512, 2048),
+            args.steps, args.warmup, "mfma", "mixiq prefill512", cpu_s=small)
+        del specq
         # the reference prefills in 4096-token blocks (docs/ENGINE.md:29-31): the dispatch at 32,768 pairs
         configs["configs[1] layer prefill 4096"] = run_layer_config(
             gpu, "configs[1] layer prefill 4096", "configs[1]'s layer at the reference's 4096-token prefill block",

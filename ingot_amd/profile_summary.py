@@ -39,6 +39,9 @@ WORKLOADS = {
                              "over each of 32 copies"),
     "mix46p": ("mix46 prefill512", "the same mix at prefill 512 (Zipf router bias): 2 eager forwards over each of "
                                    "8 copies"),
+    "mixiqb1": ("mixiq b=1", "Qwen3.8 IQ2_S/IQ3_S mix (IQ4_XS/Q2_0 shared) decode b=1: 2 eager forwards over each of "
+                             "32 copies"),
+    "mixiqp": ("mixiq prefill512", "the same mix at prefill 512: 2 eager forwards over each of 4 copies"),
 }
 SQ_PASS = ("SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_WAVES "
            "SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_INSTS_SALU GRBM_GUI_ACTIVE")
