@@ -338,6 +338,72 @@ __device__ inline void stage_half_tables() {
     }
 }
 
+// Two-phase table staging for the decode kernels (NT threads per block):
+// load() issues the global loads of this thread's table entries into
+// registers, store() writes the LDS tables that stage_half_tables (HALF) or
+// stage_codebooks would write. A kernel calls load() before its other loads
+// and store() once those are issued: vector-memory loads complete in issue
+// order, so the tables' loads hold back no later load, and store() waits for
+// nothing but them.
+template <int KIND, bool HALF, uint32_t NT>
+struct TableStage {
+    static constexpr uint32_t N = KIND == 16   ? 256u
+                                  : KIND == 17 ? 512u
+                                  : KIND == 18 ? 256u
+                                  : KIND == 20 || KIND == 23 ? 16u
+                                  : KIND == 21 ? 512u
+                                  : KIND == 22 ? 1024u
+                                  : KIND == 29 ? 2048u
+                                               : 0u;
+    static constexpr uint32_t PER = (N + NT - 1) / NT;
+    uint64_t v[PER > 0 ? PER : 1];
+    static __device__ __forceinline__ uint64_t src(uint32_t i) {
+        if constexpr (KIND == 16) return ingot_iq2xxs_grid[i];
+        else if constexpr (KIND == 17) return ingot_iq2xs_grid[i];
+        else if constexpr (KIND == 18) return ingot_iq3xxs_grid[i];
+        else if constexpr (KIND == 20 || KIND == 23) return (uint64_t)(uint8_t)ingot_kvalues_iq4nl[i];
+        else if constexpr (KIND == 21) return ingot_iq3s_grid[i];
+        else if constexpr (KIND == 22) return ingot_iq2s_grid[i];
+        else if constexpr (KIND == 29) return ingot_iq1s_grid[i];
+        else return 0;
+    }
+    __device__ __forceinline__ void load() {
+#pragma unroll
+        for (uint32_t p = 0; p < PER; ++p) {
+            const uint32_t i = threadIdx.x + NT * p;
+            v[p] = i < N ? src(i) : 0ull;
+        }
+    }
+    __device__ __forceinline__ void store() const {
+#pragma unroll
+        for (uint32_t p = 0; p < PER; ++p) {
+            const uint32_t i = threadIdx.x + NT * p;
+            if (i >= N) continue;
+            const uint64_t g = v[p];
+            if constexpr (HALF) {
+                const uint4 h = make_uint4(grid_pair_h(g, 0), grid_pair_h(g, 1), grid_pair_h(g, 2), grid_pair_h(g, 3));
+                if constexpr (KIND == 16) lds_iq2xxs_grid_h()[i] = h;
+                else if constexpr (KIND == 17) lds_iq2xs_grid_h()[i] = h;
+                else if constexpr (KIND == 22) lds_iq2s_grid_h()[i] = h;
+                else if constexpr (KIND == 21) lds_iq3s_grid_h()[i] = make_uint2(h.x, h.y);
+            } else {
+                if constexpr (KIND == 16) lds_iq2xxs_grid()[i] = g;
+                else if constexpr (KIND == 17) lds_iq2xs_grid()[i] = g;
+                else if constexpr (KIND == 18) lds_iq3xxs_grid()[i] = (uint32_t)g;
+                else if constexpr (KIND == 20 || KIND == 23) lds_iq4nl_values()[i] = (float)(int8_t)(uint8_t)g;
+                else if constexpr (KIND == 21) lds_iq3s_grid()[i] = (uint32_t)g;
+                else if constexpr (KIND == 22) lds_iq2s_grid()[i] = g;
+                else if constexpr (KIND == 29) lds_iq1s_grid()[i] = g;
+            }
+        }
+        if constexpr (HALF && (KIND == 16 || KIND == 17)) {
+            for (uint32_t i = threadIdx.x; i < 128u; i += NT) lds_iq3_signmask()[i] = sign_mask8(ingot_ksign(i));
+        } else if constexpr (HALF && (KIND == 21 || KIND == 22)) {
+            for (uint32_t i = threadIdx.x; i < 256u; i += NT) lds_sign8mask()[i] = sign_mask8(i);
+        }
+    }
+};
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);

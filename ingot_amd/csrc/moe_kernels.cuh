@@ -159,11 +159,12 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-wave LDS scratch of wave_route: K <= 64 candidates x (key, id, weight
-// input). Kernels that route use at most 8 waves per block.
+// Per-wave LDS scratch of wave_route: 64 candidate slots x (key, id, weight
+// input), then the same for 64 junk slots (one per lane) that lanes without a
+// candidate write instead. Kernels that route use at most 8 waves per block.
 constexpr uint32_t ROUTE_MAX_WAVES = 8;
 __device__ inline uint32_t* route_lds() {
-    __shared__ __align__(16) uint32_t r[ROUTE_MAX_WAVES][3 * 64];
+    __shared__ __align__(16) uint32_t r[ROUTE_MAX_WAVES][6 * 64];
     return r[threadIdx.x >> 6];
 }
 
@@ -330,41 +331,55 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
         }
     }
     }
-    // 2. compaction in id order (slot j, then lane), ranking, placement
+    // 2. compaction in id order (slot j, then lane), ranking, placement. C <=
+    // 64 (the candidates were formed so), so every position is below 64; a
+    // lane without a candidate in slot j writes its junk slot (192 + lane), so
+    // the writes need no branch.
     uint32_t* r = route_lds();
     uint32_t before = 0;
 #pragma unroll
     for (int j = 0; j < NE; ++j) {
         const uint32_t pos = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(sel[j] >> 32),
                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)sel[j], 0u));
-        if (((sel[j] >> lane) & 1ull) && pos < 64u) {
-            r[pos] = key[j];
-            r[64 + pos] = lane + 64u * j;
-            r[128 + pos] = __float_as_uint(wv[j]);
-        }
+        const uint32_t at = ((sel[j] >> lane) & 1ull) ? (pos & 63u) : 192u + lane;
+        r[at] = key[j];
+        r[64 + at] = lane + 64u * j;
+        r[128 + at] = __float_as_uint(wv[j]);
         before += (uint32_t)__popcll(sel[j]);
     }
     wave_sync();
     const bool cand = lane < C;
     const uint32_t ck = cand ? r[lane] : 0u, cid = cand ? r[64 + lane] : 0u;
     const float cv = cand ? __uint_as_float(r[128 + lane]) : 0.f;
+    // Rank: the candidates that precede this one, sixteen per step (four
+    // broadcast reads issued together; slots past C are masked); key and
+    // position compare as one 64-bit value (key, 63 - position).
+    // (slots past C read as key 0 through a uniform mask: candidate keys are
+    // >= 1, so they never precede a candidate)
+    const uint64_t mine = ((uint64_t)ck << 32) | (63u - lane);
     uint32_t rank = 0;
-    for (uint32_t m = 0; m < C; m += 4) {
-        const uint4 k4 = *reinterpret_cast<const uint4*>(r + m);
-        const uint32_t km[4] = {k4.x, k4.y, k4.z, k4.w};
+    for (uint32_t m = 0; m < C; m += 16) {  // m <= 48: reads stay in r[0, 64)
+        uint4 k4[4];
 #pragma unroll
-        for (uint32_t q = 0; q < 4; ++q)
-            rank += (m + q < C && (km[q] > ck || (km[q] == ck && m + q < lane))) ? 1u : 0u;
+        for (int q = 0; q < 4; ++q) k4[q] = *reinterpret_cast<const uint4*>(r + m + 4u * q);
+#pragma unroll
+        for (uint32_t q = 0; q < 16; ++q) {
+            const uint4 v = k4[q / 4];
+            const uint32_t p = m + q, live = p < C ? 0xffffffffu : 0u;
+            const uint32_t km = (q % 4 == 0 ? v.x : q % 4 == 1 ? v.y : q % 4 == 2 ? v.z : v.w) & live;
+            rank += ((((uint64_t)km << 32) | (63u - p)) > mine) ? 1u : 0u;
+        }
     }
-    wave_sync();
-    if (cand && rank < K) {
-        r[64 + rank] = cid;
-        r[128 + rank] = __float_as_uint(cv);
-    }
-    wave_sync();
+    // Placement: candidate of rank k < K sends its id and weight input to lane
+    // k (ds_permute: a forward permute through the LDS crossbar); the others
+    // send to lane 63, unread when K < 64 (K = 64 makes every lane a candidate
+    // of a distinct rank).
+    const uint32_t dst = (cand && rank < K) ? rank : 63u;
+    const uint32_t pid = (uint32_t)__builtin_amdgcn_ds_permute((int)(dst << 2), (int)cid);
+    const uint32_t pv = (uint32_t)__builtin_amdgcn_ds_permute((int)(dst << 2), (int)__float_as_uint(cv));
     const bool sel_k = lane < K;
-    my_id = sel_k ? min(r[64 + lane], E - 1u) : 0u;  // (always below E: a guard for the weight addresses)
-    my_v = sel_k ? __uint_as_float(r[128 + lane]) : 0.f;
+    my_id = sel_k ? min(pid, E - 1u) : 0u;  // (always below E: a guard for the weight addresses)
+    my_v = sel_k ? __uint_as_float(pv) : 0.f;
     wave_sync();  // the scratch is reused by the next call
     return bad;
 }
@@ -921,6 +936,11 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     // u % 64, chunk l + 64 (u / 512), float4 (u / 64) % 8), is loaded into
     // registers now and written to LDS after the weight loads are issued, so
     // its latency overlaps the routing's logit loads.
+    // Codebooks: loaded first, written to LDS once the weight loads are out.
+    TableStage<KIND, HX, 512> tab;
+    TableStage<KSV, HS, 512> tabs;
+    tab.load();
+    if constexpr (SH && KSV != KIND) tabs.load();
     const float* xt = x + (uint64_t)t * H;
     float4 xa[2];
     bool xok[2];
@@ -932,12 +952,23 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                        : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const float xm = (HX || HS) ? xstat[2u * t] : 0.f;
-    // decoded only after the barrier that publishes s_x4
-    if constexpr (HX) stage_half_tables<KIND>();
-    else stage_codebooks<KIND>();
-    if constexpr (SH && KSV != KIND) {
-        if constexpr (HS) stage_half_tables<KSV>();
-        else stage_codebooks<KSV>();
+    // The shared expert's rows (wave 7), loaded before the routing: they do
+    // not depend on it.
+    const bool shw = SH && wave == GU_WAVES - 1u;
+    typename Fs::Raw sg[SH ? RPW : 1][SH ? CPL : 1], su[SH ? RPW : 1][SH ? CPL : 1];
+    if constexpr (SH) {
+        if (shw) {
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) {
+                const uint32_t r = min(r0 + i, F - 1);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const uint32_t c = min(lane + 64u * j, nch - 1);
+                    sg[i][j] = Fs::load_raw(sgate + (uint64_t)r * sgstride, c);
+                    su[i][j] = Fs::load_raw(sup + (uint64_t)r * sustride, c);
+                }
+            }
+        }
     }
     __shared__ float s_sv[64];  // weight input of each selection
     uint32_t eid[NP];
@@ -990,23 +1021,9 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
         }
     }
-    // the shared expert's rows (wave 7)
-    const bool shw = SH && wave == GU_WAVES - 1u;
-    typename Fs::Raw sg[SH ? RPW : 1][SH ? CPL : 1], su[SH ? RPW : 1][SH ? CPL : 1];
-    if constexpr (SH) {
-        if (shw) {
-#pragma unroll
-            for (int i = 0; i < RPW; ++i) {
-                const uint32_t r = min(r0 + i, F - 1);
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) {
-                    const uint32_t c = min(lane + 64u * j, nch - 1);
-                    sg[i][j] = Fs::load_raw(sgate + (uint64_t)r * sgstride, c);
-                    su[i][j] = Fs::load_raw(sup + (uint64_t)r * sustride, c);
-                }
-            }
-        }
-    }
+    // (read only after the barrier below)
+    tab.store();
+    if constexpr (SH && KSV != KIND) tabs.store();
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
         const uint32_t k = wave + GU_WAVES * n;
@@ -1162,13 +1179,12 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
     constexpr bool HD = half_x<KD>(), HS = KS >= 0 && half_x<(KS < 0 ? KD : KS)>();  // f16-pair inputs
     __shared__ float4 s_act4[DOWN_LDS_FLOATS / 4];
     __shared__ float s_sum[DOWN_LDS_FLOATS / 16];
-    // Codebooks: decoded only after the barrier that follows the activation staging.
-    if constexpr (HD) stage_half_tables<KD>();
-    else stage_codebooks<KD>();
-    if constexpr (KS >= 0 && KS != KD) {
-        if constexpr (HS) stage_half_tables<(KS < 0 ? KD : KS)>();
-        else stage_codebooks<(KS < 0 ? KD : KS)>();
-    }
+    // Codebooks: loaded first, written to LDS once the weight loads are out
+    // (decoded after the barrier that follows the activation staging).
+    TableStage<KD, HD, DOWN_THREADS> tab;
+    TableStage<(KS < 0 ? KD : KS), HS, DOWN_THREADS> tabs;
+    tab.load();
+    if constexpr (KS >= 0 && KS != KD) tabs.load();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const uint32_t t = blockIdx.y;
     const uint32_t nchF = F / 32u, nchS = KS >= 0 ? SF / 32u : 0u;
@@ -1237,6 +1253,8 @@ __global__ __launch_bounds__(DOWN_THREADS) void k_dec_down(const uint8_t* __rest
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    tab.store();
+    if constexpr (KS >= 0 && KS != KD) tabs.store();
     // 4. stage the activations (shared expert's times its gate) and each
     //    chunk's two 16-value sums (xs0, xs1 of the formats' dot products).
     //    Chunks of the f16-pair formats are split after scaling by 2^ea, ea
