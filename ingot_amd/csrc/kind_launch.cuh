@@ -54,7 +54,7 @@ static bool dec_gate_up_cpl(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t r
 #define DGU_(C, N, R, P)                                                                                         \
     hipLaunchKernelGGL((k_dec_gate_up2<KIND, C, R, N, NE, -1, P>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,  \
                        a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, \
-                       a.flags, a.act)
+                       a.flags, a.act, nullptr, nullptr, 0, 0, nullptr, a.pfd, a.pfds, a.pfs, a.pfss)
 #define DGU(C, N, R)                     \
     do {                                 \
         if (NE > 2 && a.pre) DGU_(C, N, R, (NE > 2)); \
@@ -84,11 +84,12 @@ bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw
             if (a.pre)
                 hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, -1, true>), grid, dim3(512), 0, s, a.g, a.u, a.gs,
                                    a.us, a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit,
-                                   a.ids, a.w, a.flags, a.act);
+                                   a.ids, a.w, a.flags, a.act, nullptr, nullptr, 0, 0, nullptr, a.pfd, a.pfds, a.pfs,
+                                   a.pfss);
             else
                 hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,
                                    a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids,
-                                   a.w, a.flags, a.act);
+                                   a.w, a.flags, a.act, nullptr, nullptr, 0, 0, nullptr, a.pfd, a.pfds, a.pfs, a.pfss);
             return true;
         }
     return dec_gate_up_cpl<KIND, 16>(s, cpl, np, rpw, grid, a);
@@ -103,11 +104,11 @@ bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32
     if (a.pre)
         hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS, true>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,
                            a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w,
-                           a.flags, a.act, sg, su, sgs, sus, sact);
+                           a.flags, a.act, sg, su, sgs, sus, sact, a.pfd, a.pfds, a.pfs, a.pfss);
     else
         hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us, a.F,
                            a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w, a.flags,
-                           a.act, sg, su, sgs, sus, sact);
+                           a.act, sg, su, sgs, sus, sact, a.pfd, a.pfds, a.pfs, a.pfss);
     return true;
 }
 

@@ -52,6 +52,9 @@ struct DecGateUpArgs {
     uint32_t* flags;
     float* act;
     uint32_t pre;  // 1: ids and w hold the routing (k_route ran), inputs of the kernel
+    // down matrices whose rows the kernel requests ahead of k_dec_down (NULL: none)
+    const uint8_t *pfd = nullptr, *pfs = nullptr;
+    uint64_t pfds = 0, pfss = 0;
 };
 
 struct DownArgs {

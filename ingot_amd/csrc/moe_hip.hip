@@ -404,12 +404,13 @@ static bool launch_dec_gate_up(hipStream_t s, uint32_t kind, const uint8_t* g, c
                                uint64_t us, uint32_t F, uint32_t H, uint32_t T, const float* x, const float* xstat,
                                const float* logits, const float* bias, uint32_t E, uint32_t K, uint32_t mode,
                                float scale, float limit, uint32_t* ids, float* w, uint32_t* flags, float* act,
-                               uint32_t pre) {
+                               uint32_t pre, const uint8_t* pfd, uint64_t pfds) {
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     dim3 grid((F + rpw - 1) / rpw, T);
-    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act,
-                          pre};
+    DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act, pre};
+    a.pfd = pfd;
+    a.pfds = pfds;
     switch (kind) {
 #define K_(KV) case KV: return launch_dec_gate_up_k<KV>(s, cpl, np, rpw, grid, a);
         INGOT_KINDS(K_)
@@ -426,13 +427,17 @@ static bool launch_dec_gate_up_fused(hipStream_t s, uint32_t kind, uint32_t skin
                                      uint64_t sgs, uint64_t sus, uint32_t F, uint32_t H, uint32_t T, const float* x,
                                      const float* xstat, const float* logits, const float* bias, uint32_t E,
                                      uint32_t K, uint32_t mode, float scale, float limit, uint32_t* ids, float* w,
-                                     uint32_t* flags, float* act, float* sact, uint32_t pre) {
+                                     uint32_t* flags, float* act, float* sact, uint32_t pre, const uint8_t* pfd,
+                                     uint64_t pfds, const uint8_t* pfs, uint64_t pfss) {
     const uint32_t cpl = (H / 32 + 63) / 64, np = (K + GU_WAVES - 1) / GU_WAVES;
     if (K >= GU_WAVES * np) return false;  // no free pair slot
     const uint32_t rpw = dec_gate_up_rows(F, T, cpl, np);
     const dim3 grid((F + rpw - 1) / rpw, T);
-    const DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act,
-                          pre};
+    DecGateUpArgs a{g, u, gs, us, F, H, x, xstat, logits, bias, E, K, mode, scale, limit, ids, w, flags, act, pre};
+    a.pfd = pfd;
+    a.pfds = pfds;
+    a.pfs = pfs;
+    a.pfss = pfss;
 #define FG_(KG, KS)                                                                                              \
     if (kind == KG && skind == KS) return launch_dec_gate_up_fused_k<KG, KS>(s, cpl, np, rpw, grid, a, sg, su, sgs, \
                                                                              sus, sact);
@@ -1466,15 +1471,24 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         const uint32_t mode = L->routing;
         const float scale = L->scale;
         const bool hs = hs_;
+        // Down rows requested ahead by the gate/up kernel above 128 experts:
+        // there the selection over 8+ keys per lane leaves HBM idle for about
+        // 2 us of the gate/up launch (C2 b=1 step 22.2 -> 20.5 us); at 128
+        // experts its weight stream already fills HBM, and the extra bytes
+        // delay its end by more than the down kernel gains (C0 16.0 -> 16.2).
+        const bool pf = E > 128;
+        const uint8_t* pfd = pf ? down.d : nullptr;
+        const uint8_t* pfs = pf && hs ? sdown.d : nullptr;
         L->stage[ST_GATEUP] = [=](hipStream_t ss) {
             // a shared expert as wide as the routed ones joins the routed kernel where that is instantiated
             if (hs && SF == F && sgate.kind == sup.kind &&
                 launch_dec_gate_up_fused(ss, gate.kind, sgate.kind, gate.d, up.d, gate.stride, up.stride, sgate.d,
                                          sup.d, sgate.stride, sup.stride, F, H, T, xin, xstat, lg, b, E, K, mode,
-                                         scale, limit, ids, wts, flags, act, sact, pre_route ? 1u : 0u))
+                                         scale, limit, ids, wts, flags, act, sact, pre_route ? 1u : 0u, pfd,
+                                         down.stride, pfs, sdown.stride))
                 return;
             launch_dec_gate_up(ss, gate.kind, gate.d, up.d, gate.stride, up.stride, F, H, T, xin, xstat, lg, b, E, K,
-                               mode, scale, limit, ids, wts, flags, act, pre_route ? 1u : 0u);
+                               mode, scale, limit, ids, wts, flags, act, pre_route ? 1u : 0u, pfd, down.stride);
             if (hs)
                 launch_gemv_gate_up(ss, sgate.kind, sgate.d, sup.d, sgate.stride, sup.stride, SF, H, T, xin, nullptr, 1,
                                     limit, sact);

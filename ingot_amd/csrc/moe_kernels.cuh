@@ -920,7 +920,9 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                                                       uint32_t* __restrict__ flags, float* __restrict__ act,
                                                       const uint8_t* __restrict__ sgate = nullptr,
                                                       const uint8_t* __restrict__ sup = nullptr, uint64_t sgstride = 0,
-                                                      uint64_t sustride = 0, float* __restrict__ sact = nullptr) {
+                                                      uint64_t sustride = 0, float* __restrict__ sact = nullptr,
+                                                      const uint8_t* __restrict__ pfd = nullptr, uint64_t pfds = 0,
+                                                      const uint8_t* __restrict__ pfs = nullptr, uint64_t pfss = 0) {
     using Fm = Fmt<KIND>;
     constexpr bool HX = half_x<KIND>();  // input staged as f16 pairs (split_h4)
     constexpr int KSV = KS < 0 ? KIND : KS;
@@ -1018,6 +1020,41 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                 const uint32_t c = min(lane + 64u * j, nch - 1);
                 rg[n][i][j] = Fm::load_raw(grow, c);
                 ru[n][i][j] = Fm::load_raw(urow, c);
+            }
+        }
+    }
+    // Down rows ahead of k_dec_down (pfd: the routed down matrix, pfs: the
+    // shared expert's): this wave's experts' rows in this block's slice of H,
+    // the slice that block blockIdx.x of the down kernel reads when its grid
+    // splits H over as many blocks (else the rows still reach the MALL). One
+    // byte per 128-byte line, requested after the wave's own weight loads and
+    // left in registers until the empty asm at the end of the kernel, so the
+    // down kernel's weight loads hit cache instead of waiting on HBM after its
+    // expert ids arrive. Nothing is stored.
+    uint32_t pfv[NP + 1][2] = {};
+    if (pfd) {
+        const uint32_t rs = (H + gridDim.x - 1) / gridDim.x, pr0 = min(blockIdx.x * rs, H);
+        const uint32_t nr = min(pr0 + rs, H) - pr0;
+#pragma unroll
+        for (int n = 0; n < NP; ++n) {
+            const uint32_t k = wave + GU_WAVES * n;
+            if (n == 0 || k < K) {
+                const uint8_t* pb = pfd + ((uint64_t)eid[n] * H + pr0) * pfds;
+                const uint64_t span = (uint64_t)nr * pfds;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint64_t o = 128ull * (lane + 64u * i);
+                    if (o < span) pfv[n][i] = pb[o];
+                }
+            }
+        }
+        if (SH && shw && pfs) {
+            const uint8_t* pb = pfs + (uint64_t)pr0 * pfss;
+            const uint64_t span = (uint64_t)nr * pfss;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint64_t o = 128ull * (lane + 64u * i);
+                if (o < span) pfv[NP][i] = pb[o];
             }
         }
     }
@@ -1147,6 +1184,8 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
             }
         }
     }
+#pragma unroll
+    for (int n = 0; n <= NP; ++n) asm volatile("" ::"v"(pfv[n][0]), "v"(pfv[n][1]));
 }
 
 // ------------------------------------------------ decode: down + combine
