@@ -5,15 +5,18 @@
 //                            RMSNorm, optional shared-expert gate logit
 //   route    k_route         per-token top-K, one wave per token (wave_route);
 //                            softmax or sigmoid+bias weights
-//   decode   k_dec_gate_up2  each wave selects its pair's expert (wave_kth),
-//                            then act[p] = w_k SwiGLU(G_e x_t, U_e x_t), one wave
-//                            per pair
+//   decode   k_dec_gate_up2  each wave selects its pair's expert (wave_kth, or
+//                            wave_route for two pairs per wave), then act[p] =
+//                            w_k SwiGLU(G_e x_t, U_e x_t), one wave per pair;
+//                            above 128 experts it also requests the down rows
+//                            k_dec_down will read
 //            k_gemv_gate_up  the same for the shared expert (no routing)
 //            k_dec_down      out[t] = sum_k D_e act[p] (+ shared, + residual)
 //   prefill  k_dispatch      stable expert grouping, tile list (one block)
 //            (its other blocks split x into f16 hi + lo for k_gemm_f16)
 //            k_gemm_f16      f16-MFMA grouped GEMM on integer weight operands
-//                            (Q4_K, IQ3_XXS, IQ4_NL), A split into f16 hi + lo
+//                            (Q4_K, Q5_K, Q6_K, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S,
+//                            IQ4_NL, IQ4_XS), A split into f16 hi + lo
 //            k_gemm<GATEUP>  MFMA f32 grouped GEMM, dequantised weights in LDS
 //                            (every other format)
 //            k_combine       out[t] = sum_k w_k Y[inverse[p]] (+ shared, + residual)
@@ -270,14 +273,15 @@ __device__ __forceinline__ uint32_t route_threshold(const uint32_t (&key)[NE], u
 //      keys per lane (NE > 1), every key >= M, M the K-th highest of the
 //      lanes' maxima (the K lanes with the highest maxima hold K keys >= M, so
 //      the K-th highest key is >= M and so is every key of the top K; finding
-//      M costs one ballot per bit instead of NE). Otherwise (one key per lane,
+//      M takes ballots over one key per lane instead of NE). Otherwise (one key per lane,
 //      or more than 64 keys >= M, as when many keys are equal) exactly the top
 //      K: T = route_threshold(K); the K keys >= T when exact, else the keys
 //      above T, then keys equal to T by ascending id until there are K;
 //   2. the C candidates are compacted in id order into LDS, lane m < C takes
 //      candidate m, reads all C keys (LDS broadcast) and counts those that
 //      precede it (higher key, or equal key and lower id: an earlier
-//      position), and a candidate of rank < K puts itself at that rank.
+//      position), and a candidate of rank < K sends its id and weight input
+//      to lane rank (ds_permute).
 // Every key that precedes a candidate is itself a candidate, so these ranks
 // are the ranks among all keys. Lane k < K ends with selection k's id and
 // weight input. Returns whether this lane saw a non-finite logit or bias.
