@@ -81,6 +81,16 @@ bool launch_dec_gate_up_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32_t rpw
     if (a.E <= 128) return dec_gate_up_cpl<KIND, 2>(s, cpl, np, rpw, grid, a);
     if constexpr (KIND == 17)
         if (a.E <= 512 && cpl == 1 && np == 2 && rpw == 2) {
+            // one token, K <= 12: twelve waves of one pair each (with eight,
+            // the waves holding two pairs set the kernel's end); batches keep
+            // eight-wave blocks, two of which fit a CU
+            if (a.K <= 12 && !a.pre) {
+                hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 1, 8, -1, false, 12>), grid, dim3(768), 0, s, a.g, a.u,
+                                   a.gs, a.us, a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale,
+                                   a.limit, a.ids, a.w, a.flags, a.act, nullptr, nullptr, 0, 0, nullptr, a.pfd, a.pfds,
+                                   a.pfs, a.pfss);
+                return true;
+            }
             if (a.pre)
                 hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, -1, true>), grid, dim3(512), 0, s, a.g, a.u, a.gs,
                                    a.us, a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit,
@@ -101,6 +111,12 @@ bool launch_dec_gate_up_fused_k(hipStream_t s, uint32_t cpl, uint32_t np, uint32
                                 uint64_t sus, float* sact) {
     // the configs[2] shape: 512 experts, one chunk per lane, two pairs per wave, 2 rows
     if (a.E > 512 || a.E <= 128 || cpl != 1 || np != 2 || rpw != 2) return false;
+    if (a.K + 1 <= 12 && !a.pre) {  // one token: twelve waves, one pair each, the shared expert in wave 11
+        hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 1, 8, KS, false, 12>), grid, dim3(768), 0, s, a.g, a.u, a.gs,
+                           a.us, a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids,
+                           a.w, a.flags, a.act, sg, su, sgs, sus, sact, a.pfd, a.pfds, a.pfs, a.pfss);
+        return true;
+    }
     if (a.pre)
         hipLaunchKernelGGL((k_dec_gate_up2<KIND, 1, 2, 2, 8, KS, true>), grid, dim3(512), 0, s, a.g, a.u, a.gs, a.us,
                            a.F, a.H, a.x, a.xstat, a.logits, a.bias, a.E, a.K, a.mode, a.scale, a.limit, a.ids, a.w,

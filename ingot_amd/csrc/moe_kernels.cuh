@@ -165,7 +165,7 @@ __device__ __forceinline__ void wave_sync() {
 // Per-wave LDS scratch of wave_route: 64 candidate slots x (key, id, weight
 // input), then the same for 64 junk slots (one per lane) that lanes without a
 // candidate write instead. Kernels that route use at most 8 waves per block.
-constexpr uint32_t ROUTE_MAX_WAVES = 8;
+constexpr uint32_t ROUTE_MAX_WAVES = 12;
 __device__ inline uint32_t* route_lds() {
     __shared__ __align__(16) uint32_t r[ROUTE_MAX_WAVES][6 * 64];
     return r[threadIdx.x >> 6];
@@ -913,8 +913,8 @@ __device__ __forceinline__ void load_xh_ilv(const float4* __restrict__ s, uint32
 // expert and weight); the blocks skip the selection.
 constexpr uint32_t GU_WAVES = 8;
 
-template <int KIND, int CPL, int RPW, int NP, int NE, int KS = -1, bool PRE = false>
-__global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
+template <int KIND, int CPL, int RPW, int NP, int NE, int KS = -1, bool PRE = false, int GW = GU_WAVES>
+__global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
                                                       uint64_t gstride, uint64_t ustride, uint32_t F, uint32_t H,
                                                       const float* __restrict__ x, const float* __restrict__ xstat,
                                                       const float* __restrict__ logits,
@@ -928,6 +928,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
                                                       const uint8_t* __restrict__ pfd = nullptr, uint64_t pfds = 0,
                                                       const uint8_t* __restrict__ pfs = nullptr, uint64_t pfss = 0) {
     using Fm = Fmt<KIND>;
+    static_assert(GW >= 8 && GW <= (int)ROUTE_MAX_WAVES && GW * NP >= 8, "8 to 12 waves, at least 8 pair slots");
     constexpr bool HX = half_x<KIND>();  // input staged as f16 pairs (split_h4)
     constexpr int KSV = KS < 0 ? KIND : KS;
     using Fs = Fmt<KSV>;
@@ -952,7 +953,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     bool xok[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-        const uint32_t u = threadIdx.x + 512u * m, ji = u >> 6, c = (u & 63u) + 64u * (ji >> 3);
+        const uint32_t u = threadIdx.x + 64u * GW * m, ji = u >> 6, c = (u & 63u) + 64u * (ji >> 3);
         xok[m] = (ji >> 3) < (uint32_t)CPL && c < nch;
         xa[m] = xok[m] ? *reinterpret_cast<const float4*>(xt + Fm::col(c, 4u * (ji & 7u)))
                        : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -960,7 +961,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     const float xm = (HX || HS) ? xstat[2u * t] : 0.f;
     // The shared expert's rows (wave 7), loaded before the routing: they do
     // not depend on it.
-    const bool shw = SH && wave == GU_WAVES - 1u;
+    const bool shw = SH && wave == GW - 1u;
     typename Fs::Raw sg[SH ? RPW : 1][SH ? CPL : 1], su[SH ? RPW : 1][SH ? CPL : 1];
     if constexpr (SH) {
         if (shw) {
@@ -984,26 +985,27 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         // routing done by k_route (batches of several tokens): ids and weights are inputs
 #pragma unroll
         for (int n = 0; n < NP; ++n) {
-            const uint32_t k = wave + GU_WAVES * n;
+            const uint32_t k = wave + GW * n;
             eid[n] = min(ids[(uint64_t)t * K + (k < K ? k : 0u)], E - 1u);
             ev[n] = 0.f;
         }
-    } else if constexpr (NP == 1) {
+    } else if constexpr (NP == 1 && NE <= 2) {
         uint32_t key[NE];
         float wv[NE];
         bool ok[NE];
         bad = route_keys<NE>(logits + (uint64_t)t * E, bias, E, sigmoid_mode, key, wv, ok);
         eid[0] = wave_kth<NE>(key, wv, ok, wave < K ? wave : 0u, ev[0]);
     } else {
-        // Several pairs per wave: the whole selection once (one threshold
-        // search for the K-th key, then the ranks among the K) instead of a
-        // search per pair; lane k holds selection k.
+        // Several pairs per wave, or several keys per lane: the whole
+        // selection once (wave_route: the candidates by the lanes' maxima,
+        // then their ranks) instead of a search per pair; lane k holds
+        // selection k.
         uint32_t my_id;
         float my_v;
         bad = wave_route<NE>(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, my_id, my_v);
 #pragma unroll
         for (int n = 0; n < NP; ++n) {
-            const uint32_t k = wave + GU_WAVES * n, kk = k < K ? k : 0u;  // no such pair: re-read pair 0's rows (not stored)
+            const uint32_t k = wave + GW * n, kk = k < K ? k : 0u;  // no such pair: re-read pair 0's rows (not stored)
             eid[n] = (uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)kk);
             ev[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), (int)kk));
         }
@@ -1041,7 +1043,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
         const uint32_t nr = min(pr0 + rs, H) - pr0;
 #pragma unroll
         for (int n = 0; n < NP; ++n) {
-            const uint32_t k = wave + GU_WAVES * n;
+            const uint32_t k = wave + GW * n;
             if (n == 0 || k < K) {
                 const uint8_t* pb = pfd + ((uint64_t)eid[n] * H + pr0) * pfds;
                 const uint64_t span = (uint64_t)nr * pfds;
@@ -1067,7 +1069,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     if constexpr (SH && KSV != KIND) tabs.store();
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GU_WAVES * n;
+        const uint32_t k = wave + GW * n;
         if (!PRE && k < K && lane == 0) {
             s_sv[k] = ev[n];
             if (blockIdx.x == 0) ids[(uint64_t)t * K + k] = eid[n];
@@ -1077,8 +1079,8 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
 #pragma unroll
     for (int m = 0; m < 2; ++m)
         if (xok[m]) {
-            s_x4[threadIdx.x + 512u * m] = HX ? split_h4(ldexp4(xa[m], xe)) : xa[m];
-            if constexpr (XS2) s_xs4[threadIdx.x + 512u * m] = HS ? split_h4(ldexp4(xa[m], xe)) : xa[m];
+            s_x4[threadIdx.x + 64u * GW * m] = HX ? split_h4(ldexp4(xa[m], xe)) : xa[m];
+            if constexpr (XS2) s_xs4[threadIdx.x + 64u * GW * m] = HS ? split_h4(ldexp4(xa[m], xe)) : xa[m];
         }
     __syncthreads();
     // Routing weights in selection order; block 0's wave 0 publishes them.
@@ -1091,7 +1093,7 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     float wk[NP];  // routing weight of each of the wave's pairs: act is stored as w_k * SwiGLU
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GU_WAVES * n;
+        const uint32_t k = wave + GW * n;
         wk[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)(k < K ? k : 0u)));
     }
     float xv[HX ? 1 : CPL][HX ? 1 : 32], xs0[CPL], xs1[CPL];
@@ -1116,8 +1118,8 @@ __global__ __launch_bounds__(512) void k_dec_gate_up2(const uint8_t* __restrict_
     };
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GU_WAVES * n;
-        if (n == 0 || k < K) {  // a pair beyond K (its loads re-read pair 0's rows) is skipped
+        const uint32_t k = wave + GW * n;
+        if (k < K) {  // a pair beyond K (its loads re-read pair 0's rows) is skipped
             float gs[RPW], us[RPW];
 #pragma unroll
             for (int i = 0; i < RPW; ++i) {
