@@ -2149,8 +2149,13 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // other. S tiles (Q4_K group sums) by superblock parity.
     __shared__ _Float16 Ah0[TT * 64], Ah1[TT * 64], Al0[TT * 64], Al1[TT * 64];
     __shared__ _Float16 Ss[2][TT * 16];  // per row: S hi of groups 0..7, S lo of groups 0..7
-    const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk;
-    const uint32_t t = ti * 8u + (blockIdx.x & 7u);
+    // Tile rounds of 8 (one tile per XCD) alternate direction: XCD x takes tile
+    // 8 ti + x in even rounds and 8 ti + 7 - x in odd ones. The tiles come
+    // sorted by decreasing size, so a fixed direction would give XCD 0 the
+    // largest tile of every round (C1 gate/up: XCD spans 62-85 us against
+    // 70-76 us snaked, by the measured per-tile block times).
+    const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk, xcd = blockIdx.x & 7u;
+    const uint32_t t = ti * 8u + ((ti & 1u) ? 7u - xcd : xcd);
     if (t >= nt) return;
     const uint32_t* tile = tiles + 4u * t;
     const uint32_t n = tile[2];
