@@ -326,8 +326,9 @@ const char* ingot_layer_stage_kernel(const ingot_layer* layer, uint32_t stage);
  * in the same GEMM launches, its rows P + t naming token t as t K, else 0),
  * inverse[P], tiles[min(tiles_cap, info[2])][4] = {expert (E: the shared
  * expert), first packed pair, n, number of non-empty tiles}; info[4] receives
- * {P, S, length of the tile list, pairs per tile (64, or 128 when T > 64 and
- * both projections are Q4_K, Q5_K or Q6_K on the f16 GEMM)}. pairs must hold P + T
+ * {P, S, length of the tile list, pairs per tile (64, or 128 when T > 64,
+ * T K >= 32 E and both projections are Q4_K, Q5_K or Q6_K on the f16 GEMM)}.
+ * pairs must hold P + T
  * entries. The
  * reference's counterparts are the layout, pairs and tile buffers of
  * kernels/prefill.metal:7-38 (src/qwen_prefill.rs:30-116); this accessor exists

@@ -1529,8 +1529,16 @@ static int layer_forward(ingot_layer* L, const Ws& w, const float* d_x, const fl
         const int aord = f16 ? a_order(down.kind) : A_F32, xord = a_order(gate.kind);
         const bool mins = f16 && (down.kind == 12 || down.kind == 13);
         // 128-token tiles when an expert can take more than 64 pairs (each takes at
-        // most one per token) and both projections have the TT 128 kernel.
-        const bool tt128 = f16 && T > TM && f16_tt128_kind(gate.kind) && f16_tt128_kind(down.kind);
+        // most one per token), the launch averages at least 32 pairs per expert
+        // and both projections have the TT 128 kernel. Below that average most
+        // tiles have one or two 16-row blocks, which run faster as 64-token
+        // tiles (each wave decoding four B blocks instead of two). Gate/up +
+        // down us, 128- against 64-token tiles, at 128 experts top-8: uniform
+        // routing 128 tokens 125.5 / 113.5, 256 137 / 124.5, 512 168 / 160;
+        // the Zipf-biased C1 router 128 tokens 79 / 70, 256 90 / 91, 512 127.5
+        // / 131. (A Q6_K projection runs its 128-token kernel on either.)
+        const bool tt128 = f16 && T > TM && (uint64_t)T * K >= 32ull * E && f16_tt128_kind(gate.kind) &&
+                           f16_tt128_kind(down.kind);
         const uint32_t tm = tt128 ? 2u * TM : TM;
         // The f16 GEMMs read the tiled copies where every matrix of the launch has one.
         const bool tlg = f16gu && gate.t && up.t && (!merge || (sgate.t && sup.t));

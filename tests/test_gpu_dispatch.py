@@ -6,8 +6,9 @@ the reference's expert_layout / expert_pairs contract (kernels/prefill.metal:
 tests/test_oracle.py). Index work must match exactly, not merely produce the
 right layer outputs: a wrong but self-consistent permutation would pass every
 end-to-end test. The GPU tile list holds the same {expert, first, n} tiles (64
-pairs each, or 128 when an expert can take more than 64 pairs and both
-projections are Q4_K or Q5_K on the f16 GEMM) in its own order: the shared
+pairs each, or 128 when an expert can take more than 64 pairs, the batch
+averages at least 32 pairs per expert and both projections are Q4_K or Q5_K
+on the f16 GEMM) in its own order: the shared
 expert's tiles first, then every full tile, then the partial tiles by
 decreasing n; its fourth word is the number of non-empty tiles.
 """
@@ -18,6 +19,11 @@ from ingot_amd import configs as CF
 from ingot_amd.moe import GEMM_FP32, IQ4_NL, Q4_K, Q8_0, MoeLayer
 
 pytestmark = pytest.mark.gpu
+
+
+def f16_tile(T, K, E):
+    """Tile size of the f16 GEMM's dispatch for Q4_K/Q5_K projections."""
+    return 128 if T > 64 and T * K >= 32 * E else 64
 
 
 def check_dispatch(layer, spec, x, oracle, label, tile=64):
@@ -69,7 +75,7 @@ def test_dispatch_c1_zipf(gpu, oracle, T, seed):
     spec = CF.c1_layer()
     layer = MoeLayer(gpu, spec)
     ids = check_dispatch(layer, spec, CF.inputs(1, T, 2048, seed=seed), oracle, f"C1 T={T}",
-                         tile=128 if T > 64 else 64)
+                         tile=f16_tile(T, spec.top_k, spec.experts))
     if T >= 512:
         counts = np.bincount(ids.ravel(), minlength=128)
         assert counts.max() == T and (counts == 0).any()
@@ -78,9 +84,10 @@ def test_dispatch_c1_zipf(gpu, oracle, T, seed):
 
 def test_dispatch_tile_tails(gpu, oracle):
     """Expert loads around the tile size (1, 15, 16, 17, 31, 32, 33, 63, 64, 65,
-    129) and empty experts, through an identity router."""
+    129, and a second 64 that brings the batch to 128-pair tiles) and empty
+    experts, through an identity router."""
     E, K, H = 16, 1, 1024
-    loads = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 129, 0, 0, 0, 0, 0]
+    loads = [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 129, 64, 0, 0, 0, 0]
     T = sum(loads)
     spec = CF.make_layer(11, E, H, E, K, 256, Q4_K, Q4_K)
     spec.router = np.zeros((E, H), np.float32)
@@ -91,6 +98,7 @@ def test_dispatch_tile_tails(gpu, oracle):
     x[:, :E] = 0.0
     x[np.arange(T), order] = 4.0
     layer = MoeLayer(gpu, spec)
+    assert f16_tile(T, K, E) == 128
     check_dispatch(layer, spec, x, oracle, "tails", tile=128)
     layer.set_gemm_mode(GEMM_FP32)
     check_dispatch(layer, spec, x, oracle, "tails, fp32 GEMM", tile=64)
