@@ -2200,6 +2200,11 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     __shared__ int2 s_rowe[TT];
     // TT 128 gate/up: each wave's 16-column halves of the act group sums
     __shared__ float gpart[GATEUP && TT == 128 ? 4 : 1][TT];
+    // gate/up: each wave's maximum of |act| over its columns of a row, reduced
+    // over the NW waves before one atomicMax per row and block (one per wave
+    // before: C1 gate/up 86.2-86.6 to 81.9-85.7 us, the Q4_K/Q6_K mix at 512
+    // tokens 111.8-114.3 to 101.6-105.1)
+    __shared__ uint32_t rpart[GATEUP ? NW : 1][TT];
     if constexpr (GATEUP) {
         if (tid < TT) {
             const uint32_t q = q0 + (tid < n ? tid : 0u);
@@ -2964,7 +2969,7 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x4e, 0xf, 0xf, false));
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x141, 0xf, 0xf, false));
                     rm = max(rm, (uint32_t)__builtin_amdgcn_mov_dpp((int)rm, 0x140, 0xf, 0xf, false));
-                    if (rowmax != nullptr && m < n && ln == 0u) atomicMax(rowmax + q, rm);
+                    if (ln == 0u) rpart[wave][m] = rm;
                     _Float16 hh[HB], ll[HB];
 #pragma unroll
                     for (int h = 0; h < (int)HB; ++h) split_f16(v[h], hh[h], ll[h]);
@@ -3005,12 +3010,20 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
                     }
                 }
             }
-        if constexpr (GATEUP && HB == 1 && AORD != A_F32) {
-            // 32-column group g of the block's 64 act columns = waves 2 g, 2 g + 1
-            if (out_gs != nullptr) {
-                __syncthreads();
-                const uint32_t g = tid / TT, m = tid % TT;
-                if (m < n) out_gs[(q0 + m) * (ldo / 32u) + row0 / 32u + g] = gpart[2u * g][m] + gpart[2u * g + 1u][m];
+        if constexpr (GATEUP && AORD != A_F32) {
+            if ((HB == 1 && out_gs != nullptr) || rowmax != nullptr) __syncthreads();
+            if constexpr (HB == 1) {
+                // 32-column group g of the block's 64 act columns = waves 2 g, 2 g + 1
+                if (out_gs != nullptr) {
+                    const uint32_t g = tid / TT, m = tid % TT;
+                    if (m < n) out_gs[(q0 + m) * (ldo / 32u) + row0 / 32u + g] = gpart[2u * g][m] + gpart[2u * g + 1u][m];
+                }
+            }
+            if (rowmax != nullptr && tid < n) {
+                uint32_t v = rpart[0][tid];
+#pragma unroll
+                for (uint32_t w = 1; w < NW; ++w) v = max(v, rpart[w][tid]);
+                atomicMax(rowmax + q0 + tid, v);
             }
         }
     };
