@@ -2152,8 +2152,10 @@ __global__ __launch_bounds__(TT * 2) __attribute__((amdgpu_waves_per_eu(2))) voi
     // Tile rounds of 8 (one tile per XCD) alternate direction: XCD x takes tile
     // 8 ti + x in even rounds and 8 ti + 7 - x in odd ones. The tiles come
     // sorted by decreasing size, so a fixed direction would give XCD 0 the
-    // largest tile of every round (C1 gate/up: XCD spans 62-85 us against
-    // 70-76 us snaked, by the measured per-tile block times).
+    // largest tile of every round (a dispatch simulation over C1's tiles with
+    // measured block times: XCD spans 62-85 us against 70-76 us snaked;
+    // measured: C1 gate/up about 1.4 us shorter, C3 gate/up 176-178 to
+    // 169-170 us, C3 down 114-116 to 111-113).
     const uint32_t nt = tiles[3], slot = blockIdx.x >> 3, ti = slot / nblk, xcd = blockIdx.x & 7u;
     const uint32_t t = ti * 8u + ((ti & 1u) ? 7u - xcd : xcd);
     if (t >= nt) return;
