@@ -285,9 +285,14 @@ __device__ __forceinline__ uint32_t route_threshold(const uint32_t (&key)[NE], u
 // Every key that precedes a candidate is itself a candidate, so these ranks
 // are the ranks among all keys. Lane k < K ends with selection k's id and
 // weight input. Returns whether this lane saw a non-finite logit or bias.
+// wave_route_compact: step 1 and the compaction of step 2 (C candidates in
+// the wave's LDS scratch, in id order: key r[m], id r[64 + m], weight input
+// r[128 + m]); wave_route_rank: the ranks and the placement. The caller may
+// issue loads between them (wave_route_compact ends with the scratch
+// visible to the whole wave).
 template <int NE>
-__device__ __forceinline__ bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
-                                  uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
+__device__ __forceinline__ bool wave_route_compact(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E,
+                                                   uint32_t K, uint32_t sigmoid_mode, uint32_t& C_out) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t key[NE];
     float wv[NE];
@@ -352,6 +357,14 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
         before += (uint32_t)__popcll(sel[j]);
     }
     wave_sync();
+    C_out = C;
+    return bad;
+}
+// rank: this lane's candidate's rank (lane < C).
+__device__ __forceinline__ void wave_route_rank(uint32_t C, uint32_t E, uint32_t K, uint32_t& my_id, float& my_v,
+                                                uint32_t& rank) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t* r = route_lds();
     const bool cand = lane < C;
     const uint32_t ck = cand ? r[lane] : 0u, cid = cand ? r[64 + lane] : 0u;
     const float cv = cand ? __uint_as_float(r[128 + lane]) : 0.f;
@@ -361,7 +374,7 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
     // (slots past C read as key 0 through a uniform mask: candidate keys are
     // >= 1, so they never precede a candidate)
     const uint64_t mine = ((uint64_t)ck << 32) | (63u - lane);
-    uint32_t rank = 0;
+    rank = 0;
     for (uint32_t m = 0; m < C; m += 16) {  // m <= 48: reads stay in r[0, 64)
         uint4 k4[4];
 #pragma unroll
@@ -385,6 +398,13 @@ __device__ __forceinline__ bool wave_route(const float* __restrict__ l, const fl
     my_id = sel_k ? min(pid, E - 1u) : 0u;  // (always below E: a guard for the weight addresses)
     my_v = sel_k ? __uint_as_float(pv) : 0.f;
     wave_sync();  // the scratch is reused by the next call
+}
+template <int NE>
+__device__ __forceinline__ bool wave_route(const float* __restrict__ l, const float* __restrict__ bias, uint32_t E, uint32_t K,
+                                  uint32_t sigmoid_mode, uint32_t& my_id, float& my_v) {
+    uint32_t C, rank;
+    const bool bad = wave_route_compact<NE>(l, bias, E, K, sigmoid_mode, C);
+    wave_route_rank(C, E, K, my_id, my_v, rank);
     return bad;
 }
 
@@ -980,7 +1000,15 @@ __global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restr
     __shared__ float s_sv[64];  // weight input of each selection
     uint32_t eid[NP];
     float ev[NP];
+    // the pair each of the wave's slots computes (K: none, not stored)
+    uint32_t kp[NP];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) kp[n] = wave + GW * n;
     bool bad = false;
+    // One pair per wave with wave_route: when every candidate has a wave (C <=
+    // GW), wave w loads candidate w's rows while the ranks are formed, and
+    // computes the pair of that candidate's rank (none if it is K or more).
+    uint32_t spec_c = 0;
     if constexpr (PRE) {
         // routing done by k_route (batches of several tokens): ids and weights are inputs
 #pragma unroll
@@ -1000,14 +1028,21 @@ __global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restr
         // selection once (wave_route: the candidates by the lanes' maxima,
         // then their ranks) instead of a search per pair; lane k holds
         // selection k.
-        uint32_t my_id;
+        uint32_t my_id, C, rank;
         float my_v;
-        bad = wave_route<NE>(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, my_id, my_v);
+        bad = wave_route_compact<NE>(logits + (uint64_t)t * E, bias, E, K, sigmoid_mode, C);
+        if (NP == 1 && C <= GW) {
+            spec_c = C;
+            eid[0] = route_lds()[64u + min(wave, C - 1u)];  // (a wave past C re-reads the last candidate's rows)
+            ev[0] = 0.f;
+        } else {
+            wave_route_rank(C, E, K, my_id, my_v, rank);
 #pragma unroll
-        for (int n = 0; n < NP; ++n) {
-            const uint32_t k = wave + GW * n, kk = k < K ? k : 0u;  // no such pair: re-read pair 0's rows (not stored)
-            eid[n] = (uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)kk);
-            ev[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), (int)kk));
+            for (int n = 0; n < NP; ++n) {
+                const uint32_t k = kp[n], kk = k < K ? k : 0u;  // no such pair: re-read pair 0's rows (not stored)
+                eid[n] = (uint32_t)__builtin_amdgcn_readlane((int)my_id, (int)kk);
+                ev[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), (int)kk));
+            }
         }
     }
     // Weight loads of the wave's pairs k = wave + 8n (n < NP; K <= 8 NP);
@@ -1043,7 +1078,7 @@ __global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restr
         const uint32_t nr = min(pr0 + rs, H) - pr0;
 #pragma unroll
         for (int n = 0; n < NP; ++n) {
-            const uint32_t k = wave + GW * n;
+            const uint32_t k = kp[n];
             if (n == 0 || k < K) {
                 const uint8_t* pb = pfd + ((uint64_t)eid[n] * H + pr0) * pfds;
                 const uint64_t span = (uint64_t)nr * pfds;
@@ -1064,12 +1099,23 @@ __global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restr
             }
         }
     }
+    if (!PRE && spec_c != 0u) {
+        // the ranks, with the candidates' loads in flight: this wave's
+        // candidate's rank is its pair, and selection k's weight input is
+        // lane k's after the placement
+        uint32_t my_id, rank;
+        float my_v;
+        wave_route_rank(spec_c, E, K, my_id, my_v, rank);
+        const uint32_t kw = (uint32_t)__builtin_amdgcn_readlane((int)rank, (int)min(wave, spec_c - 1u));
+        kp[0] = wave < spec_c && kw < K ? kw : K;
+        ev[0] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_v), (int)(kp[0] < K ? kp[0] : 0u)));
+    }
     // (read only after the barrier below)
     tab.store();
     if constexpr (SH && KSV != KIND) tabs.store();
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GW * n;
+        const uint32_t k = kp[n];
         if (!PRE && k < K && lane == 0) {
             s_sv[k] = ev[n];
             if (blockIdx.x == 0) ids[(uint64_t)t * K + k] = eid[n];
@@ -1093,7 +1139,7 @@ __global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restr
     float wk[NP];  // routing weight of each of the wave's pairs: act is stored as w_k * SwiGLU
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GW * n;
+        const uint32_t k = kp[n];
         wk[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)(k < K ? k : 0u)));
     }
     float xv[HX ? 1 : CPL][HX ? 1 : 32], xs0[CPL], xs1[CPL];
@@ -1118,7 +1164,7 @@ __global__ __launch_bounds__(64 * GW) void k_dec_gate_up2(const uint8_t* __restr
     };
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
-        const uint32_t k = wave + GW * n;
+        const uint32_t k = kp[n];
         if (k < K) {  // a pair beyond K (its loads re-read pair 0's rows) is skipped
             float gs[RPW], us[RPW];
 #pragma unroll
