@@ -446,6 +446,31 @@ def test_decode_route_many_experts_ties(gpu, oracle, E, K):
     layer.destroy()
 
 
+@pytest.mark.parametrize("E,K,kind", [(256, 8, Q8_0), (512, 10, IQ2_XS)])
+def test_decode_route_one_token_ties(gpu, oracle, E, K, kind):
+    """One-token decode above 128 experts, where every wave routes the token
+    itself (wave_route) and, when each candidate has a wave, loads its
+    candidate's rows before the ranks are formed (8-wave blocks at 256
+    experts, 12-wave blocks for IQ2_XS at 512): all logits tied, a tie at the
+    top among every 13th expert (20 or 40 candidates, more than the waves:
+    the ranks come first), ties spread over the lanes, and untied logits.
+    Ids bit-exact, lower id first."""
+    H = 1024
+    spec = identity_router_layer(E, K, H, F=256 if kind == IQ2_XS else 64, kind=kind)
+    x = CF.inputs(15, 4, H) * 0.05
+    x[0, :E] = 1.0
+    x[1, :E] = np.where(np.arange(E) % 13 == 0, 2.0, 0.0)
+    x[2, :E] = ((np.arange(E) * 17) % 23) - 11.0
+    layer = MoeLayer(gpu, spec)
+    for i in range(4):
+        _, ids, _ = check_layer(layer, spec, x[i:i + 1], oracle, f"one-token route E={E} K={K} input {i}")
+        if i == 0:
+            assert list(ids[0]) == list(range(K))
+        if i == 1:
+            assert list(ids[0]) == [13 * j for j in range(K)]
+    layer.destroy()
+
+
 def test_tiled_copies_made_for_prefill_only(gpu, oracle):
     """The prefill GEMM's tiled weight copies appear at the first batch that
     takes the prefill path (never for decode), travel with clones, and leave
