@@ -393,9 +393,13 @@ bool launch_gemm_f16(hipStream_t s, uint32_t kind, int aord, bool tt128, bool tl
 
 // Rows per wave: 3 when that spreads the blocks more evenly over the 256 CUs
 // (F = 768 at one token: 256 blocks of 3 rows instead of 384 of 2, half of
-// the CUs running two), else 2.
+// the CUs running two) and for batches of several tokens (a block's routing
+// and load round trip then cover half as many rows again: C0's layer gate/up
+// at 2 / 4 / 8 tokens 12.0 / 21.0 / 37.8 us against 12.6-12.8 / 21.8-22.0 /
+// 38.8-39.9 with 2 rows; 4 and 6 rows measured no better), else 2.
 static uint32_t dec_gate_up_rows(uint32_t F, uint32_t T, uint32_t cpl, uint32_t np) {
     if (cpl != 1 || np != 1) return 2;
+    if (T >= 2) return 3;
     auto per_cu = [&](uint32_t r) { return ((F + r - 1) / r * T + 255) / 256 * r; };
     return per_cu(3) < per_cu(2) ? 3 : 2;
 }
@@ -662,7 +666,11 @@ static uint64_t carve(const ingot_layer* L, uint32_t T, void* base, Ws* out) {
 }
 
 // Pairs up to this count take the GEMV (decode) kernels; more take the
-// dispatch + grouped MFMA GEMM (prefill) kernels.
+// dispatch + grouped MFMA GEMM (prefill) kernels. Whole-layer us over 32
+// weight copies, decode kernels against the prefill path: C0's layer at 6 / 8
+// tokens (48 / 64 pairs) 47.7 / 59.6 against 62.2 / 65.8; configs[2]'s (512
+// experts, top-10) at 2 / 4 / 6 tokens 30.3 / 47.6 / 65.0 against 112.5 /
+// 124.9 / 128.7.
 static const uint32_t GEMV_MAX_PAIRS = 64;
 
 // Whether a forward of T tokens takes the decode kernels (else routing,
