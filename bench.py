@@ -117,10 +117,11 @@ def timed_launches(gpu, step, steps, warmup, copies):
             "steps_per_launch": s, "steps": steps, "copies_per_launch": min(copies, s)}
 
 
-def time_stages(layers, reps):
-    """Mean us per launch of every stage that ran in the layers' last forward
-    (ingot_layers_time_stage: graph-captured replays round-robin over the
-    layers, HIP events on the context stream)."""
+def time_stages(layers, reps, repeat=3):
+    """us per launch of every stage that ran in the layers' last forward: the
+    median over `repeat` measurements of the mean of `reps` graph-captured
+    replays round-robin over the layers (ingot_layers_time_stage, HIP events
+    on the context stream)."""
     from ingot_amd.moe import (STAGE_COMBINE, STAGE_DISPATCH, STAGE_DOWN, STAGE_GATEUP, STAGE_ROUTE, STAGE_ROUTER,
                                time_stage)
     ids = {"router": STAGE_ROUTER, "route": STAGE_ROUTE, "dispatch": STAGE_DISPATCH, "gate_up": STAGE_GATEUP,
@@ -129,7 +130,8 @@ def time_stages(layers, reps):
     for name in STAGE_ORDER:
         kernel = layers[0].stage_kernel(ids[name])
         if kernel:
-            out[name] = {"us": 1e3 * time_stage(layers, ids[name], reps), "kernel": kernel}
+            us = sorted(1e3 * time_stage(layers, ids[name], reps) for _ in range(repeat))
+            out[name] = {"us": us[len(us) // 2], "kernel": kernel}
     layers[0].gpu.synchronize()
     return out
 
