@@ -164,7 +164,8 @@ __device__ __forceinline__ void wave_sync() {
 
 // Per-wave LDS scratch of wave_route: 64 candidate slots x (key, id, weight
 // input), then the same for 64 junk slots (one per lane) that lanes without a
-// candidate write instead. Kernels that route use at most 8 waves per block.
+// candidate write instead. Kernels that route use at most ROUTE_MAX_WAVES
+// waves per block (12: the one-token decode blocks at 512 experts).
 constexpr uint32_t ROUTE_MAX_WAVES = 12;
 __device__ inline uint32_t* route_lds() {
     __shared__ __align__(16) uint32_t r[ROUTE_MAX_WAVES][6 * 64];
