@@ -353,6 +353,21 @@ def test_decode_rows_independent_of_batch(gpu):
     layer.destroy()
 
 
+def test_decode_batches_c0_shape_odd_sizes(gpu, oracle):
+    """configs[0]'s layer (128 experts, top-8, F = 768) at 2, 5 and 7 tokens on
+    the decode kernels (three gate/up rows per wave, 256 row groups per
+    token): the oracle's bar, and every row bit-equal to its one-token forward."""
+    spec = CF.c0_layer()
+    layer = MoeLayer(gpu, spec)
+    for T in (2, 5, 7):
+        x = CF.inputs(0, T, 2048, seed=T)
+        out, ids, w = check_layer(layer, spec, x, oracle, f"C0 decode b={T}")
+        for t in range(T):
+            o1, i1, w1 = layer(x[t:t + 1])
+            assert np.array_equal(o1[0], out[t]) and np.array_equal(i1[0], ids[t]) and np.array_equal(w1[0], w[t])
+    layer.destroy()
+
+
 # ---------------------------------------------------- dispatch edge cases
 def identity_router_layer(E, K, H=1024, F=256, kind=Q4_K):
     """Router W = [I | 0]: logits[t] = x[t][:E] exactly, so x chooses the routing."""
