@@ -291,12 +291,15 @@ bool launch_router(hipStream_t s, uint32_t HB, uint32_t T, uint32_t E, bool has_
     return false;
 }
 
-// Top-K routing, keys per lane NE = E/64 rounded up to a power of two.
+// Top-K routing, keys per lane NE = E/64 rounded up to a power of two; one
+// one-wave block per token (four tokens per block measured 0.1 us slower at 4
+// and 64 tokens: the selection's ballot, count and compare chain runs on the
+// scalar unit, one per CU).
 void launch_route(hipStream_t s, const float* logits, const float* bias, uint32_t T, uint32_t E, uint32_t K,
                   uint32_t mode, float scale, uint32_t* ids, float* w, uint32_t* flags) {
-    dim3 grid((T + 3) / 4);
+    dim3 grid(T);
     const uint32_t ne = (E + 63) / 64;
-#define ROUTE(NEV) hipLaunchKernelGGL((k_route<NEV>), grid, dim3(256), 0, s, logits, bias, T, E, K, mode, scale, ids, w, flags)
+#define ROUTE(NEV) hipLaunchKernelGGL((k_route<NEV>), grid, dim3(64), 0, s, logits, bias, T, E, K, mode, scale, ids, w, flags)
     if (ne <= 1) ROUTE(1);
     else if (ne <= 2) ROUTE(2);
     else if (ne <= 4) ROUTE(4);

@@ -853,7 +853,7 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
                                                float scale, uint32_t* __restrict__ ids, float* __restrict__ wts,
                                                uint32_t* __restrict__ flags) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t t = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (t >= T) return;  // whole waves
     uint32_t my_id;
     float my_v;
